@@ -1,0 +1,310 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused AttnRes read (forward + backward) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c3]
+
+A "step" is one forward + one backward of the read over one batch of synthetic
+input already resident in HBM, launched through the library's C ABI (the
+drop-in boundary) on the current stream.  The default workload is BASELINE
+config 3 (LR read, B8 T2048 d1024 N13 r64 H4, bf16), the configuration the
+metric is quoted on.  Prints ONE JSON line.
+
+Besides the contract fields the line carries:
+  roofline      HBM roofline of the dominant kernel (the backward), from its
+                average launch duration measured with HIP events on its stream
+  cpu_baseline  the eager PyTorch restatement (oracle/) timed on the host cores
+                on a bounded token sample of the same workload
+  kernels       per-call average durations and algorithmic GB/s of fwd and bwd
+  api           ms/step through the Python autograd API (custom op + ctypes)
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "lr-attnres_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
+
+CONFIGS = {
+    "c1": dict(kind="base", B=2, T=128, D=128, N=4, R=0, H=1, scale=1.0, dtype=torch.float32, qstd=0.02,
+               fwd_only=True),
+    "c2": dict(kind="base", B=8, T=1024, D=768, N=7, R=0, H=1, scale=1.0, dtype=torch.bfloat16, qstd=0.02),
+    "c3": dict(kind="lr", B=8, T=2048, D=1024, N=13, R=64, H=4, scale=0.25, dtype=torch.bfloat16, qstd=0.02),
+    "c4": dict(kind="lr_gated", B=4, T=4096, D=2048, N=17, R=128, H=8, scale=0.25, dtype=torch.bfloat16,
+               qstd=0.02),
+}
+
+
+def bytes_per_token(c):
+    """Algorithmic HBM bytes per token (fwd, bwd): every tensor the op must
+    touch, once.  s = element size; saved softmax weights are fp32."""
+    s = torch.finfo(c["dtype"]).bits // 8
+    N, D, R, H = c["N"], c["D"], c["R"], c["H"]
+    w = N * H * 4
+    fwd = N * D * s + N * R * s + D * s + (w if not c.get("fwd_only") else 0)
+    bwd = D * s + N * D * s + N * R * s + w + N * D * s + N * R * s
+    if c["kind"] == "lr_gated":
+        fwd += R * s + H * s
+        bwd += 2 * R * s + 2 * H * s
+    if c.get("fwd_only"):
+        bwd = 0
+    return fwd, bwd
+
+
+class Workload:
+    """Inputs, outputs and C descriptors of one configuration, allocated once."""
+
+    def __init__(self, c, device, seed=0):
+        import _attnres_hip as H
+
+        self.H = H
+        self.c = c
+        g = torch.Generator(device=device).manual_seed(seed)
+        B, T, D, N, R, Hh, dt = c["B"], c["T"], c["D"], c["N"], c["R"], c["H"], c["dtype"]
+        self.n_tok = B * T
+        rn = lambda *shape, std=1.0: (torch.randn(shape, generator=g, device=device) * std).to(dt)
+        self.values = [rn(B, T, D) for _ in range(N)]
+        self.keys = [rn(B, T, R) for _ in range(N)] if R else []
+        if c["kind"] == "base":
+            self.query = rn(D, std=c["qstd"])
+        else:
+            self.query = rn(Hh, R // Hh, std=c["qstd"])
+        self.query_dyn = rn(B, T, R) if c["kind"] == "lr_gated" else None
+        self.gate = rn(B, T, Hh) if c["kind"] == "lr_gated" else None
+        self.grad_out = rn(B, T, D)
+        gate_act = H.GATE_SIGMOID if self.gate is not None else H.GATE_NONE
+        self.desc = H.Desc(self.values, self.keys, self.query, self.query_dyn, self.gate, None, Hh, c["scale"], True,
+                           False, H.MODE_SOFTMAX, gate_act, self.gate is not None)
+        self.out = torch.empty((self.n_tok, D), device=device, dtype=dt)
+        self.weights = torch.empty((self.n_tok, Hh, N), device=device, dtype=torch.float32)
+        self.dvals = [torch.empty((self.n_tok, D), device=device, dtype=dt) for _ in range(N)]
+        self.dkeys = [torch.empty((self.n_tok, R), device=device, dtype=dt) for _ in range(N)] if R else []
+        self.dq = torch.empty_like(self.query)
+        self.dqd = torch.empty((self.n_tok, R), device=device, dtype=dt) if self.query_dyn is not None else None
+        self.dg = torch.empty_like(self.gate) if self.gate is not None else None
+        lib = H.load()
+        self.lib = lib
+        ws = lib.attnres_read_backward_workspace_size(ctypes.byref(self.desc.c))
+        self.ws = torch.empty((max(1, ws),), device=device, dtype=torch.uint8)
+        gr = H.ReadGrads()
+        gr.grad_out = self.grad_out.data_ptr()
+        gr.weights = ctypes.cast(ctypes.c_void_p(self.weights.data_ptr()), ctypes.POINTER(ctypes.c_float))
+        self._dv = (ctypes.c_void_p * N)(*[t.data_ptr() for t in self.dvals])
+        gr.dvalues = self._dv
+        if R:
+            self._dk = (ctypes.c_void_p * N)(*[t.data_ptr() for t in self.dkeys])
+            gr.dkeys = self._dk
+        gr.dquery = self.dq.data_ptr()
+        gr.dquery_dyn = self.dqd.data_ptr() if self.dqd is not None else None
+        gr.dgate = self.dg.data_ptr() if self.dg is not None else None
+        gr.workspace = self.ws.data_ptr()
+        gr.workspace_bytes = ws
+        self.grads = gr
+        self.wptr = ctypes.cast(ctypes.c_void_p(self.weights.data_ptr()), ctypes.POINTER(ctypes.c_float))
+        self.outptr = ctypes.c_void_p(self.out.data_ptr())
+        self.fwd_only = bool(c.get("fwd_only"))
+
+    def fwd(self, stream):
+        rc = self.lib.attnres_read_forward(ctypes.byref(self.desc.c), self.outptr,
+                                          None if self.fwd_only else self.wptr, None, stream)
+        if rc:
+            raise RuntimeError(self.lib.attnres_last_error().decode())
+
+    def bwd(self, stream):
+        if self.fwd_only:
+            return
+        rc = self.lib.attnres_read_backward(ctypes.byref(self.desc.c), ctypes.byref(self.grads), stream)
+        if rc:
+            raise RuntimeError(self.lib.attnres_last_error().decode())
+
+
+def time_steps(wl, steps, warmup, stream, sv):
+    for _ in range(warmup):
+        wl.fwd(sv)
+        wl.bwd(sv)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        wl.fwd(sv)
+        wl.bwd(sv)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def time_kernels(wl, steps, stream, sv):
+    """Average duration of each C call, bracketed by events on its stream."""
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        wl.fwd(sv)
+        ev[i][1].record(stream)
+        ev[i][2].record(stream)
+        wl.bwd(sv)
+        ev[i][3].record(stream)
+    torch.cuda.synchronize()
+    f = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    b = sum(e[2].elapsed_time(e[3]) for e in ev) / steps
+    return f, b
+
+
+def time_api(c, wl, steps, warmup):
+    """ms/step through the public autograd API (drop-in module)."""
+    import attnres_ops as ops
+
+    vals = [v.detach().requires_grad_(True) for v in wl.values]
+    keys = [k.detach().requires_grad_(True) for k in wl.keys]
+    q = wl.query.detach().float().requires_grad_(True)
+
+    def step():
+        for t in vals + keys + [q]:
+            t.grad = None
+        if c["kind"] == "base":
+            out = ops.attention_residual_read(vals, q, True)
+        elif c["kind"] == "lr":
+            out = ops.lrid_attention_residual_read(vals, keys, q, c["H"], c["scale"], True)
+        else:
+            out = ops.lrid_attention_residual_read_gated(vals, keys, q, wl.query_dyn, wl.gate, c["H"], c["scale"],
+                                                         True, gate_activation="sigmoid")
+        if not c.get("fwd_only"):
+            out.backward(wl.grad_out)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def cpu_baseline(c, budget_s):
+    """The eager restatement (oracle/) on the host cores, bounded token sample."""
+    from oracle import attnres_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(1)
+    D, N, R, Hh, dt = c["D"], c["N"], c["R"], c["H"], c["dtype"]
+    T = 2048
+    B = 1
+    mk = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(dt).requires_grad_(True)
+    vals = [mk(B, T, D) for _ in range(N)]
+    keys = [mk(B, T, R) for _ in range(N)] if R else []
+    up = torch.randn(B, T, D, generator=g).to(dt)
+    if c["kind"] == "base":
+        q = mk(D, std=c["qstd"])
+    else:
+        q = mk(Hh, R // Hh, std=c["qstd"])
+    qd = mk(B, T, Hh, R // Hh) if c["kind"] == "lr_gated" else None
+    gt = mk(B, T, Hh) if c["kind"] == "lr_gated" else None
+
+    def step():
+        if c["kind"] == "base":
+            out = O.attention_residual_read_ref(vals, q, True)
+        elif c["kind"] == "lr":
+            out = O.lrid_attention_residual_read_ref(vals, keys, q, Hh, c["scale"], True)
+        else:
+            qq = O.gated_query_ref(q.float(), qd.float(), gt.float(), Hh, "sigmoid")
+            out = O.lrid_attention_residual_read_ref(vals, keys, qq, Hh, c["scale"], True)
+        if not c.get("fwd_only"):
+            out.backward(up)
+
+    step()  # warmup
+    t0 = time.perf_counter()
+    step()
+    one = time.perf_counter() - t0
+    iters = max(2, min(2000, int(budget_s / max(one, 1e-4))))
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        step()
+    el = time.perf_counter() - t0
+    return dict(value=B * T * iters / el, unit="tokens/s", cores=cores, kind="port",
+                sample=f"oracle eager fwd{'' if c.get('fwd_only') else '+bwd'} on B={B} T={T} tokens of the "
+                       f"workload ({dt}), {iters} iterations in {el:.1f} s, torch {torch.__version__}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-api", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the AttnRes read shards "
+              "by tokens with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    c = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = Workload(c, dev)
+    stream = torch.cuda.current_stream(dev)
+    sv = ctypes.c_void_p(stream.cuda_stream)
+
+    ms = time_steps(wl, args.steps, args.warmup, stream, sv)
+    f_ms, b_ms = time_kernels(wl, args.steps, stream, sv)
+    api_ms = None if args.no_api else time_api(c, wl, max(5, args.steps // 5), 3)
+
+    fwd_b, bwd_b = bytes_per_token(c)
+    n_tok = wl.n_tok
+    tok_s = n_tok / (ms / 1e3)
+    gbs_step = (fwd_b + bwd_b) * n_tok / (ms / 1e3) / 1e9
+    fwd_gbs = fwd_b * n_tok / (f_ms / 1e3) / 1e9
+    bwd_gbs = bwd_b * n_tok / (b_ms / 1e3) / 1e9 if bwd_b else 0.0
+    dom_gbs, dom_name, dom_bytes = (bwd_gbs, "backward", bwd_b) if bwd_b else (fwd_gbs, "forward", fwd_b)
+
+    res = {
+        "metric": "AttnRes fwd+bwd tokens/s (d=1024,N=13,r=64,bf16); HBM GB/s as % of peak",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[c["dtype"]],
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: " + ("LR" if c["kind"] != "base" else "base")
+                   + f" read fwd+bwd B{c['B']} T{c['T']} d{c['D']} N{c['N']}"
+                   + (f" r{c['R']} H{c['H']}" if c["R"] else "") + (" gated dyn query" if c["kind"] == "lr_gated"
+                                                                    else ""),
+                   "tokens": n_tok, "parallelism": "single GPU"},
+        "hbm_gbs_step": round(gbs_step, 1),
+        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
+                     "bytes_per_token": dom_bytes, "traffic": None},
+        "kernels": {"forward_ms": round(f_ms, 5), "forward_gbs": round(fwd_gbs, 1),
+                    "backward_ms": round(b_ms, 5), "backward_gbs": round(bwd_gbs, 1),
+                    "bytes_per_token": {"fwd": fwd_b, "bwd": bwd_b}},
+        "api": {"ms_per_step": round(api_ms, 4) if api_ms else None},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(c, args.cpu_seconds)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,236 @@
+"""ctypes binding of libattnres_hip.so (the C ABI in include/attnres_hip.h).
+
+This is the whole host boundary: tensors become device pointers, row strides
+and sizes; the call runs on the current HIP stream of the tensors' device.
+There is no CPU path: a missing library or a non-GPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
+
+ABI_VERSION = 1
+MAX_SOURCES = 64
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+MODE_SOFTMAX, MODE_AVERAGE = 0, 1
+GATE_NONE, GATE_LINEAR, GATE_SIGMOID = 0, 1, 2
+FLT_EPSILON = float(torch.finfo(torch.float32).eps)
+
+
+class ReadDesc(ctypes.Structure):
+    """attnres_read_desc (field order and types as in include/attnres_hip.h)."""
+
+    _fields_ = [
+        ("n_src", c_int32),
+        ("dtype", c_int32),
+        ("n_tok", c_int64),
+        ("dim", c_int32),
+        ("rank", c_int32),
+        ("heads", c_int32),
+        ("mode", c_int32),
+        ("key_norm", c_int32),
+        ("normalize_output", c_int32),
+        ("logit_scale", c_float),
+        ("norm_eps", c_float),
+        ("values", POINTER(c_void_p)),
+        ("value_row_stride", POINTER(c_int64)),
+        ("keys", POINTER(c_void_p)),
+        ("key_row_stride", POINTER(c_int64)),
+        ("query", c_void_p),
+        ("query_dyn", c_void_p),
+        ("query_dyn_row_stride", c_int64),
+        ("gate", c_void_p),
+        ("gate_per_token", c_int32),
+        ("gate_act", c_int32),
+        ("logit_bias", POINTER(c_float)),
+    ]
+
+
+class ReadGrads(ctypes.Structure):
+    """attnres_read_grads."""
+
+    _fields_ = [
+        ("grad_out", c_void_p),
+        ("out", c_void_p),
+        ("out_inv_rms", POINTER(c_float)),
+        ("weights", POINTER(c_float)),
+        ("dvalues", POINTER(c_void_p)),
+        ("dkeys", POINTER(c_void_p)),
+        ("dquery", c_void_p),
+        ("dquery_dyn", c_void_p),
+        ("dgate", c_void_p),
+        ("dbias", POINTER(c_float)),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise with a build hint if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"attnres HIP library not found at {LIB_PATH}; build it with "
+            "`python lr-attnres_amd/build.py` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.attnres_abi_version.restype = c_int
+    lib.attnres_last_error.restype = ctypes.c_char_p
+    lib.attnres_read_forward.restype = c_int
+    lib.attnres_read_forward.argtypes = [POINTER(ReadDesc), c_void_p, POINTER(c_float), POINTER(c_float), c_void_p]
+    lib.attnres_read_backward.restype = c_int
+    lib.attnres_read_backward.argtypes = [POINTER(ReadDesc), POINTER(ReadGrads), c_void_p]
+    lib.attnres_read_backward_workspace_size.restype = c_size_t
+    lib.attnres_read_backward_workspace_size.argtypes = [POINTER(ReadDesc)]
+    v = lib.attnres_abi_version()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"libattnres_hip ABI {v} != expected {ABI_VERSION}; rebuild the library")
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    try:
+        load()
+    except (OSError, RuntimeError):
+        return False
+    return torch.cuda.is_available()
+
+
+def _ptr(t):
+    return c_void_p(t.data_ptr()) if t is not None else c_void_p(0)
+
+
+def _fptr(t):
+    return ctypes.cast(c_void_p(t.data_ptr()), POINTER(c_float)) if t is not None else None
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        msg = load().attnres_last_error().decode(errors="replace")
+        raise RuntimeError(f"attnres HIP {what} failed (code {rc}): {msg}")
+
+
+def _stream(device) -> c_void_p:
+    return c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _row_view_ok(t: torch.Tensor) -> bool:
+    # [B,T,W] with a contiguous last dim and one uniform token stride
+    return t.dim() == 3 and t.stride(-1) == 1 and t.stride(0) == t.size(1) * t.stride(1)
+
+
+def as_rows(t: torch.Tensor) -> torch.Tensor:
+    """A [B,T,W] tensor whose tokens are uniformly strided rows (copy if not)."""
+    return t if _row_view_ok(t) else t.contiguous()
+
+
+class Desc:
+    """Builds the C descriptor for one read; keeps the ctypes arrays alive."""
+
+    def __init__(self, values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm,
+                 normalize_output, mode, gate_act, gate_per_token, eps=FLT_EPSILON):
+        v0 = values[0]
+        B, T, D = v0.shape
+        n = len(values)
+        self.n_src = n
+        self.n_tok = B * T
+        self.D = D
+        self.R = keys[0].size(-1) if keys else 0
+        self.heads = heads
+        self._vals = (c_void_p * n)(*[t.data_ptr() for t in values])
+        self._vstr = (c_int64 * n)(*[t.stride(1) for t in values])
+        if keys:
+            self._keys = (c_void_p * n)(*[t.data_ptr() for t in keys])
+            self._kstr = (c_int64 * n)(*[t.stride(1) for t in keys])
+        d = ReadDesc()
+        d.n_src = n
+        d.dtype = DTYPE_CODE[v0.dtype]
+        d.n_tok = self.n_tok
+        d.dim = D
+        d.rank = self.R
+        d.heads = heads
+        d.mode = mode
+        d.key_norm = int(bool(key_norm))
+        d.normalize_output = int(bool(normalize_output))
+        d.logit_scale = float(logit_scale)
+        d.norm_eps = float(eps)
+        d.values = self._vals
+        d.value_row_stride = self._vstr
+        if keys:
+            d.keys = self._keys
+            d.key_row_stride = self._kstr
+        d.query = query.data_ptr() if query is not None else None
+        d.query_dyn = query_dyn.data_ptr() if query_dyn is not None else None
+        d.query_dyn_row_stride = query_dyn.stride(1) if query_dyn is not None else 0
+        d.gate = gate.data_ptr() if gate is not None else None
+        d.gate_per_token = int(bool(gate_per_token))
+        d.gate_act = gate_act
+        d.logit_bias = _fptr(bias)
+        self.c = d
+
+
+def forward(desc: Desc, device, dtype, need_weights: bool, normalize_output: bool):
+    """Launch the forward; returns (out [n_tok, D], weights [n_tok,H,N] | empty, inv_rms [n_tok] | empty)."""
+    lib = load()
+    out = torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype)
+    if need_weights:
+        w = torch.empty((desc.n_tok, desc.heads, desc.n_src), device=device, dtype=torch.float32)
+    else:
+        w = torch.empty((0,), device=device, dtype=torch.float32)
+    inv = torch.empty((desc.n_tok if normalize_output else 0,), device=device, dtype=torch.float32)
+    rc = lib.attnres_read_forward(ctypes.byref(desc.c), _ptr(out), _fptr(w) if need_weights else None,
+                                  _fptr(inv) if normalize_output else None, _stream(device))
+    _check(rc, "forward")
+    return out, w, inv
+
+
+def backward(desc: Desc, device, dtype, grad_out, out, inv_rms, weights, want_dquery: bool,
+             want_dgate: bool, want_dbias: bool, query_shape, gate_shape, lr: bool, has_query_dyn: bool):
+    """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias)."""
+    lib = load()
+    n = desc.n_src
+    dvals = [torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype) for _ in range(n)]
+    dkeys = [torch.empty((desc.n_tok, desc.R), device=device, dtype=dtype) for _ in range(n)] if lr else []
+    dq = torch.empty(query_shape, device=device, dtype=dtype) if want_dquery else None
+    dqd = torch.empty((desc.n_tok, desc.R), device=device, dtype=dtype) if has_query_dyn else None
+    dg = torch.empty(gate_shape, device=device, dtype=dtype) if want_dgate else None
+    db = torch.empty((n,), device=device, dtype=torch.float32) if want_dbias else None
+    g = ReadGrads()
+    g.grad_out = grad_out.data_ptr()
+    g.out = out.data_ptr() if out is not None and out.numel() else None
+    g.out_inv_rms = _fptr(inv_rms) if inv_rms is not None and inv_rms.numel() else None
+    g.weights = _fptr(weights) if weights is not None and weights.numel() else None
+    dv_arr = (c_void_p * n)(*[t.data_ptr() for t in dvals])
+    g.dvalues = dv_arr
+    if lr:
+        dk_arr = (c_void_p * n)(*[t.data_ptr() for t in dkeys])
+        g.dkeys = dk_arr
+    g.dquery = dq.data_ptr() if dq is not None else None
+    g.dquery_dyn = dqd.data_ptr() if dqd is not None else None
+    g.dgate = dg.data_ptr() if dg is not None else None
+    g.dbias = _fptr(db)
+    # workspace for the cross-token partial sums of the requested gradients
+    ws_bytes = lib.attnres_read_backward_workspace_size(ctypes.byref(desc.c))
+    ws = torch.empty((max(int(ws_bytes), 1),), device=device, dtype=torch.uint8)
+    g.workspace = ws.data_ptr()
+    g.workspace_bytes = int(ws_bytes)
+    rc = lib.attnres_read_backward(ctypes.byref(desc.c), ctypes.byref(g), _stream(device))
+    _check(rc, "backward")
+    return dvals, dkeys, dq, dqd, dg, db

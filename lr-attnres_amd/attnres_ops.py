@@ -1,0 +1,428 @@
+"""Drop-in replacement of the reference's ``attnres_ops`` module, backed by HIP kernels for MI355X.
+
+Keeps the reference's public names, argument meaning and error behaviour
+(``/root/reference/attnres_ops.py:26-40``), so a model written against it --
+``from attnres_ops import lrid_attention_residual_read`` -- runs unchanged when
+``lr-attnres_amd`` is on ``sys.path`` instead of the reference.
+
+Every read runs the hand-written gfx950 kernels in ``libattnres_hip.so``
+through its C ABI (``include/attnres_hip.h``); there is no Triton, no eager
+fallback and no dispatch switch.  Tensors that are not on a ROCm GPU, or a
+missing library, raise ``RuntimeError``.  ``force_triton`` is accepted for
+signature compatibility and has no effect (the HIP path is the only path).
+
+Autograd goes through ``torch.library.custom_op`` (``attnres_hip::read`` /
+``attnres_hip::read_backward``), with fake implementations for
+``torch.compile``.  The forward saves the fp32 softmax weights
+``[B*T, H, N]``; the backward recomputes nothing from the keys except the key
+norm, and reduces cross-token gradients (static query, per-site gate, bias)
+deterministically.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+from torch.nn import functional as F
+
+import _attnres_hip as _hip
+
+__all__ = [
+    "attention_residual_average_read",
+    "attention_residual_phase1",
+    "attention_residual_phase1_from_logits",
+    "attention_residual_phase2",
+    "attention_residual_phase2_from_logit",
+    "attention_residual_phase2_torch",
+    "attention_residual_read",
+    "attention_residual_read_torch",
+    "is_fused_attnres_available",
+    "lrid_attention_residual_phase2",
+    "lrid_attention_residual_phase2_torch",
+    "lrid_attention_residual_read",
+    "lrid_attention_residual_read_gated",
+    "lrid_attention_residual_read_torch",
+]
+
+_ALLOWED = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def is_fused_attnres_available() -> bool:
+    """True when the HIP library loads and a ROCm GPU is visible (reference: attnres_ops.py:123-124)."""
+    return _hip.available()
+
+
+# ---------------------------------------------------------------- argument handling
+
+def _source_logit_bias(source_counts, source_logit_biases, n_sources: int, device) -> Optional[Tensor]:
+    """fp32 [N] logit bias with the reference's rules and errors (attnres_ops.py:65-105)."""
+    if source_counts is not None and source_logit_biases is not None:
+        raise RuntimeError("source_counts and source_logit_biases are mutually exclusive")
+    if source_logit_biases is None:
+        if source_counts is None:
+            return None
+        if isinstance(source_counts, Tensor):
+            counts = source_counts.reshape(-1).to(device=device, dtype=torch.float32)
+        elif isinstance(source_counts, (int, float)):
+            counts = torch.full((n_sources,), float(source_counts), device=device, dtype=torch.float32)
+        else:
+            if len(source_counts) != n_sources:
+                raise RuntimeError("source_counts length must match the number of sources")
+            vals = [float(c) for c in source_counts]
+            if any(c <= 0.0 for c in vals):
+                raise RuntimeError("source_counts must be positive")
+            counts = torch.tensor(vals, device=device, dtype=torch.float32)
+        if counts.numel() != n_sources:
+            raise RuntimeError("source_counts length must match the number of sources")
+        return counts.log()
+    if isinstance(source_logit_biases, Tensor):
+        biases = source_logit_biases.reshape(-1).to(device=device, dtype=torch.float32)
+    elif isinstance(source_logit_biases, (int, float)):
+        biases = torch.full((n_sources,), float(source_logit_biases), device=device, dtype=torch.float32)
+    else:
+        if len(source_logit_biases) != n_sources:
+            raise RuntimeError("source_logit_biases length must match the number of sources")
+        items = [b.to(device=device, dtype=torch.float32).reshape(()) if isinstance(b, Tensor)
+                 else torch.tensor(float(b), device=device, dtype=torch.float32) for b in source_logit_biases]
+        biases = torch.stack(items)
+    if biases.numel() != n_sources:
+        raise RuntimeError("source_logit_biases length must match the number of sources")
+    return biases.contiguous()
+
+
+def _sources(values) -> list:
+    if isinstance(values, Tensor):
+        if values.dim() != 4:
+            raise RuntimeError("stacked sources must be [S, B, T, D]")
+        return list(values.unbind(0))
+    return list(values)
+
+
+def _check_gpu(tensors, what):
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(f"{what}: the AttnRes HIP kernels need tensors on a ROCm GPU (got {dev}); "
+                           "this build has no CPU path")
+    for t in tensors:
+        if t.device != dev:
+            raise RuntimeError(f"{what}: all tensors must be on {dev} (got {t.device})")
+    return dev
+
+
+def _check_sources(srcs, what):
+    if len(srcs) == 0:
+        raise RuntimeError(f"{what} requires at least one source")
+    if len(srcs) > _hip.MAX_SOURCES:
+        raise RuntimeError(f"{what} supports at most {_hip.MAX_SOURCES} sources, got {len(srcs)}")
+    first = srcs[0]
+    if first.dim() != 3:
+        raise RuntimeError(f"{what}: sources must be [B, T, D]")
+    for t in srcs:
+        if t.shape != first.shape:
+            raise RuntimeError(f"{what}: every source must have shape {tuple(first.shape)}, got {tuple(t.shape)}")
+        if t.dtype != first.dtype:
+            raise RuntimeError(f"{what}: every source must have dtype {first.dtype}, got {t.dtype}")
+    if first.dtype not in _ALLOWED:
+        raise RuntimeError(f"{what}: dtype {first.dtype} is not supported (fp32, bf16, fp16)")
+
+
+def _norm(x: Tensor) -> Tensor:
+    # identity-path output norm for a single source; same op as the reference
+    return F.rms_norm(x, (x.size(-1),))
+
+
+# ---------------------------------------------------------------- the custom ops
+
+def _empty(device):
+    return torch.empty((0,), device=device)
+
+
+@torch.library.custom_op("attnres_hip::read", mutates_args=())
+def _read_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], query_dyn: Optional[Tensor],
+             gate: Optional[Tensor], bias: Optional[Tensor], heads: int, logit_scale: float, key_norm: bool,
+             normalize_output: bool, mode: int, gate_act: int, gate_per_token: bool,
+             save_weights: bool) -> tuple[Tensor, Tensor, Tensor]:
+    v0 = values[0]
+    B, T, D = v0.shape
+    desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
+                     mode, gate_act, gate_per_token)
+    with torch.cuda.device(v0.device):
+        out, w, inv = _hip.forward(desc, v0.device, v0.dtype, save_weights and mode == _hip.MODE_SOFTMAX,
+                                   normalize_output)
+    return out.view(B, T, D), w, inv
+
+
+@_read_op.register_fake
+def _read_fake(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode,
+               gate_act, gate_per_token, save_weights):
+    v0 = values[0]
+    B, T, D = v0.shape
+    n_tok = B * T
+    out = v0.new_empty((B, T, D))
+    w = v0.new_empty((n_tok, heads, len(values)) if save_weights and mode == 0 else (0,), dtype=torch.float32)
+    inv = v0.new_empty((n_tok if normalize_output else 0,), dtype=torch.float32)
+    return out, w, inv
+
+
+@torch.library.custom_op("attnres_hip::read_backward", mutates_args=())
+def _read_backward_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], query_dyn: Optional[Tensor],
+                      gate: Optional[Tensor], bias: Optional[Tensor], grad_out: Tensor, out: Tensor,
+                      inv_rms: Tensor, weights: Tensor, heads: int, logit_scale: float, key_norm: bool,
+                      normalize_output: bool, mode: int, gate_act: int,
+                      gate_per_token: bool) -> tuple[list[Tensor], list[Tensor], Tensor, Tensor, Tensor, Tensor]:
+    v0 = values[0]
+    B, T, D = v0.shape
+    dev = v0.device
+    desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
+                     mode, gate_act, gate_per_token)
+    lr = len(keys) > 0
+    with torch.cuda.device(dev):
+        dvals, dkeys, dq, dqd, dg, db = _hip.backward(
+            desc, dev, v0.dtype, grad_out.contiguous(), out, inv_rms, weights,
+            want_dquery=query is not None and mode == _hip.MODE_SOFTMAX,
+            want_dgate=gate is not None, want_dbias=bias is not None,
+            query_shape=tuple(query.shape) if query is not None else (0,),
+            gate_shape=tuple(gate.shape) if gate is not None else (0,), lr=lr,
+            has_query_dyn=query_dyn is not None)
+    dvals = [t.view(B, T, D) for t in dvals]
+    dkeys = [t.view(B, T, keys[0].size(-1)) for t in dkeys]
+    # absent gradients are distinct empty tensors (custom-op outputs may not alias)
+    return (dvals, dkeys, dq if dq is not None else _empty(dev),
+            dqd.view(query_dyn.shape) if dqd is not None else _empty(dev),
+            dg if dg is not None else _empty(dev), db if db is not None else _empty(dev))
+
+
+@_read_backward_op.register_fake
+def _read_backward_fake(values, keys, query, query_dyn, gate, bias, grad_out, out, inv_rms, weights, heads,
+                        logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token):
+    e = lambda: values[0].new_empty((0,))  # noqa: E731
+    return ([v.new_empty(v.shape) for v in values], [k.new_empty(k.shape) for k in keys],
+            query.new_empty(query.shape) if query is not None else e(),
+            query_dyn.new_empty(query_dyn.shape) if query_dyn is not None else e(),
+            gate.new_empty(gate.shape) if gate is not None else e(),
+            bias.new_empty(bias.shape) if bias is not None else e())
+
+
+def _read_setup_context(ctx, inputs, output):
+    (values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode, gate_act,
+     gate_per_token, save_weights) = inputs
+    out, w, inv = output
+    ctx.n_values = len(values)
+    ctx.n_keys = len(keys)
+    ctx.has = (query is not None, query_dyn is not None, gate is not None, bias is not None)
+    opt = [t for t in (query, query_dyn, gate, bias) if t is not None]
+    ctx.save_for_backward(*values, *keys, *opt, out, w, inv)
+    ctx.flags = (heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token)
+
+
+def _read_backward(ctx, grad_out, grad_w, grad_inv):
+    saved = list(ctx.saved_tensors)
+    values = saved[:ctx.n_values]
+    keys = saved[ctx.n_values:ctx.n_values + ctx.n_keys]
+    rest = saved[ctx.n_values + ctx.n_keys:]
+    opt = []
+    for present in ctx.has:
+        opt.append(rest.pop(0) if present else None)
+    query, query_dyn, gate, bias = opt
+    out, w, inv = rest
+    heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token = ctx.flags
+    dvals, dkeys, dq, dqd, dg, db = _read_backward_op(values, keys, query, query_dyn, gate, bias, grad_out, out,
+                                                      inv, w, heads, logit_scale, key_norm, normalize_output, mode,
+                                                      gate_act, gate_per_token)
+    return (dvals, dkeys,
+            dq if query is not None else None, dqd if query_dyn is not None else None,
+            dg if gate is not None else None, db if bias is not None else None,
+            None, None, None, None, None, None, None, None)
+
+
+_read_op.register_autograd(_read_backward, setup_context=_read_setup_context)
+
+
+def _run(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode,
+         gate_act=_hip.GATE_NONE, gate_per_token=False):
+    save = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in [*values, *keys, query, query_dyn, gate, bias])
+    out, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, int(heads), float(logit_scale), bool(key_norm),
+                         bool(normalize_output), int(mode), int(gate_act), bool(gate_per_token), bool(save))
+    return out
+
+
+# ---------------------------------------------------------------- public API: base read
+
+def attention_residual_read(values, query: Tensor, key_norm: bool, force_triton: bool = False,
+                            normalize_output: bool = False, source_counts=None, source_logit_biases=None) -> Tensor:
+    """Base AttnRes read (reference: attnres_ops.py:2503-2565).
+
+    values: list of N [B,T,D] tensors or a stacked [N,B,T,D] tensor; query [D].
+    Keys are ``rms_norm(values)`` when ``key_norm``.  A single source is
+    returned as is (rms-normed when ``normalize_output``).
+    """
+    srcs = _sources(values)
+    _check_sources(srcs, "attention_residual_read")
+    if len(srcs) == 1:
+        return _norm(srcs[0]) if normalize_output else srcs[0]
+    dev = _check_gpu(srcs + [query], "attention_residual_read")
+    dtype = srcs[0].dtype
+    D = srcs[0].size(-1)
+    query = query.to(dtype)
+    if query.numel() != D:
+        raise RuntimeError(f"attention_residual_read: query must have {D} elements, got {query.numel()}")
+    bias = _source_logit_bias(source_counts, source_logit_biases, len(srcs), dev)
+    srcs = [_hip.as_rows(t) for t in srcs]
+    return _run(srcs, [], query.reshape(D).contiguous(), None, None, bias, 1, 1.0, key_norm, normalize_output,
+                _hip.MODE_SOFTMAX)
+
+
+def attention_residual_read_torch(values, query: Tensor, key_norm: bool, source_counts=None,
+                                  source_logit_biases=None) -> Tensor:
+    """Name kept for import compatibility (reference: attnres_ops.py:2217-2225).
+
+    In this build it runs the same HIP kernel as ``attention_residual_read``;
+    the eager restatement used to check the kernels lives in ``oracle/``.
+    """
+    return attention_residual_read(values, query, key_norm, source_counts=source_counts,
+                                   source_logit_biases=source_logit_biases)
+
+
+def attention_residual_average_read(values, normalize_output: bool = False, force_triton: bool = False) -> Tensor:
+    """Uniform mean over the sources (reference: attnres_ops.py:2568-2617), with a backward."""
+    srcs = _sources(values)
+    _check_sources(srcs, "attention_residual_average_read")
+    if len(srcs) == 1:
+        return _norm(srcs[0]) if normalize_output else srcs[0]
+    _check_gpu(srcs, "attention_residual_average_read")
+    srcs = [_hip.as_rows(t) for t in srcs]
+    return _run(srcs, [], None, None, None, None, 1, 1.0, False, normalize_output, _hip.MODE_AVERAGE)
+
+
+# ---------------------------------------------------------------- public API: LR read
+
+def _lr_common(values, keys, num_heads, what):
+    vs = _sources(values)
+    ks = _sources(keys)
+    if len(vs) != len(ks):
+        raise RuntimeError(f"{what}: got {len(vs)} value sources and {len(ks)} key sources")
+    _check_sources(vs, what)
+    _check_sources(ks, what)
+    H = int(num_heads)
+    B, T, D = vs[0].shape
+    R = ks[0].size(-1)
+    if ks[0].shape[:2] != (B, T):
+        raise RuntimeError(f"{what}: keys must be [B, T, R] with the values' B, T")
+    if H < 1 or D % H or R % H:
+        raise RuntimeError(f"{what}: num_heads={H} must divide n_embd={D} and rank={R}")
+    return vs, ks, H, D, R
+
+
+def lrid_attention_residual_read(values, keys, query: Tensor, num_heads: int, logit_scale: float, key_norm: bool,
+                                 force_triton: bool = False, normalize_output: bool = False, source_counts=None,
+                                 source_logit_biases=None) -> Tensor:
+    """LR AttnRes read (reference: attnres_ops.py:4852-5003).
+
+    values: N x [B,T,D] (list or stacked); keys: N x [B,T,R]; query [H, R/H]
+    (static, per read site) or [B,T,H,R/H] (input dependent).  The query is
+    cast to the key dtype first, as in the reference.  The optional output
+    rms-norm is fused for any number of heads.
+    """
+    vs, ks, H, D, R = _lr_common(values, keys, num_heads, "lrid_attention_residual_read")
+    query = query.to(ks[0].dtype)
+    if len(vs) == 1:
+        return _norm(vs[0]) if normalize_output else vs[0]
+    dev = _check_gpu(vs + ks + [query], "lrid_attention_residual_read")
+    dtype = vs[0].dtype
+    if ks[0].dtype != dtype:
+        ks = [k.to(dtype) for k in ks]
+        query = query.to(dtype)
+    B, T, _ = vs[0].shape
+    bias = _source_logit_bias(source_counts, source_logit_biases, len(vs), dev)
+    vs = [_hip.as_rows(t) for t in vs]
+    ks = [_hip.as_rows(t) for t in ks]
+    if query.dim() == 4:
+        if tuple(query.shape) != (B, T, H, R // H):
+            raise RuntimeError(f"lrid_attention_residual_read: per-token query must be {(B, T, H, R // H)}, "
+                               f"got {tuple(query.shape)}")
+        qd = _hip.as_rows(query.reshape(B, T, R))
+        return _run(vs, ks, None, qd, None, bias, H, logit_scale, key_norm, normalize_output, _hip.MODE_SOFTMAX)
+    if query.numel() != R:
+        raise RuntimeError(f"lrid_attention_residual_read: static query must have {R} elements "
+                           f"([{H}, {R // H}]), got {tuple(query.shape)}")
+    return _run(vs, ks, query.reshape(H, R // H).contiguous(), None, None, bias, H, logit_scale, key_norm,
+                normalize_output, _hip.MODE_SOFTMAX)
+
+
+def lrid_attention_residual_read_gated(values, keys, static_query: Optional[Tensor], dynamic_query: Tensor,
+                                       gate: Optional[Tensor], num_heads: int, logit_scale: float, key_norm: bool,
+                                       gate_activation: str = "sigmoid", normalize_output: bool = False,
+                                       source_counts=None, source_logit_biases=None) -> Tensor:
+    """LR read with the query composed inside the kernel: ``q = q_static + act(gate) * q_dyn``.
+
+    ``gate_activation="linear"`` with a per-site ``gate[H]`` is the model's
+    input-dependent query (model.py:2102-2113); ``"sigmoid"`` with a per-token
+    ``gate[B,T,H]`` is benchmark config 4.  ``dynamic_query`` is [B,T,R] or
+    [B,T,H,R/H]; ``static_query`` is [H,R/H] or None.  Gradients flow to all
+    three (the per-site gate and static query are reduced over tokens
+    deterministically).  Not present in the reference, which composes the query
+    eagerly and then reads with an input-dependent query.
+    """
+    vs, ks, H, D, R = _lr_common(values, keys, num_heads, "lrid_attention_residual_read_gated")
+    dtype = vs[0].dtype
+    B, T, _ = vs[0].shape
+    dev = _check_gpu(vs + ks + [dynamic_query], "lrid_attention_residual_read_gated")
+    ks = [k.to(dtype) for k in ks]
+    if dynamic_query.numel() != B * T * R:
+        raise RuntimeError(f"dynamic_query must hold [B, T, {R}] elements")
+    qd = _hip.as_rows(dynamic_query.to(dtype).reshape(B, T, R))
+    qs = None
+    if static_query is not None:
+        if static_query.numel() != R:
+            raise RuntimeError(f"static_query must have {R} elements")
+        qs = static_query.to(dtype).reshape(H, R // H).contiguous()
+    act = {"linear": _hip.GATE_LINEAR, "sigmoid": _hip.GATE_SIGMOID}.get(gate_activation)
+    if act is None:
+        raise RuntimeError(f"unknown gate_activation {gate_activation!r}")
+    g = None
+    per_token = False
+    if gate is not None:
+        g = gate.to(dtype)
+        if g.numel() == H:
+            g = g.reshape(H).contiguous()
+        elif g.numel() == B * T * H:
+            g = g.reshape(B, T, H).contiguous()
+            per_token = True
+        else:
+            raise RuntimeError(f"gate must be [{H}] (per site) or [B, T, {H}] (per token)")
+    if len(vs) == 1:
+        return _norm(vs[0]) if normalize_output else vs[0]
+    bias = _source_logit_bias(source_counts, source_logit_biases, len(vs), dev)
+    vs = [_hip.as_rows(t) for t in vs]
+    ks = [_hip.as_rows(t) for t in ks]
+    return _run(vs, ks, qs, qd, g, bias, H, logit_scale, key_norm, normalize_output, _hip.MODE_SOFTMAX,
+                act if g is not None else _hip.GATE_NONE, per_token)
+
+
+def lrid_attention_residual_read_torch(values, keys, query: Tensor, num_heads: int, logit_scale: float,
+                                       key_norm: bool, source_counts=None, source_logit_biases=None) -> Tensor:
+    """Name kept for import compatibility (reference: attnres_ops.py:4235-4256); runs the HIP kernel."""
+    return lrid_attention_residual_read(values, keys, query, num_heads, logit_scale, key_norm,
+                                        source_counts=source_counts, source_logit_biases=source_logit_biases)
+
+
+# ---------------------------------------------------------------- cached-logit phases (not yet built)
+
+def _not_built(name):
+    def f(*args, **kwargs):
+        raise NotImplementedError(f"{name} (cached-logit block schedule) is not implemented in the HIP build yet")
+    f.__name__ = name
+    return f
+
+
+attention_residual_phase1 = _not_built("attention_residual_phase1")
+attention_residual_phase1_from_logits = _not_built("attention_residual_phase1_from_logits")
+attention_residual_phase2 = _not_built("attention_residual_phase2")
+attention_residual_phase2_from_logit = _not_built("attention_residual_phase2_from_logit")
+attention_residual_phase2_torch = _not_built("attention_residual_phase2_torch")
+lrid_attention_residual_phase2 = _not_built("lrid_attention_residual_phase2")
+lrid_attention_residual_phase2_torch = _not_built("lrid_attention_residual_phase2_torch")

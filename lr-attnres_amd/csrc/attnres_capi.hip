@@ -1,0 +1,368 @@
+// C ABI of the AttnRes read library: argument checking, kernel selection and
+// launch geometry.  Declared in include/attnres_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "attnres_launch.h"
+#include "attnres_params.h"
+
+using namespace attnres;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int elem_size(int dtype) { return dtype == ATTNRES_DTYPE_F32 ? 4 : 2; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Largest dynamic LDS a workgroup may use on this device.
+size_t lds_limit() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 65536;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+    return 65536;
+  return (size_t)v;
+}
+
+struct Plan {
+  bool lr;
+  int vec;        // 16-byte path
+  int E;          // elements per vector
+  int cb;         // columns per lane
+  int ncols;
+  int wpt;
+  int nmax;
+  int key_vec;
+};
+
+int check_desc(const attnres_read_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->n_src < 1 || d->n_src > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_src=%d outside [1, %d]", d->n_src, ATTNRES_MAX_SOURCES);
+  if (d->dtype != ATTNRES_DTYPE_F32 && d->dtype != ATTNRES_DTYPE_BF16 && d->dtype != ATTNRES_DTYPE_F16)
+    return fail(ATTNRES_EINVAL, "unknown dtype %d", d->dtype);
+  if (d->n_tok < 0) return fail(ATTNRES_EINVAL, "n_tok=%lld < 0", (long long)d->n_tok);
+  if (d->dim < 1) return fail(ATTNRES_EINVAL, "dim=%d < 1", d->dim);
+  if (d->mode != ATTNRES_MODE_SOFTMAX && d->mode != ATTNRES_MODE_AVERAGE)
+    return fail(ATTNRES_EINVAL, "unknown mode %d", d->mode);
+  if (!d->values || !d->value_row_stride) return fail(ATTNRES_EINVAL, "values / value_row_stride is NULL");
+  const bool live = d->n_tok > 0;  // empty inputs may carry NULL data pointers
+  for (int s = 0; s < d->n_src; ++s) {
+    if (live && !d->values[s]) return fail(ATTNRES_EINVAL, "values[%d] is NULL", s);
+    if (d->value_row_stride[s] < d->dim || d->value_row_stride[s] > INT32_MAX)
+      return fail(ATTNRES_EINVAL, "value_row_stride[%d]=%lld must be in [dim, 2^31)", s,
+                  (long long)d->value_row_stride[s]);
+  }
+  if (d->mode == ATTNRES_MODE_AVERAGE) return ATTNRES_OK;
+  if (d->heads < 1) return fail(ATTNRES_EINVAL, "heads=%d < 1", d->heads);
+  if (d->rank == 0) {
+    if (d->heads != 1) return fail(ATTNRES_EINVAL, "base read (rank 0) needs heads == 1, got %d", d->heads);
+    if (!d->query) return fail(ATTNRES_EINVAL, "base read needs a [dim] query");
+    if (d->query_dyn || d->gate) return fail(ATTNRES_EUNSUPPORTED, "base read has no per-token query or gate");
+  } else {
+    if (d->rank < 0) return fail(ATTNRES_EINVAL, "rank=%d < 0", d->rank);
+    if (d->dim % d->heads || d->rank % d->heads)
+      return fail(ATTNRES_EINVAL, "heads=%d must divide dim=%d and rank=%d", d->heads, d->dim, d->rank);
+    if (!d->keys || !d->key_row_stride) return fail(ATTNRES_EINVAL, "LR read needs keys and key_row_stride");
+    for (int s = 0; s < d->n_src; ++s) {
+      if (live && !d->keys[s]) return fail(ATTNRES_EINVAL, "keys[%d] is NULL", s);
+      if (d->key_row_stride[s] < d->rank || d->key_row_stride[s] > INT32_MAX)
+        return fail(ATTNRES_EINVAL, "key_row_stride[%d]=%lld must be in [rank, 2^31)", s,
+                    (long long)d->key_row_stride[s]);
+    }
+    if (!d->query && !d->query_dyn && live)
+      return fail(ATTNRES_EINVAL, "LR read needs a static and/or per-token query");
+    if (d->query_dyn && d->query_dyn_row_stride < d->rank)
+      return fail(ATTNRES_EINVAL, "query_dyn_row_stride=%lld < rank", (long long)d->query_dyn_row_stride);
+    if (d->gate && !d->query_dyn && live) return fail(ATTNRES_EINVAL, "a gate needs a per-token query");
+    if (d->gate && d->gate_act != ATTNRES_GATE_LINEAR && d->gate_act != ATTNRES_GATE_SIGMOID)
+      return fail(ATTNRES_EINVAL, "unknown gate activation %d", d->gate_act);
+  }
+  return ATTNRES_OK;
+}
+
+// Geometry shared by forward and backward.  `extra` are the other [n_tok, dim]
+// buffers that must be 16-byte aligned for the vector path.
+int make_plan(const attnres_read_desc* d, const void* const* extra, int n_extra, void* const* extra_src, Plan* pl) {
+  const int es = elem_size(d->dtype);
+  const int EV = 16 / es;
+  pl->lr = d->mode == ATTNRES_MODE_SOFTMAX && d->rank > 0;
+  const int heads = d->mode == ATTNRES_MODE_SOFTMAX ? d->heads : 1;
+  const int dh = d->dim / heads;
+  bool vec = (d->dim % EV == 0) && (dh % EV == 0);
+  for (int s = 0; vec && s < d->n_src; ++s)
+    vec = aligned16(d->values[s]) && ((d->value_row_stride[s] * es) % 16 == 0);
+  for (int i = 0; vec && i < n_extra; ++i) vec = !extra[i] || aligned16(extra[i]);
+  for (int s = 0; vec && extra_src && s < d->n_src; ++s) vec = !extra_src[s] || aligned16(extra_src[s]);
+  if (vec && d->mode == ATTNRES_MODE_SOFTMAX && d->rank == 0) vec = aligned16(d->query);
+  pl->vec = vec ? 1 : 0;
+  pl->E = vec ? EV : 1;
+  pl->ncols = (d->dim + kWaveSize * pl->E - 1) / (kWaveSize * pl->E);
+  pl->nmax = 0;
+  if (d->mode == ATTNRES_MODE_SOFTMAX && d->rank == 0) {
+    // register-resident kernels for up to 16 sources, streaming beyond
+    pl->nmax = d->n_src <= 8 ? 8 : d->n_src <= 16 ? 16 : 64;
+    pl->cb = vec ? 2 : 4;
+  } else {
+    pl->cb = vec ? 2 : 4;
+  }
+  pl->wpt = (pl->ncols + pl->cb - 1) / pl->cb;
+  if (pl->wpt > 16)
+    return fail(ATTNRES_EUNSUPPORTED, "dim=%d needs %d waves per token (max 16) on the %s path", d->dim, pl->wpt,
+                vec ? "vector" : "unaligned");
+  pl->key_vec = 0;
+  if (pl->lr) {
+    const int rh = d->rank / d->heads;
+    bool kv = rh % EV == 0;
+    for (int s = 0; kv && s < d->n_src; ++s) kv = aligned16(d->keys[s]) && ((d->key_row_stride[s] * es) % 16 == 0);
+    if (kv && d->query) kv = aligned16(d->query);
+    if (kv && d->query_dyn) kv = aligned16(d->query_dyn) && ((d->query_dyn_row_stride * es) % 16 == 0);
+    pl->key_vec = kv ? 1 : 0;
+  }
+  return ATTNRES_OK;
+}
+
+void fill_params(const attnres_read_desc* d, const Plan& pl, ReadParams* p) {
+  memset(p, 0, sizeof(*p));
+  for (int s = 0; s < d->n_src; ++s) {
+    p->val[s] = d->values[s];
+    p->vstride[s] = (int32_t)d->value_row_stride[s];
+    if (pl.lr) {
+      p->key[s] = d->keys[s];
+      p->kstride[s] = (int32_t)d->key_row_stride[s];
+    }
+  }
+  const bool softmax = d->mode == ATTNRES_MODE_SOFTMAX;
+  p->q_static = softmax ? d->query : nullptr;
+  p->q_dyn = softmax ? d->query_dyn : nullptr;
+  p->q_dyn_stride = d->query_dyn_row_stride;
+  p->gate = softmax ? d->gate : nullptr;
+  p->bias = softmax ? d->logit_bias : nullptr;
+  p->n_tok = d->n_tok;
+  p->n_src = d->n_src;
+  p->D = d->dim;
+  p->H = softmax ? d->heads : 1;
+  p->R = pl.lr ? d->rank : 0;
+  p->rh = pl.lr ? d->rank / d->heads : 0;
+  p->dh = d->dim / p->H;
+  p->ncols = pl.ncols;
+  p->key_norm = d->key_norm ? 1 : 0;
+  p->norm_out = d->normalize_output ? 1 : 0;
+  p->mode = d->mode;
+  p->gate_per_token = d->gate_per_token ? 1 : 0;
+  p->gate_act = d->gate_act;
+  p->key_vec = pl.key_vec;
+  p->scale = pl.lr ? d->logit_scale : 1.0f;
+  p->eps = d->norm_eps;
+}
+
+struct PartLayout {
+  int n_part, part_q, n_q, part_gate, n_gate, part_bias, n_bias;
+};
+
+PartLayout part_layout(const attnres_read_desc* d, bool want_q, bool want_gate, bool want_bias) {
+  PartLayout L{0, -1, 0, -1, 0, -1, 0};
+  if (d->mode != ATTNRES_MODE_SOFTMAX) return L;
+  const bool lr = d->rank > 0;
+  if (want_q && d->query) {
+    L.part_q = L.n_part;
+    L.n_q = lr ? d->rank : d->dim;
+    L.n_part += L.n_q;
+  }
+  if (want_gate && lr && d->gate && d->query_dyn && !d->gate_per_token) {
+    L.part_gate = L.n_part;
+    L.n_gate = d->heads;
+    L.n_part += L.n_gate;
+  }
+  if (want_bias && d->logit_bias) {
+    L.part_bias = L.n_part;
+    L.n_bias = d->n_src;
+    L.n_part += L.n_bias;
+  }
+  return L;
+}
+
+int64_t bwd_groups(int64_t n_tok) { return n_tok < kMaxBwdGroups ? n_tok : kMaxBwdGroups; }
+
+size_t lr_bwd_lds(const attnres_read_desc* d, const Plan& pl, int n_part) {
+  const int HN = d->heads * d->n_src;
+  const int cph_full = (d->dim / d->heads) / pl.E;
+  int gl = cph_full & (-cph_full);
+  if (gl > kWaveSize) gl = kWaveSize;
+  const int gpc = kWaveSize / gl;
+  const size_t floats =
+      5 * (size_t)HN + (size_t)d->n_src * pl.ncols * gpc + (size_t)d->n_src * d->rank + d->rank + n_part + 32;
+  return floats * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" int attnres_abi_version(void) { return ATTNRES_ABI_VERSION; }
+
+extern "C" const char* attnres_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" size_t attnres_read_backward_workspace_size(const attnres_read_desc* d) {
+  if (check_desc(d) != ATTNRES_OK) return 0;
+  const PartLayout L = part_layout(d, true, true, true);
+  if (L.n_part == 0 || d->n_tok == 0) return 0;
+  return (size_t)bwd_groups(d->n_tok) * L.n_part * sizeof(float);
+}
+
+extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, float* weights, float* out_inv_rms,
+                                    void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!out) return fail(ATTNRES_EINVAL, "out is NULL");
+  Plan pl;
+  const void* extra[1] = {out};
+  rc = make_plan(d, extra, 1, nullptr, &pl);
+  if (rc) return rc;
+  ReadParams p;
+  fill_params(d, pl, &p);
+  p.out = out;
+  p.weights = weights;
+  p.out_inv_rms = out_inv_rms;
+
+  Launch L;
+  L.vec = pl.vec;
+  L.wpt = pl.wpt;
+  L.nmax = pl.nmax;
+  L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t err;
+  if (d->mode == ATTNRES_MODE_AVERAGE) {
+    L.lds = 32 * sizeof(float);
+    err = launch_average_forward(d->dtype, p, L, st);
+  } else if (pl.lr) {
+    L.lds = (2 * (size_t)d->heads * d->n_src + 32) * sizeof(float);
+    if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LDS need %zu bytes", L.lds);
+    err = launch_lr_forward(d->dtype, p, L, st);
+  } else {
+    L.lds = (pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : (size_t)d->n_src + 32) * sizeof(float);
+    err = launch_base_forward(d->dtype, p, L, st);
+  }
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_read_grads* g, void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!g) return fail(ATTNRES_EINVAL, "grads is NULL");
+  const bool softmax = d->mode == ATTNRES_MODE_SOFTMAX;
+  const bool lr = softmax && d->rank > 0;
+  if (d->n_tok > 0) {
+    if (!g->grad_out) return fail(ATTNRES_EINVAL, "grad_out is NULL");
+    if (!g->dvalues) return fail(ATTNRES_EINVAL, "dvalues is NULL");
+    for (int s = 0; s < d->n_src; ++s)
+      if (!g->dvalues[s]) return fail(ATTNRES_EINVAL, "dvalues[%d] is NULL", s);
+    if (softmax && !g->weights) return fail(ATTNRES_EINVAL, "the backward needs the saved softmax weights");
+    if (d->normalize_output && (!g->out || !g->out_inv_rms))
+      return fail(ATTNRES_EINVAL, "normalize_output backward needs out and out_inv_rms");
+    if (lr) {
+      if (!g->dkeys) return fail(ATTNRES_EINVAL, "LR backward needs dkeys");
+      for (int s = 0; s < d->n_src; ++s)
+        if (!g->dkeys[s]) return fail(ATTNRES_EINVAL, "dkeys[%d] is NULL", s);
+      if (d->query_dyn && !g->dquery_dyn) return fail(ATTNRES_EINVAL, "per-token query needs dquery_dyn");
+      if (d->gate && d->gate_per_token && !g->dgate) return fail(ATTNRES_EINVAL, "per-token gate needs dgate");
+    }
+  }
+  if (d->n_tok == 0) {
+    // gradients of the cross-token quantities are zero
+    hipStream_t st = (hipStream_t)stream;
+    const int es = elem_size(d->dtype);
+    if (softmax && g->dquery && d->query)
+      (void)hipMemsetAsync(g->dquery, 0, (size_t)(lr ? d->rank : d->dim) * es, st);
+    if (softmax && g->dgate && d->gate && !d->gate_per_token) (void)hipMemsetAsync(g->dgate, 0, (size_t)d->heads * es, st);
+    if (softmax && g->dbias && d->logit_bias) (void)hipMemsetAsync(g->dbias, 0, (size_t)d->n_src * 4, st);
+    return ATTNRES_OK;
+  }
+  Plan pl;
+  const void* extra[2] = {g->grad_out, d->normalize_output ? g->out : nullptr};
+  rc = make_plan(d, extra, 2, g->dvalues, &pl);
+  if (rc) return rc;
+
+  ReadBwdParams bp;
+  memset(&bp, 0, sizeof(bp));
+  fill_params(d, pl, &bp.f);
+  bp.f.out = const_cast<void*>(g->out);
+  bp.gout = g->grad_out;
+  bp.saved_w = g->weights;
+  bp.saved_inv = g->out_inv_rms;
+  for (int s = 0; s < d->n_src; ++s) {
+    bp.dval[s] = g->dvalues[s];
+    if (lr) bp.dkey[s] = g->dkeys[s];
+  }
+  bp.dq_dyn = lr ? g->dquery_dyn : nullptr;
+  bp.dgate = lr ? g->dgate : nullptr;
+
+  const PartLayout PL = part_layout(d, g->dquery != nullptr, g->dgate != nullptr, g->dbias != nullptr);
+  const int64_t groups = bwd_groups(d->n_tok);
+  if (PL.n_part > 0) {
+    const size_t need = (size_t)groups * PL.n_part * sizeof(float);
+    if (!g->workspace || g->workspace_bytes < need)
+      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
+                  g->workspace ? g->workspace_bytes : (size_t)0);
+    bp.partials = (float*)g->workspace;
+  }
+  bp.n_part = PL.n_part;
+  bp.part_q = PL.part_q;
+  bp.part_gate = PL.part_gate;
+  bp.part_bias = PL.part_bias;
+
+  Launch L;
+  L.vec = pl.vec;
+  L.wpt = pl.wpt;
+  L.nmax = pl.nmax;
+  L.grid = (int)groups;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t err;
+  if (d->mode == ATTNRES_MODE_AVERAGE) {
+    L.lds = 32 * sizeof(float);
+    err = launch_average_backward(d->dtype, bp, L, st);
+  } else if (lr) {
+    L.lds = lr_bwd_lds(d, pl, PL.n_part);
+    if (L.lds > lds_limit())
+      return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS (limit %zu)", L.lds, lds_limit());
+    err = launch_lr_backward(d->dtype, bp, L, st);
+  } else {
+    L.lds = (pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : 2 * (size_t)d->n_src + 32) * sizeof(float);
+    err = launch_base_backward(d->dtype, bp, L, st);
+  }
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
+
+  if (PL.n_part > 0) {
+    ReduceParams rp;
+    rp.partials = bp.partials;
+    rp.n_groups = (int32_t)groups;
+    rp.n_part = PL.n_part;
+    rp.part_q = PL.part_q;
+    rp.n_q = PL.n_q;
+    rp.part_gate = PL.part_gate;
+    rp.n_gate = PL.n_gate;
+    rp.part_bias = PL.part_bias;
+    rp.n_bias = PL.n_bias;
+    rp.dquery = g->dquery;
+    rp.dgate = g->dgate;
+    rp.dbias = g->dbias;
+    err = launch_reduce_partials(d->dtype, rp, st);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
+  }
+  return ATTNRES_OK;
+}

@@ -1,0 +1,170 @@
+// Device-side helpers shared by the AttnRes read kernels (gfx950 / CDNA4).
+//
+// Storage types are raw bits (fp32 as float, bf16 and fp16 as 16-bit words);
+// every computation is fp32.  The rounding helpers reproduce PyTorch's
+// round-to-nearest-even casts, which is how the kernels mirror the points
+// where the reference's eager op rounds to the tensor dtype.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace attnres {
+
+constexpr int kWave = 64;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bits_to_f32(uint32_t u) { return __uint_as_float(u); }
+
+// bf16 <-> fp32, round to nearest even (NaN stays NaN)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xffffu));
+}
+__device__ __forceinline__ float round_f16(float f) { return (float)(_Float16)f; }
+
+// ---------------------------------------------------------------- dtype tags
+struct F32 {
+  using S = float;
+  static constexpr int kCode = 0;
+  __device__ __forceinline__ static float rnd(float x) { return x; }
+  __device__ __forceinline__ static float from_bits(uint32_t u) { return __uint_as_float(u); }
+  __device__ __forceinline__ static float load1(const S* p) { return *p; }
+  __device__ __forceinline__ static void store1(S* p, float x) { *p = x; }
+};
+struct BF16 {
+  using S = uint16_t;
+  static constexpr int kCode = 1;
+  __device__ __forceinline__ static float rnd(float x) { return round_bf16(x); }
+  __device__ __forceinline__ static float load1(const S* p) { return __uint_as_float(((uint32_t)*p) << 16); }
+  __device__ __forceinline__ static void store1(S* p, float x) { *p = (S)f32_to_bf16_bits(x); }
+};
+struct F16 {
+  using S = uint16_t;
+  static constexpr int kCode = 2;
+  __device__ __forceinline__ static float rnd(float x) { return round_f16(x); }
+  __device__ __forceinline__ static float load1(const S* p) { return f16_bits_to_f32(*p); }
+  __device__ __forceinline__ static void store1(S* p, float x) { *p = (S)f32_to_f16_bits(x); }
+};
+
+// ---------------------------------------------------------------- vectors
+// A "vector" is E consecutive elements loaded or stored with one access:
+// 16 bytes on the fast path (8 bf16/fp16 or 4 fp32), one element otherwise.
+template <class DT, int E> struct Vec {
+  static constexpr int kBytes = E * (int)sizeof(typename DT::S);
+  static constexpr int kWords = kBytes >= 4 ? kBytes / 4 : 1;
+};
+
+template <class DT, int E>
+struct Raw {  // raw bits of one vector, kept packed in VGPRs until used
+  uint32_t w[Vec<DT, E>::kWords];
+};
+
+template <class DT, int E>
+__device__ __forceinline__ void load_raw(const typename DT::S* __restrict__ p, Raw<DT, E>& r) {
+  constexpr int B = Vec<DT, E>::kBytes;
+  if constexpr (B == 16) {
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  } else if constexpr (B == 8) {
+    u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    r.w[0] = v.x; r.w[1] = v.y;
+  } else if constexpr (B == 4) {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else {
+    r.w[0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(p));
+  }
+}
+
+template <class DT, int E>
+__device__ __forceinline__ void unpack(const Raw<DT, E>& r, float (&o)[E]) {
+  if constexpr (sizeof(typename DT::S) == 4) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) o[i] = __uint_as_float(r.w[i]);
+  } else if constexpr (E == 1) {
+    if constexpr (DT::kCode == 1) o[0] = __uint_as_float(r.w[0] << 16);
+    else o[0] = f16_bits_to_f32(r.w[0]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+      if constexpr (DT::kCode == 1) {
+        o[2 * i] = __uint_as_float(r.w[i] << 16);
+        o[2 * i + 1] = __uint_as_float(r.w[i] & 0xffff0000u);
+      } else {
+        o[2 * i] = f16_bits_to_f32(r.w[i]);
+        o[2 * i + 1] = f16_bits_to_f32(r.w[i] >> 16);
+      }
+    }
+  }
+}
+
+template <class DT, int E>
+__device__ __forceinline__ void load_vec(const typename DT::S* __restrict__ p, float (&o)[E]) {
+  Raw<DT, E> r;
+  load_raw<DT, E>(p, r);
+  unpack<DT, E>(r, o);
+}
+
+// store E fp32 values (already rounded where the caller wants) as DT
+template <class DT, int E>
+__device__ __forceinline__ void store_vec(typename DT::S* __restrict__ p, const float (&x)[E]) {
+  if constexpr (sizeof(typename DT::S) == 4) {
+    if constexpr (E == 4) {
+      u32x4 v = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
+      *reinterpret_cast<u32x4*>(p) = v;
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) p[i] = x[i];
+    }
+  } else {
+    if constexpr (E == 8) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t lo, hi;
+        if constexpr (DT::kCode == 1) { lo = f32_to_bf16_bits(x[2 * i]); hi = f32_to_bf16_bits(x[2 * i + 1]); }
+        else { lo = f32_to_f16_bits(x[2 * i]); hi = f32_to_f16_bits(x[2 * i + 1]); }
+        w[i] = lo | (hi << 16);
+      }
+      u32x4 v = {w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(p) = v;
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) DT::store1(p + i, x[i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- reductions
+// Butterfly all-reduce over the 64 lanes of a wave (every lane gets the sum;
+// the association order is fixed, so results are deterministic).
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+// Butterfly all-reduce inside aligned groups of `width` lanes (power of two).
+__device__ __forceinline__ float group_sum(float x, int width) {
+  for (int o = 1; o < width; o <<= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+__device__ __forceinline__ float gate_value(float g, int act) {
+  return act == 2 ? 1.0f / (1.0f + expf(-g)) : g;
+}
+
+}  // namespace attnres

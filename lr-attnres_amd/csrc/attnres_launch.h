@@ -1,0 +1,27 @@
+// Internal launch interface between the C ABI (attnres_capi.hip) and the
+// kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "attnres_params.h"
+
+namespace attnres {
+
+struct Launch {
+  int vec;      // 16-byte vector path (else one element per access)
+  int wpt;      // waves per token (workgroup = wpt * 64 threads)
+  int grid;     // workgroups (persistent over tokens)
+  size_t lds;   // dynamic LDS bytes
+  int nmax;     // base read: register-resident source slots (8/16/32/64)
+};
+
+hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_lr_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_base_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_base_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_average_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_average_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_reduce_partials(int dtype, const ReduceParams& p, hipStream_t st);
+
+}  // namespace attnres

@@ -1,0 +1,482 @@
+// LR AttnRes read: low-rank keys, multi-head depth softmax, forward and backward.
+//
+// Semantics follow the reference's eager op (attnres_ops.py:4163-4192) with its
+// rounding points mirrored: keys are rms-normed per head in fp32 and rounded to
+// the tensor dtype, logits are a dtype-rounded contraction times the scale
+// (rounded again) plus an fp32 bias, the softmax is fp32 and the mix uses the
+// dtype-rounded weights with fp32 accumulation.
+//
+// Work decomposition (one workgroup = one token at a time, persistent over
+// tokens):
+//   phase A  one thread per (head, source) pair scores its key slice
+//   phase B  the same pairs turn logits into softmax weights (saved as fp32)
+//   phase C  each wave streams its columns of the N value rows (16-byte loads,
+//            up to 8 sources x CB columns in flight per lane) and mixes them
+// The backward streams the value rows once more: dW partials and dv = w*g are
+// produced in the same pass, dW is reduced per (head, source) through LDS, and
+// the key/query chain runs on the (head, source) pairs.  Cross-token sums
+// (static query, per-site gate, bias) go to per-workgroup partials that
+// attnres_reduce_partials_kernel folds in a fixed order: no atomics.
+#include "attnres_device.h"
+#include "attnres_params.h"
+#include "attnres_launch.h"
+
+namespace attnres {
+
+constexpr int kSrcGroup = 8;
+
+// query element j of head h for token tok (fp32; composed queries are rounded
+// to the tensor dtype, as the reference casts the composed query)
+template <class DT>
+struct QueryView {
+  const typename DT::S* qs;
+  const typename DT::S* qd;
+  float gf;
+  __device__ __forceinline__ float at(int j) const {
+    float q = qs ? DT::load1(qs + j) : 0.f;
+    if (qd) q = DT::rnd(q + gf * DT::load1(qd + j));
+    return q;
+  }
+};
+
+template <class DT>
+__device__ __forceinline__ QueryView<DT> query_view(const ReadParams& p, int64_t tok, int h) {
+  using S = typename DT::S;
+  QueryView<DT> v;
+  v.qs = p.q_static ? (const S*)p.q_static + h * p.rh : nullptr;
+  v.qd = p.q_dyn ? (const S*)p.q_dyn + tok * p.q_dyn_stride + h * p.rh : nullptr;
+  v.gf = 1.f;
+  if (v.qd && p.gate) {
+    const S* gp = (const S*)p.gate + (p.gate_per_token ? tok * p.H : 0) + h;
+    v.gf = gate_value(DT::load1(gp), p.gate_act);
+  }
+  return v;
+}
+
+// Sum of squares of one key slice (rh elements).
+template <class DT>
+__device__ __forceinline__ float key_sumsq(const typename DT::S* kp, int rh, bool vec) {
+  constexpr int KV = 16 / (int)sizeof(typename DT::S);
+  float ss = 0.f;
+  if (vec) {
+    for (int j = 0; j < rh; j += KV) {
+      float k[KV];
+      load_vec<DT, KV>(kp + j, k);
+#pragma unroll
+      for (int i = 0; i < KV; ++i) ss += k[i] * k[i];
+    }
+  } else {
+    for (int j = 0; j < rh; ++j) {
+      const float k = DT::load1(kp + j);
+      ss += k * k;
+    }
+  }
+  return ss;
+}
+
+// logit of (head h, source s) for token tok
+template <class DT>
+__device__ float lr_logit(const ReadParams& p, int64_t tok, int h, int s) {
+  using S = typename DT::S;
+  constexpr int KV = 16 / (int)sizeof(S);
+  const int rh = p.rh;
+  const S* kp = (const S*)p.key[s] + tok * (int64_t)p.kstride[s] + h * rh;
+  const QueryView<DT> q = query_view<DT>(p, tok, h);
+  const bool vec = p.key_vec != 0;
+  float inv = 1.f;
+  if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(kp, rh, vec) / (float)rh + p.eps);
+  float dot = 0.f;
+  if (vec) {
+    for (int j = 0; j < rh; j += KV) {
+      float k[KV];
+      load_vec<DT, KV>(kp + j, k);
+#pragma unroll
+      for (int i = 0; i < KV; ++i) {
+        const float kh = p.key_norm ? DT::rnd(k[i] * inv) : k[i];
+        dot += kh * q.at(j + i);
+      }
+    }
+  } else {
+    for (int j = 0; j < rh; ++j) {
+      float k = DT::load1(kp + j);
+      const float kh = p.key_norm ? DT::rnd(k * inv) : k;
+      dot += kh * q.at(j);
+    }
+  }
+  float logit = DT::rnd(DT::rnd(dot) * p.scale);
+  if (p.bias) logit += p.bias[s];
+  return logit;
+}
+
+// softmax over the N sources of head h (logits in LDS); returns weight of pair pi
+__device__ __forceinline__ float softmax_pair(const float* s_logit, int N, int h, int pi) {
+  const float* lg = s_logit + h * N;
+  float m = lg[0];
+  for (int s = 1; s < N; ++s) m = fmaxf(m, lg[s]);
+  float den = 0.f;
+  for (int s = 0; s < N; ++s) den += expf(lg[s] - m);
+  return expf(s_logit[pi] - m) / den;
+}
+
+// ============================================================== forward
+template <class DT, int E, int CB>
+__global__ void __launch_bounds__(1024) lr_fwd_kernel(const ReadParams p) {
+  using S = typename DT::S;
+  extern __shared__ float smem[];
+  const int N = p.n_src, H = p.H, HN = H * N;
+  float* s_logit = smem;
+  float* s_w = smem + HN;
+  float* s_red = smem + 2 * HN;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int wpt = blockDim.x / kWave;
+
+  int eoff[CB], hd[CB];
+  bool ok[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    const int col = wave + c * wpt;
+    const int e = (col * kWave + lane) * E;
+    ok[c] = col < p.ncols && e < p.D;
+    eoff[c] = e;
+    hd[c] = ok[c] ? e / p.dh : 0;
+  }
+
+  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    for (int pi = tid; pi < HN; pi += blockDim.x) {
+      const int h = pi / N;
+      s_logit[pi] = lr_logit<DT>(p, tok, h, pi - h * N);
+    }
+    __syncthreads();
+    for (int pi = tid; pi < HN; pi += blockDim.x) {
+      const float pr = softmax_pair(s_logit, N, pi / N, pi);
+      if (p.weights) p.weights[tok * HN + pi] = pr;
+      s_w[pi] = DT::rnd(pr);
+    }
+    __syncthreads();
+
+    float acc[CB][E];
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc[c][i] = 0.f;
+
+    for (int s0 = 0; s0 < N; s0 += kSrcGroup) {
+      Raw<DT, E> r[kSrcGroup][CB];
+#pragma unroll
+      for (int i = 0; i < kSrcGroup; ++i) {
+        const int s = s0 + i;
+        if (s < N) {
+          const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
+#pragma unroll
+          for (int c = 0; c < CB; ++c)
+            if (ok[c]) load_raw<DT, E>(vp + eoff[c], r[i][c]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kSrcGroup; ++i) {
+        const int s = s0 + i;
+        if (s < N) {
+#pragma unroll
+          for (int c = 0; c < CB; ++c) {
+            if (ok[c]) {
+              float v[E];
+              unpack<DT, E>(r[i][c], v);
+              const float w = s_w[hd[c] * N + s];
+#pragma unroll
+              for (int e = 0; e < E; ++e) acc[c][e] += w * v[e];
+            }
+          }
+        }
+      }
+    }
+
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        acc[c][e] = DT::rnd(acc[c][e]);
+        if (ok[c]) ss += acc[c][e] * acc[c][e];
+      }
+    if (p.norm_out) {
+      ss = wave_sum(ss);
+      if (wpt > 1) {
+        if (lane == 0) s_red[wave] = ss;
+        __syncthreads();
+        ss = 0.f;
+        for (int w = 0; w < wpt; ++w) ss += s_red[w];
+      }
+      const float inv = 1.0f / sqrtf(ss / (float)p.D + p.eps);
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e] * inv);
+      if (tid == 0 && p.out_inv_rms) p.out_inv_rms[tok] = inv;
+    }
+    S* op = (S*)p.out + tok * (int64_t)p.D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+      if (ok[c]) store_vec<DT, E>(op + eoff[c], acc[c]);
+    __syncthreads();
+  }
+}
+
+// ============================================================== backward
+template <class DT, int E, int CB>
+__global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
+  using S = typename DT::S;
+  const ReadParams& p = bp.f;
+  extern __shared__ float smem[];
+  const int N = p.n_src, H = p.H, HN = H * N, R = p.R, rh = p.rh, D = p.D;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int wpt = blockDim.x / kWave;
+  // lanes per dW pre-reduction group: largest power of two dividing the
+  // vectors per head, at most a wave
+  const int cph_full = p.dh / E;
+  int gl = cph_full & (-cph_full);
+  if (gl > kWave) gl = kWave;
+  const int gpc = kWave / gl;       // groups per column
+  const int cph = cph_full / gl;    // groups per head
+
+  float* s_p = smem;
+  float* s_w = s_p + HN;
+  float* s_dw = s_w + HN;
+  float* s_ge = s_dw + HN;
+  float* s_dl = s_ge + HN;
+  float* s_part = s_dl + HN;                   // [N * ncols * gpc]
+  float* s_kh = s_part + N * p.ncols * gpc;    // [N * R]
+  float* s_dq = s_kh + N * R;                  // [R]
+  float* s_acc = s_dq + R;                     // [n_part]
+  float* s_red = s_acc + bp.n_part;            // [32]
+
+  for (int i = tid; i < bp.n_part; i += blockDim.x) s_acc[i] = 0.f;
+
+  int eoff[CB], hd[CB];
+  bool ok[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    const int col = wave + c * wpt;
+    const int e = (col * kWave + lane) * E;
+    ok[c] = col < p.ncols && e < D;
+    eoff[c] = e;
+    hd[c] = ok[c] ? e / p.dh : 0;
+  }
+  __syncthreads();
+
+  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    // ---- A: saved weights, upstream gradient (through the output norm)
+    for (int pi = tid; pi < HN; pi += blockDim.x) {
+      const float pr = bp.saved_w[tok * HN + pi];
+      s_p[pi] = pr;
+      s_w[pi] = DT::rnd(pr);
+    }
+    float g[CB][E];
+    const S* gp = (const S*)bp.gout + tok * (int64_t)D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      if (ok[c]) load_vec<DT, E>(gp + eoff[c], g[c]);
+      else
+#pragma unroll
+        for (int e = 0; e < E; ++e) g[c][e] = 0.f;
+    }
+    if (p.norm_out) {
+      float y[CB][E];
+      const S* yp = (const S*)p.out + tok * (int64_t)D;
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        if (ok[c]) load_vec<DT, E>(yp + eoff[c], y[c]);
+        else
+#pragma unroll
+          for (int e = 0; e < E; ++e) y[c][e] = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) dot += g[c][e] * y[c][e];
+      }
+      dot = wave_sum(dot);
+      if (wpt > 1) {
+        if (lane == 0) s_red[wave] = dot;
+        __syncthreads();
+        dot = 0.f;
+        for (int w = 0; w < wpt; ++w) dot += s_red[w];
+      }
+      const float inv = bp.saved_inv[tok];
+      const float md = dot / (float)D;
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) g[c][e] = ok[c] ? DT::rnd(inv * (g[c][e] - y[c][e] * md)) : 0.f;
+    }
+    __syncthreads();
+
+    // ---- B: stream the value rows: dW partials and dv = w * g
+    for (int s0 = 0; s0 < N; s0 += kSrcGroup) {
+      Raw<DT, E> r[kSrcGroup][CB];
+#pragma unroll
+      for (int i = 0; i < kSrcGroup; ++i) {
+        const int s = s0 + i;
+        if (s < N) {
+          const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
+#pragma unroll
+          for (int c = 0; c < CB; ++c)
+            if (ok[c]) load_raw<DT, E>(vp + eoff[c], r[i][c]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kSrcGroup; ++i) {
+        const int s = s0 + i;
+        if (s < N) {
+          S* dvp = (S*)bp.dval[s] + tok * (int64_t)D;
+#pragma unroll
+          for (int c = 0; c < CB; ++c) {
+            float part = 0.f;
+            if (ok[c]) {
+              float v[E], dv[E];
+              unpack<DT, E>(r[i][c], v);
+              const float w = s_w[hd[c] * N + s];
+#pragma unroll
+              for (int e = 0; e < E; ++e) {
+                part += g[c][e] * v[e];
+                dv[e] = DT::rnd(w * g[c][e]);
+              }
+              store_vec<DT, E>(dvp + eoff[c], dv);
+            }
+            part = group_sum(part, gl);
+            const int col = wave + c * wpt;
+            if (ok[c] && (lane & (gl - 1)) == 0) s_part[(s * p.ncols + col) * gpc + lane / gl] = part;
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- C: dW per (head, source)
+    for (int pi = tid; pi < HN; pi += blockDim.x) {
+      const int h = pi / N, s = pi - h * N;
+      const float* sp = s_part + s * p.ncols * gpc + h * cph;
+      float dw = 0.f;
+      for (int j = 0; j < cph; ++j) dw += sp[j];
+      s_dw[pi] = DT::rnd(dw);
+    }
+    __syncthreads();
+
+    // ---- D: softmax backward, key gradient, normalised keys for dq
+    for (int pi = tid; pi < HN; pi += blockDim.x) {
+      const int h = pi / N, s = pi - h * N;
+      float dot = 0.f;
+      for (int t = 0; t < N; ++t) dot += s_p[h * N + t] * s_dw[h * N + t];
+      const float dl = s_p[pi] * (s_dw[pi] - dot);
+      s_dl[pi] = dl;
+      const float ge = DT::rnd(DT::rnd(dl) * p.scale);
+      s_ge[pi] = ge;
+
+      const S* kp = (const S*)p.key[s] + tok * (int64_t)p.kstride[s] + h * rh;
+      const QueryView<DT> q = query_view<DT>(p, tok, h);
+      float inv = 1.f;
+      if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(kp, rh, p.key_vec != 0) / (float)rh + p.eps);
+      float m = 0.f;
+      for (int j = 0; j < rh; ++j) {
+        const float k = DT::load1(kp + j);
+        const float kh = p.key_norm ? DT::rnd(k * inv) : k;
+        s_kh[s * R + h * rh + j] = kh;
+        if (p.key_norm) m += DT::rnd(ge * q.at(j)) * (k * inv);
+      }
+      S* dkp = (S*)bp.dkey[s] + tok * (int64_t)R + h * rh;
+      const float mr = m / (float)rh;
+      for (int j = 0; j < rh; ++j) {
+        const float dkh = DT::rnd(ge * q.at(j));
+        float dk = dkh;
+        if (p.key_norm) {
+          const float yk = DT::load1(kp + j) * inv;
+          dk = DT::rnd(inv * (dkh - yk * mr));
+        }
+        DT::store1(dkp + j, dk);
+      }
+    }
+    __syncthreads();
+
+    // ---- E: query gradient (per token or accumulated), bias accumulation
+    for (int j = tid; j < R; j += blockDim.x) {
+      const int h = j / rh;
+      float a = 0.f;
+      for (int s = 0; s < N; ++s) a += s_ge[h * N + s] * s_kh[s * R + j];
+      const float t = p.q_dyn ? DT::rnd(a) : a;
+      if (bp.part_q >= 0) s_acc[bp.part_q + j] += t;
+      if (p.q_dyn) {
+        const QueryView<DT> q = query_view<DT>(p, tok, h);
+        if (bp.dq_dyn) DT::store1((S*)bp.dq_dyn + tok * (int64_t)R + j, DT::rnd(q.gf * t));
+        if (p.gate) s_dq[j] = t * DT::load1(q.qd + (j - h * rh));
+      }
+    }
+    if (bp.part_bias >= 0) {
+      for (int s = tid; s < N; s += blockDim.x) {
+        float b = 0.f;
+        for (int h = 0; h < H; ++h) b += s_dl[h * N + s];
+        s_acc[bp.part_bias + s] += b;
+      }
+    }
+    if (p.q_dyn && p.gate) {
+      __syncthreads();
+      for (int h = tid; h < H; h += blockDim.x) {
+        float c = 0.f;
+        for (int j = 0; j < rh; ++j) c += s_dq[h * rh + j];
+        const S* gptr = (const S*)p.gate + (p.gate_per_token ? tok * H : 0) + h;
+        if (p.gate_act == ATTNRES_GATE_SIGMOID) {
+          const float sg = gate_value(DT::load1(gptr), p.gate_act);
+          c *= sg * (1.f - sg);
+        }
+        if (p.gate_per_token) {
+          if (bp.dgate) DT::store1((S*)bp.dgate + tok * H + h, DT::rnd(c));
+        } else if (bp.part_gate >= 0) {
+          s_acc[bp.part_gate + h] += c;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (bp.partials)
+    for (int i = tid; i < bp.n_part; i += blockDim.x) bp.partials[(int64_t)blockIdx.x * bp.n_part + i] = s_acc[i];
+}
+
+// ============================================================== launchers
+template <class DT, int E, int CB>
+static hipError_t launch_lr_fwd_t(const ReadParams& p, int wpt, int grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((lr_fwd_kernel<DT, E, CB>), dim3(grid), dim3(wpt * kWave), lds, st, p);
+  return hipGetLastError();
+}
+
+template <class DT, int E, int CB>
+static hipError_t launch_lr_bwd_t(const ReadBwdParams& p, int wpt, int grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((lr_bwd_kernel<DT, E, CB>), dim3(grid), dim3(wpt * kWave), lds, st, p);
+  return hipGetLastError();
+}
+
+template <class DT>
+static hipError_t lr_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st) {
+  if (L.vec) return launch_lr_fwd_t<DT, 16 / sizeof(typename DT::S), 2>(p, L.wpt, L.grid, L.lds, st);
+  return launch_lr_fwd_t<DT, 1, 4>(p, L.wpt, L.grid, L.lds, st);
+}
+
+template <class DT>
+static hipError_t lr_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
+  if (L.vec) return launch_lr_bwd_t<DT, 16 / sizeof(typename DT::S), 2>(p, L.wpt, L.grid, L.lds, st);
+  return launch_lr_bwd_t<DT, 1, 4>(p, L.wpt, L.grid, L.lds, st);
+}
+
+hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {
+  switch (dtype) {
+    case ATTNRES_DTYPE_F32: return lr_fwd_dt<F32>(p, L, st);
+    case ATTNRES_DTYPE_BF16: return lr_fwd_dt<BF16>(p, L, st);
+    default: return lr_fwd_dt<F16>(p, L, st);
+  }
+}
+
+hipError_t launch_lr_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st) {
+  switch (dtype) {
+    case ATTNRES_DTYPE_F32: return lr_bwd_dt<F32>(p, L, st);
+    case ATTNRES_DTYPE_BF16: return lr_bwd_dt<BF16>(p, L, st);
+    default: return lr_bwd_dt<F16>(p, L, st);
+  }
+}
+
+}  // namespace attnres

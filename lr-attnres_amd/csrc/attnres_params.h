@@ -1,0 +1,66 @@
+// Kernel parameter blocks (passed by value as kernel arguments) and the
+// launch helpers shared by the LR and base read kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/attnres_hip.h"
+
+namespace attnres {
+
+constexpr int kMaxSources = ATTNRES_MAX_SOURCES;
+constexpr int kWaveSize = 64;  // CDNA wavefront
+// Backward grids are capped so the per-workgroup partial sums stay small and
+// the cross-token reduction order does not depend on the device.
+constexpr int kMaxBwdGroups = 2048;
+constexpr int kMaxFwdGroups = 65536;
+
+struct ReadParams {
+  const void* val[kMaxSources];
+  const void* key[kMaxSources];
+  int32_t vstride[kMaxSources];  // row strides in elements
+  int32_t kstride[kMaxSources];
+  const void* q_static;  // LR [H*rh] / base [D]
+  const void* q_dyn;     // [n_tok rows of R]
+  const void* gate;      // [H] or [n_tok, H]
+  const float* bias;     // [N]
+  void* out;             // [n_tok, D]
+  float* weights;        // [n_tok, H, N]
+  float* out_inv_rms;    // [n_tok]
+  int64_t n_tok;
+  int64_t q_dyn_stride;
+  int32_t n_src, D, H, R, rh, dh;
+  int32_t ncols;         // vector columns per row: ceil(D / (64*E))
+  int32_t key_norm, norm_out, mode;
+  int32_t gate_per_token, gate_act;
+  int32_t key_vec;       // keys / per-token queries allow 16-byte loads
+  float scale, eps;
+};
+
+struct ReadBwdParams {
+  ReadParams f;
+  const void* gout;          // [n_tok, D]
+  const float* saved_w;      // [n_tok, H, N]
+  const float* saved_inv;    // [n_tok]
+  void* dval[kMaxSources];   // [n_tok, D]
+  void* dkey[kMaxSources];   // [n_tok, R]
+  void* dq_dyn;              // [n_tok, R]
+  void* dgate;               // per-token gate gradient [n_tok, H]
+  float* partials;           // [gridDim.x, n_part]
+  int32_t n_part;            // slots per workgroup: q (R or D) | gate (H) | bias (N)
+  int32_t part_q, part_gate, part_bias;  // slot offsets (-1 = unused)
+};
+
+struct ReduceParams {
+  const float* partials;
+  int32_t n_groups, n_part;
+  int32_t part_q, n_q;        // static query slots
+  int32_t part_gate, n_gate;  // per-site gate slots
+  int32_t part_bias, n_bias;
+  void* dquery;               // dtype
+  void* dgate;                // dtype
+  float* dbias;
+};
+
+}  // namespace attnres

@@ -1,0 +1,169 @@
+"""CPU checks of the boundary: the C-ABI library loads, exports every symbol the
+header declares, lays out its structs as ctypes does, and validates arguments
+on the host (no kernel is launched here); the Python drop-in fails loudly
+without a GPU and keeps the reference's argument errors."""
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "attnres_hip.h")
+
+import _attnres_hip as H  # noqa: E402
+import attnres_ops as ops  # noqa: E402
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(attnres_[a-z_]+)\s*\(", text)))
+
+
+needs_lib = pytest.mark.skipif(not os.path.exists(H.LIB_PATH), reason="libattnres_hip.so not built")
+
+
+@needs_lib
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(H.LIB_PATH)
+    names = _declared_functions()
+    assert names == sorted(["attnres_abi_version", "attnres_last_error", "attnres_read_backward",
+                            "attnres_read_backward_workspace_size", "attnres_read_forward"])
+    for n in names:
+        assert hasattr(lib, n), n
+    nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
+    for n in names:
+        assert re.search(rf"\bT {n}\b", nm), f"{n} not exported"
+
+
+@needs_lib
+def test_abi_version_and_error_reporting():
+    lib = H.load()
+    assert lib.attnres_abi_version() == 1
+    rc = lib.attnres_read_forward(None, None, None, None, None)
+    assert rc == -1
+    assert b"desc is NULL" in lib.attnres_last_error()
+
+
+def _c_layout():
+    """offsetof / sizeof of the two structs, from a C compile of the header."""
+    src = r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "attnres_hip.h"
+#define P(s, f) printf(#s " " #f " %zu\n", offsetof(s, f));
+int main(void) {
+  printf("attnres_read_desc sizeof %zu\n", sizeof(attnres_read_desc));
+  printf("attnres_read_grads sizeof %zu\n", sizeof(attnres_read_grads));
+''' + "".join(f"  P(attnres_read_desc, {f})\n" for f, _ in H.ReadDesc._fields_) + \
+        "".join(f"  P(attnres_read_grads, {f})\n" for f, _ in H.ReadGrads._fields_) + "  return 0;\n}\n"
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "p.c")
+        exe = os.path.join(d, "p")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    res = {}
+    for line in out.strip().splitlines():
+        s, f, v = line.split()
+        res[(s, f)] = int(v)
+    return res
+
+
+def test_ctypes_structs_match_the_header():
+    lay = _c_layout()
+    for cls, name in ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads")):
+        assert ctypes.sizeof(cls) == lay[(name, "sizeof")]
+        for f, _ in cls._fields_:
+            assert getattr(cls, f).offset == lay[(name, f)], (name, f)
+
+
+def _desc(n_src=3, n_tok=16, dim=64, rank=16, heads=2, **kw):
+    vals = (ctypes.c_void_p * n_src)(*([0x1000] * n_src))
+    vstr = (ctypes.c_int64 * n_src)(*([dim] * n_src))
+    keys = (ctypes.c_void_p * n_src)(*([0x2000] * n_src))
+    kstr = (ctypes.c_int64 * n_src)(*([rank] * n_src))
+    d = H.ReadDesc()
+    d.n_src, d.dtype, d.n_tok, d.dim, d.rank, d.heads = n_src, 1, n_tok, dim, rank, heads
+    d.mode, d.key_norm, d.logit_scale, d.norm_eps = 0, 1, 0.25, H.FLT_EPSILON
+    d.values, d.value_row_stride = vals, vstr
+    if rank:
+        d.keys, d.key_row_stride = keys, kstr
+    d.query = 0x3000
+    for k, v in kw.items():
+        setattr(d, k, v)
+    d._keep = (vals, vstr, keys, kstr)
+    return d
+
+
+@needs_lib
+def test_host_validation_rejects_bad_descriptions_without_launching():
+    lib = H.load()
+    cases = [
+        (dict(n_src=0), -2, b"n_src"),
+        (dict(n_src=65), -2, b"n_src"),
+        (dict(heads=3), -1, b"heads"),
+        (dict(rank=0, heads=2), -1, b"heads == 1"),
+        (dict(dtype=7), -1, b"dtype"),
+        (dict(query=None), -1, b"query"),
+    ]
+    for kw, code, msg in cases:
+        n_src = kw.pop("n_src", 3)
+        d = _desc(n_src=max(1, min(n_src, 64)), **{k: v for k, v in kw.items() if k not in ("dtype",)})
+        d.n_src = n_src
+        if "dtype" in kw:
+            d.dtype = kw["dtype"]
+        rc = lib.attnres_read_forward(ctypes.byref(d), ctypes.c_void_p(0x4000), None, None, None)
+        assert rc == code, (kw, rc, lib.attnres_last_error())
+        assert msg in lib.attnres_last_error(), lib.attnres_last_error()
+
+
+@needs_lib
+def test_workspace_size_is_a_host_computation():
+    lib = H.load()
+    d = _desc(n_src=13, n_tok=16384, dim=1024, rank=64, heads=4)
+    # 2048 workgroups x (64 query slots) floats; no bias
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 2048 * 64 * 4
+    bias = (ctypes.c_float * 13)()
+    d.logit_bias = ctypes.cast(bias, ctypes.POINTER(ctypes.c_float))
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 2048 * (64 + 13) * 4
+    d.n_tok = 5
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 5 * (64 + 13) * 4
+    d.n_tok = 0
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 0
+
+
+def test_product_path_fails_loudly_on_cpu_tensors():
+    vs = [torch.randn(1, 2, 8) for _ in range(3)]
+    ks = [torch.randn(1, 2, 4) for _ in range(3)]
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lrid_attention_residual_read(vs, ks, torch.zeros(1, 4), 1, 1.0, True)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attention_residual_read(vs, torch.zeros(8), True)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attention_residual_average_read(vs)
+
+
+def test_reference_argument_errors_are_kept():
+    vs = [torch.randn(1, 2, 8) for _ in range(3)]
+    with pytest.raises(RuntimeError, match="mutually exclusive"):
+        ops._source_logit_bias([1, 2, 3], [0.0, 0.0, 0.0], 3, "cpu")
+    with pytest.raises(RuntimeError, match="length must match"):
+        ops._source_logit_bias([1, 2], None, 3, "cpu")
+    with pytest.raises(RuntimeError, match="must be positive"):
+        ops._source_logit_bias([1, 0, 2], None, 3, "cpu")
+    with pytest.raises(RuntimeError, match="value sources"):
+        ops.lrid_attention_residual_read(vs, vs[:2], torch.zeros(1, 8), 1, 1.0, True)
+    with pytest.raises(RuntimeError, match="must divide"):
+        ops.lrid_attention_residual_read(vs, [torch.randn(1, 2, 6)] * 3, torch.zeros(6), 4, 1.0, True)
+    # single source is the identity, as in the reference (no GPU needed)
+    assert ops.lrid_attention_residual_read(vs[:1], [torch.randn(1, 2, 4)], torch.zeros(1, 4), 1, 1.0, True) is vs[0]
+    assert ops.attention_residual_read(vs[:1], torch.zeros(8), True) is vs[0]
+    torch.testing.assert_close(ops.attention_residual_read(vs[:1], torch.zeros(8), True, normalize_output=True),
+                               torch.nn.functional.rms_norm(vs[0], (8,)))

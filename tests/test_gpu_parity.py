@@ -1,0 +1,381 @@
+"""GPU parity: the HIP kernels (through the drop-in API and its C ABI) against
+the CPU oracle and the reference's golden vectors, forward and backward."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import attnres_oracle as O
+import attnres_ops as ops
+import _attnres_hip as H
+from _golden import load, names
+from gpu_util import DEV, assert_close, leaf, gen, randn
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    H.load()
+
+
+# ------------------------------------------------------------------ golden vectors
+
+@pytest.mark.parametrize("name", names("lr"))
+def test_lr_golden(name):
+    t, m = load(name)
+    dt = DT[m["dtype"]]
+    S = m["S"]
+    v = [leaf(x) for x in t["values"].unbind(0)]
+    k = [leaf(x) for x in t["keys"].unbind(0)]
+    q = leaf(t["query"])
+    kw = {}
+    b = None
+    if m["has_bias"]:
+        b = leaf(t["bias"])
+        kw["source_logit_biases"] = b
+    if m["has_counts"]:
+        kw["source_counts"] = t["counts"].tolist()
+    out = ops.lrid_attention_residual_read(v, k, q, m["H"], m["scale"], m["key_norm"],
+                                           normalize_output=m["normalize_output"], **kw)
+    out.backward(t["grad_out"].to(DEV))
+    assert_close(out, t["out"], dt, "out")
+    for s in range(S):
+        assert_close(v[s].grad, t["dvalues"][s], dt, f"dv{s}")
+        assert_close(k[s].grad, t["dkeys"][s], dt, f"dk{s}")
+    assert_close(q.grad, t["dquery"], dt, "dq", reduced=not m["dynamic"])
+    if b is not None:
+        assert_close(b.grad, t["dbias"], dt, "dbias", reduced=True)
+
+
+@pytest.mark.parametrize("name", names("base"))
+def test_base_golden(name):
+    t, m = load(name)
+    dt = DT[m["dtype"]]
+    v = [leaf(x) for x in t["values"].unbind(0)]
+    q = leaf(t["query"])
+    kw = {}
+    b = None
+    if m["has_bias"]:
+        b = leaf(t["bias"])
+        kw["source_logit_biases"] = b
+    if m["has_counts"]:
+        kw["source_counts"] = t["counts"].tolist()
+    out = ops.attention_residual_read(v, q, m["key_norm"], normalize_output=m["normalize_output"], **kw)
+    out.backward(t["grad_out"].to(DEV))
+    assert_close(out, t["out"], dt, "out")
+    for s in range(m["S"]):
+        assert_close(v[s].grad, t["dvalues"][s], dt, f"dv{s}")
+    assert_close(q.grad, t["dquery"], dt, "dq", reduced=True)
+    if b is not None:
+        assert_close(b.grad, t["dbias"], dt, "dbias", reduced=True)
+
+
+@pytest.mark.parametrize("name", names("average"))
+def test_average_golden(name):
+    t, m = load(name)
+    out = ops.attention_residual_average_read([x.to(DEV) for x in t["values"].unbind(0)], m["normalize_output"])
+    assert_close(out, t["out"], DT[m["dtype"]], "out")
+
+
+# ------------------------------------------------------------------ oracle sweeps
+
+def _lr_case(seed, dtype, B, T, D, S, R, Hh, scale, key_norm, dynamic=False, bias=None, counts=None,
+             normalize_output=False, stacked=False):
+    g = gen(seed)
+    vals = [randn(g, (B, T, D), dtype) for _ in range(S)]
+    keys = [randn(g, (B, T, R), dtype) for _ in range(S)]
+    qshape = (B, T, Hh, R // Hh) if dynamic else (Hh, R // Hh)
+    query = randn(g, qshape, torch.float32, 0.5)
+    up = randn(g, (B, T, D), dtype)
+    kw = {}
+    bias_c = bias_d = None
+    if bias is not None:
+        bias_c = torch.tensor(bias, dtype=torch.float32, requires_grad=True)
+        bias_d = leaf(bias_c)
+    if counts is not None:
+        kw["source_counts"] = counts
+    # GPU
+    vd = [leaf(x) for x in vals]
+    kd = [leaf(x) for x in keys]
+    qd = leaf(query)
+    vin = torch.stack(vd) if stacked else vd
+    out = ops.lrid_attention_residual_read(vin, kd, qd, Hh, scale, key_norm, normalize_output=normalize_output,
+                                           source_logit_biases=bias_d, **kw)
+    out.backward(up.to(DEV))
+    # oracle (CPU)
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    kc = [x.clone().requires_grad_(True) for x in keys]
+    qc = query.clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref(vc, kc, qc, Hh, scale, key_norm, normalize_output=normalize_output,
+                                             source_logit_biases=bias_c, **kw)
+    ref.backward(up)
+    assert_close(out, ref, dtype, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, dtype, f"dv{s}")
+        assert_close(kd[s].grad, kc[s].grad, dtype, f"dk{s}")
+    assert_close(qd.grad, qc.grad, dtype, "dq", reduced=not dynamic)
+    if bias is not None:
+        assert_close(bias_d.grad, bias_c.grad, dtype, "dbias", reduced=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Hh,key_norm", [(1, True), (4, True), (4, False), (2, True)])
+def test_lr_matches_oracle(dtype, Hh, key_norm):
+    _lr_case(100 + Hh + 10 * int(key_norm), dtype, 2, 7, 128, 6, 32, Hh, 0.25, key_norm)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lr_options_dynamic_bias_norm(dtype):
+    _lr_case(201, dtype, 2, 6, 128, 4, 32, 2, 0.5, True, dynamic=True)
+    _lr_case(202, dtype, 1, 9, 64, 5, 16, 2, 0.25, True, bias=[0.0, 0.69, -0.3, 1.2, 0.1])
+    _lr_case(203, dtype, 1, 9, 64, 5, 16, 2, 0.25, True, counts=[1, 2, 3, 4, 2])
+    _lr_case(204, dtype, 2, 5, 256, 5, 64, 1, 0.125, True, normalize_output=True)
+    _lr_case(205, dtype, 2, 5, 256, 5, 64, 4, 0.125, True, normalize_output=True, bias=[0.1, 0.2, 0.3, 0.4, 0.5])
+
+
+@pytest.mark.parametrize("S", [2, 9, 16, 17, 33, 64])
+def test_lr_source_counts(S):
+    _lr_case(300 + S, torch.bfloat16, 1, 5, 128, S, 32, 2, 0.25, True)
+
+
+@pytest.mark.parametrize("D,R,Hh", [(40, 6, 2), (24, 12, 3), (2048, 128, 8), (1024, 512, 1), (520, 16, 2)])
+def test_lr_odd_and_large_shapes(D, R, Hh):
+    # D=40/24: not a multiple of 8 -> one-element path; R/H=3: scalar key path;
+    # R=512/H=1: long key rows; D=2048: two waves per token; D=520: partial column
+    _lr_case(400 + D, torch.bfloat16, 1, 5, D, 5, R, Hh, 1.0 / math.sqrt(R // Hh), True)
+
+
+def test_lr_stacked_and_unaligned_keys():
+    _lr_case(501, torch.bfloat16, 2, 4, 128, 5, 32, 2, 0.25, True, stacked=True)
+    # keys as views of the value tails (model.py lrid_key_from_output_tail): not 16-byte aligned rows
+    g = gen(502)
+    vals = [randn(g, (2, 4, 128), torch.float32) for _ in range(5)]
+    vd = [leaf(x) for x in vals]
+    kd = [x[..., -24:] for x in vd]
+    q = leaf(randn(g, (2, 12), torch.float32, 0.5))
+    out = ops.lrid_attention_residual_read(vd, kd, q, 2, 0.3, True)
+    up = randn(g, (2, 4, 128), torch.float32)
+    out.backward(up.to(DEV))
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    qc = q.detach().cpu().clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref(vc, [x[..., -24:] for x in vc], qc, 2, 0.3, True)
+    ref.backward(up)
+    assert_close(out, ref, torch.float32, "out")
+    for s in range(5):
+        assert_close(vd[s].grad, vc[s].grad, torch.float32, f"dv{s}")
+    assert_close(q.grad, qc.grad, torch.float32, "dq")
+
+
+def test_lr_aliased_sources_and_row_strides():
+    g = gen(503)
+    base = randn(g, (2, 4, 256), torch.bfloat16)
+    vd_base = leaf(base)
+    a = vd_base[..., :128]          # row stride 256 (not dense)
+    b = vd_base[..., 128:]
+    keys = [randn(g, (2, 4, 32), torch.bfloat16) for _ in range(3)]
+    kd = [leaf(x) for x in keys]
+    q = leaf(randn(g, (2, 16), torch.float32, 0.5))
+    out = ops.lrid_attention_residual_read([a, b, a], kd, q, 2, 0.25, True)   # `a` twice
+    up = randn(g, (2, 4, 128), torch.bfloat16)
+    out.backward(up.to(DEV))
+    vc = base.clone().requires_grad_(True)
+    kc = [x.clone().requires_grad_(True) for x in keys]
+    qc = q.detach().cpu().clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref([vc[..., :128], vc[..., 128:], vc[..., :128]], kc, qc, 2, 0.25, True)
+    ref.backward(up)
+    assert_close(out, ref, torch.bfloat16, "out")
+    assert_close(vd_base.grad, vc.grad, torch.bfloat16, "dvalues (aliased)")
+
+
+def _base_case(seed, dtype, B, T, D, S, key_norm, bias=None, counts=None, normalize_output=False, qstd=0.5):
+    g = gen(seed)
+    vals = [randn(g, (B, T, D), dtype) for _ in range(S)]
+    query = randn(g, (D,), torch.float32, qstd)
+    up = randn(g, (B, T, D), dtype)
+    kw = {}
+    bias_c = bias_d = None
+    if bias is not None:
+        bias_c = torch.tensor(bias, dtype=torch.float32, requires_grad=True)
+        bias_d = leaf(bias_c)
+    if counts is not None:
+        kw["source_counts"] = counts
+    vd = [leaf(x) for x in vals]
+    qd = leaf(query)
+    out = ops.attention_residual_read(vd, qd, key_norm, normalize_output=normalize_output,
+                                      source_logit_biases=bias_d, **kw)
+    out.backward(up.to(DEV))
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    qc = query.clone().requires_grad_(True)
+    ref = O.attention_residual_read_ref(vc, qc, key_norm, normalize_output=normalize_output,
+                                        source_logit_biases=bias_c, **kw)
+    ref.backward(up)
+    assert_close(out, ref, dtype, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, dtype, f"dv{s}")
+    assert_close(qd.grad, qc.grad, dtype, "dq", reduced=True)
+    if bias is not None:
+        assert_close(bias_d.grad, bias_c.grad, dtype, "dbias", reduced=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("key_norm", [True, False])
+def test_base_matches_oracle(dtype, key_norm):
+    _base_case(600 + int(key_norm), dtype, 2, 6, 256, 5, key_norm)
+
+
+@pytest.mark.parametrize("S,D", [(2, 64), (7, 768), (12, 1024), (16, 2048), (17, 256), (40, 128), (5, 40)])
+def test_base_shapes(S, D):
+    _base_case(700 + S, torch.bfloat16, 1, 5, D, S, True)
+
+
+def test_base_options():
+    _base_case(801, torch.bfloat16, 2, 3, 64, 3, True, counts=[1, 3, 2])
+    _base_case(802, torch.float32, 1, 4, 32, 4, True, bias=[0.0, 0.7, -0.3, 1.1])
+    _base_case(803, torch.bfloat16, 1, 4, 128, 6, True, normalize_output=True)
+    _base_case(804, torch.bfloat16, 2, 4, 1536, 20, True, normalize_output=True, bias=[0.1] * 20)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("normalize_output", [False, True])
+def test_average_forward_backward(dtype, normalize_output):
+    g = gen(900)
+    vals = [randn(g, (2, 3, 96), dtype) for _ in range(5)]
+    up = randn(g, (2, 3, 96), dtype)
+    vd = [leaf(x) for x in vals]
+    out = ops.attention_residual_average_read(vd, normalize_output=normalize_output)
+    out.backward(up.to(DEV))
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    ref = O.attention_residual_average_read_ref(vc, normalize_output)
+    ref.backward(up)
+    assert_close(out, ref, dtype, "out")
+    for s in range(5):
+        assert_close(vd[s].grad, vc[s].grad, dtype, f"dv{s}")
+
+
+@pytest.mark.parametrize("act,per_token", [("sigmoid", True), ("linear", False)])
+def test_gated_query_matches_oracle(act, per_token):
+    dtype = torch.bfloat16
+    g = gen(1000 + int(per_token))
+    B, T, D, S, R, Hh = 2, 5, 256, 5, 64, 4
+    vals = [randn(g, (B, T, D), dtype) for _ in range(S)]
+    keys = [randn(g, (B, T, R), dtype) for _ in range(S)]
+    qs = randn(g, (Hh, R // Hh), dtype, 0.3)
+    qdyn = randn(g, (B, T, R), dtype)
+    gate = randn(g, (B, T, Hh) if per_token else (Hh,), dtype)
+    up = randn(g, (B, T, D), dtype)
+    vd, kd = [leaf(x) for x in vals], [leaf(x) for x in keys]
+    qsd, qdd, gd = leaf(qs), leaf(qdyn), leaf(gate)
+    out = ops.lrid_attention_residual_read_gated(vd, kd, qsd, qdd, gd, Hh, 0.25, True, gate_activation=act)
+    out.backward(up.to(DEV))
+    vc, kc = [x.clone().requires_grad_(True) for x in vals], [x.clone().requires_grad_(True) for x in keys]
+    qsc, qdc, gc = (x.clone().requires_grad_(True) for x in (qs, qdyn, gate))
+    # the kernel composes in fp32 and rounds once; the oracle composes in fp32 too
+    q = O.gated_query_ref(qsc.float(), qdc.float(), gc.float(), Hh, act)
+    ref = O.lrid_attention_residual_read_ref(vc, kc, q, Hh, 0.25, True)
+    ref.backward(up)
+    assert_close(out, ref, dtype, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, dtype, f"dv{s}")
+        assert_close(kd[s].grad, kc[s].grad, dtype, f"dk{s}")
+    assert_close(qdd.grad, qdc.grad, dtype, "dq_dyn")
+    assert_close(qsd.grad, qsc.grad, dtype, "dq_static", reduced=True)
+    assert_close(gd.grad, gc.grad, dtype, "dgate", reduced=not per_token)
+
+
+# ------------------------------------------------------------------ properties
+
+def test_weights_sum_to_one_and_match_oracle():
+    g = gen(1100)
+    B, T, D, S, R, Hh = 2, 64, 1024, 13, 64, 4
+    vals = [randn(g, (B, T, D), torch.bfloat16) for _ in range(S)]
+    keys = [randn(g, (B, T, R), torch.bfloat16) for _ in range(S)]
+    q = randn(g, (Hh, R // Hh), torch.bfloat16, 0.5)
+    vd, kd = [x.to(DEV) for x in vals], [x.to(DEV) for x in keys]
+    desc = H.Desc(vd, kd, q.to(DEV), None, None, None, Hh, 0.25, True, False, H.MODE_SOFTMAX, 0, False)
+    out, w, _ = H.forward(desc, vd[0].device, torch.bfloat16, True, False)
+    torch.cuda.synchronize()
+    sums = w.double().sum(-1)
+    assert float((sums - 1).abs().max()) <= 1e-6
+    ref = O.softmax_weights_ref(keys, q, Hh, 0.25, True, base=False)  # [S,B,T,H]
+    ref = ref.permute(1, 2, 3, 0).reshape(B * T, Hh, S)
+    assert float((w.cpu() - ref).abs().max()) <= 1e-6
+
+
+def test_backward_is_deterministic():
+    g = gen(1200)
+    B, T, D, S, R, Hh = 4, 256, 1024, 13, 64, 4
+    vals = [randn(g, (B, T, D), torch.bfloat16).to(DEV) for _ in range(S)]
+    keys = [randn(g, (B, T, R), torch.bfloat16).to(DEV) for _ in range(S)]
+    q = randn(g, (Hh, R // Hh), torch.float32, 0.5).to(DEV)
+    bias = torch.randn(S, generator=g).to(DEV)
+    up = randn(g, (B, T, D), torch.bfloat16).to(DEV)
+    grads = []
+    for _ in range(2):
+        vd = [x.clone().requires_grad_(True) for x in vals]
+        kd = [x.clone().requires_grad_(True) for x in keys]
+        qd = q.clone().requires_grad_(True)
+        bd = bias.clone().requires_grad_(True)
+        ops.lrid_attention_residual_read(vd, kd, qd, Hh, 0.25, True, source_logit_biases=bd).backward(up)
+        grads.append((qd.grad.clone(), bd.grad.clone(), vd[3].grad.clone(), kd[5].grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+def test_empty_and_single_source():
+    v = [torch.randn(2, 0, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True) for _ in range(3)]
+    k = [torch.randn(2, 0, 16, device=DEV, dtype=torch.bfloat16, requires_grad=True) for _ in range(3)]
+    q = torch.randn(2, 8, device=DEV, requires_grad=True)
+    out = ops.lrid_attention_residual_read(v, k, q, 2, 0.25, True)
+    assert out.shape == (2, 0, 64)
+    out.sum().backward()
+    assert q.grad is not None and float(q.grad.abs().sum()) == 0.0
+    x = torch.randn(1, 3, 64, device=DEV)
+    assert ops.lrid_attention_residual_read([x], [torch.randn(1, 3, 16, device=DEV)], q, 2, 0.25, True) is x
+    with pytest.raises(RuntimeError, match="at most 64"):
+        ops.attention_residual_read([x] * 65, torch.randn(64, device=DEV), True)
+
+
+def test_config3_full_size_token_subset():
+    """C3 (B8 T2048 d1024 N13 r64 H4 bf16) at full size: tokens are independent,
+    so the oracle on a token subset checks the full-size launch exactly; the
+    static-query gradient over all tokens is checked by linearity (sum of the
+    gradients of two token halves)."""
+    g = gen(3)
+    B, T, D, S, R, Hh = 8, 2048, 1024, 13, 64, 4
+    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
+    keys = [torch.randn(B, T, R, generator=g).to(torch.bfloat16) for _ in range(S)]
+    q = (torch.randn(Hh, R // Hh, generator=g) * 0.02)
+    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    vd = [leaf(x) for x in vals]
+    kd = [leaf(x) for x in keys]
+    qd = leaf(q)
+    out = ops.lrid_attention_residual_read(vd, kd, qd, Hh, 0.25, True)
+    out.backward(up.to(DEV))
+    torch.cuda.synchronize()
+    sel = (slice(3, 4), slice(1000, 1064))
+    vc = [x[sel].clone().requires_grad_(True) for x in vals]
+    kc = [x[sel].clone().requires_grad_(True) for x in keys]
+    qc = q.clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref(vc, kc, qc, Hh, 0.25, True)
+    ref.backward(up[sel])
+    assert_close(out[sel], ref, torch.bfloat16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad[sel], vc[s].grad, torch.bfloat16, f"dv{s}")
+        assert_close(kd[s].grad[sel], kc[s].grad, torch.bfloat16, f"dk{s}")
+    # linearity of the cross-token reduction
+    halves = []
+    for part in (slice(0, 4), slice(4, 8)):
+        qh = leaf(q)
+        o = ops.lrid_attention_residual_read([x.detach()[part] for x in vd], [x.detach()[part] for x in kd], qh,
+                                             Hh, 0.25, True)
+        o.backward(up[part].to(DEV))
+        halves.append(qh.grad)
+    full = qd.grad.float().cpu()
+    summed = (halves[0].float() + halves[1].float()).cpu()
+    assert float((full - summed).abs().max()) <= 2e-2 * max(1.0, float(full.abs().max()))
