@@ -116,7 +116,7 @@ class Workload:
         self.fwd_only = bool(c.get("fwd_only"))
 
     def fwd(self, stream):
-        rc = self.lib.attnres_read_forward(ctypes.byref(self.desc.c), self.outptr,
+        rc = self.lib.attnres_read_forward(ctypes.byref(self.desc.c), self.outptr, None,
                                           None if self.fwd_only else self.wptr, None, stream)
         if rc:
             raise RuntimeError(self.lib.attnres_last_error().decode())
@@ -240,6 +240,27 @@ def cpu_baseline(c, budget_s):
                        f"workload ({dt}), {iters} iterations in {el:.1f} s, torch {torch.__version__}")
 
 
+def copy_calibration(steps, gib=1.0):
+    """A plain device-to-device copy of known size: the achievable-bandwidth
+    reference, and the kernel whose FETCH_SIZE / WRITE_SIZE counters scale the
+    AttnRes kernels' counter readings to bytes."""
+    n = int(gib * (1 << 30)) // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    nbytes = 2 * n * 4
+    print(json.dumps({"copy_bytes_per_launch": nbytes, "ms": round(ms, 5), "gbs": round(nbytes / ms / 1e6, 1)}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,15 +270,20 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-api", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="time a plain 1 GiB device copy instead (bandwidth / counter reference)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the AttnRes read shards "
               "by tokens with no exchange, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
-    c = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
+    c = CONFIGS[args.config]
     wl = Workload(c, dev)
     stream = torch.cuda.current_stream(dev)
     sv = ctypes.c_void_p(stream.cuda_stream)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 1
+#define ATTNRES_ABI_VERSION 2
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -90,7 +90,7 @@ typedef struct attnres_read_desc {
 /* Gradient buffers for attnres_read_backward. */
 typedef struct attnres_read_grads {
   const void* grad_out;      /* [n_tok, dim] dense */
-  const void* out;           /* forward output [n_tok, dim] (read when normalize_output) */
+  const void* out_prenorm;   /* forward output before its rms-norm [n_tok, dim] (when normalize_output) */
   const float* out_inv_rms;  /* [n_tok] from the forward (when normalize_output) */
   const float* weights;      /* [n_tok, heads, n_src] softmax weights saved by the forward */
   void* const* dvalues;      /* [n_src] device pointers, each [n_tok, dim] dense */
@@ -112,16 +112,17 @@ const char* attnres_last_error(void);
 /*
  * Forward read.  Writes out [n_tok, dim] (dtype); when `weights` is not NULL
  * also the fp32 softmax weights [n_tok, heads, n_src] (the backward needs
- * them); when normalize_output, out is rms-normed and out_inv_rms [n_tok]
- * (fp32, may be NULL when no backward follows) receives 1/rms.
+ * them); when normalize_output, out is rms-normed, out_prenorm [n_tok, dim]
+ * (dtype) receives the read before the norm and out_inv_rms [n_tok] (fp32)
+ * receives 1/rms -- both may be NULL when no backward follows.
  *
  * Replaces: _lrid_read_list_triton / attnres::lrid_read_list
  *   (attnres_ops.py:4533-4629, 4636-4722), _attnres_read_list_triton
  *   (attnres_ops.py:2297-2339), _attnres_read_triton (attnres_ops.py:2271-2294)
  *   and the average-read launcher (attnres_ops.py:2568-2617).
  */
-int attnres_read_forward(const attnres_read_desc* desc, void* out, float* weights, float* out_inv_rms,
-                         void* stream);
+int attnres_read_forward(const attnres_read_desc* desc, void* out, void* out_prenorm, float* weights,
+                         float* out_inv_rms, void* stream);
 
 /*
  * Backward of attnres_read_forward from the saved weights.  Writes every

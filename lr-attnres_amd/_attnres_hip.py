@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_SOURCES = 64
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -59,7 +59,7 @@ class ReadGrads(ctypes.Structure):
 
     _fields_ = [
         ("grad_out", c_void_p),
-        ("out", c_void_p),
+        ("out_prenorm", c_void_p),
         ("out_inv_rms", POINTER(c_float)),
         ("weights", POINTER(c_float)),
         ("dvalues", POINTER(c_void_p)),
@@ -93,7 +93,8 @@ def load() -> ctypes.CDLL:
     lib.attnres_abi_version.restype = c_int
     lib.attnres_last_error.restype = ctypes.c_char_p
     lib.attnres_read_forward.restype = c_int
-    lib.attnres_read_forward.argtypes = [POINTER(ReadDesc), c_void_p, POINTER(c_float), POINTER(c_float), c_void_p]
+    lib.attnres_read_forward.argtypes = [POINTER(ReadDesc), c_void_p, c_void_p, POINTER(c_float), POINTER(c_float),
+                                         c_void_p]
     lib.attnres_read_backward.restype = c_int
     lib.attnres_read_backward.argtypes = [POINTER(ReadDesc), POINTER(ReadGrads), c_void_p]
     lib.attnres_read_backward_workspace_size.restype = c_size_t
@@ -186,22 +187,29 @@ class Desc:
         self.c = d
 
 
-def forward(desc: Desc, device, dtype, need_weights: bool, normalize_output: bool):
-    """Launch the forward; returns (out [n_tok, D], weights [n_tok,H,N] | empty, inv_rms [n_tok] | empty)."""
+def forward(desc: Desc, device, dtype, need_weights: bool, normalize_output: bool, for_backward: bool):
+    """Launch the forward.
+
+    Returns (out [n_tok, D], weights [n_tok,H,N] | empty, inv_rms [n_tok] | empty,
+    prenorm [n_tok, D] | empty); weights are written when ``need_weights``, the
+    output-norm state when ``normalize_output and for_backward``.
+    """
     lib = load()
     out = torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype)
     if need_weights:
         w = torch.empty((desc.n_tok, desc.heads, desc.n_src), device=device, dtype=torch.float32)
     else:
         w = torch.empty((0,), device=device, dtype=torch.float32)
-    inv = torch.empty((desc.n_tok if normalize_output else 0,), device=device, dtype=torch.float32)
-    rc = lib.attnres_read_forward(ctypes.byref(desc.c), _ptr(out), _fptr(w) if need_weights else None,
-                                  _fptr(inv) if normalize_output else None, _stream(device))
+    keep = normalize_output and for_backward
+    inv = torch.empty((desc.n_tok if keep else 0,), device=device, dtype=torch.float32)
+    pre = torch.empty((desc.n_tok, desc.D) if keep else (0,), device=device, dtype=dtype)
+    rc = lib.attnres_read_forward(ctypes.byref(desc.c), _ptr(out), _ptr(pre) if keep else None,
+                                  _fptr(w) if need_weights else None, _fptr(inv) if keep else None, _stream(device))
     _check(rc, "forward")
-    return out, w, inv
+    return out, w, inv, pre
 
 
-def backward(desc: Desc, device, dtype, grad_out, out, inv_rms, weights, want_dquery: bool,
+def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, want_dquery: bool,
              want_dgate: bool, want_dbias: bool, query_shape, gate_shape, lr: bool, has_query_dyn: bool):
     """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias)."""
     lib = load()
@@ -214,7 +222,7 @@ def backward(desc: Desc, device, dtype, grad_out, out, inv_rms, weights, want_dq
     db = torch.empty((n,), device=device, dtype=torch.float32) if want_dbias else None
     g = ReadGrads()
     g.grad_out = grad_out.data_ptr()
-    g.out = out.data_ptr() if out is not None and out.numel() else None
+    g.out_prenorm = prenorm.data_ptr() if prenorm is not None and prenorm.numel() else None
     g.out_inv_rms = _fptr(inv_rms) if inv_rms is not None and inv_rms.numel() else None
     g.weights = _fptr(weights) if weights is not None and weights.numel() else None
     dv_arr = (c_void_p * n)(*[t.data_ptr() for t in dvals])

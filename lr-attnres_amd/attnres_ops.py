@@ -144,15 +144,15 @@ def _empty(device):
 def _read_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], query_dyn: Optional[Tensor],
              gate: Optional[Tensor], bias: Optional[Tensor], heads: int, logit_scale: float, key_norm: bool,
              normalize_output: bool, mode: int, gate_act: int, gate_per_token: bool,
-             save_weights: bool) -> tuple[Tensor, Tensor, Tensor]:
+             save_weights: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     v0 = values[0]
     B, T, D = v0.shape
     desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
                      mode, gate_act, gate_per_token)
     with torch.cuda.device(v0.device):
-        out, w, inv = _hip.forward(desc, v0.device, v0.dtype, save_weights and mode == _hip.MODE_SOFTMAX,
-                                   normalize_output)
-    return out.view(B, T, D), w, inv
+        out, w, inv, pre = _hip.forward(desc, v0.device, v0.dtype, save_weights and mode == _hip.MODE_SOFTMAX,
+                                        normalize_output, save_weights)
+    return out.view(B, T, D), w, inv, pre
 
 
 @_read_op.register_fake
@@ -163,13 +163,15 @@ def _read_fake(values, keys, query, query_dyn, gate, bias, heads, logit_scale, k
     n_tok = B * T
     out = v0.new_empty((B, T, D))
     w = v0.new_empty((n_tok, heads, len(values)) if save_weights and mode == 0 else (0,), dtype=torch.float32)
-    inv = v0.new_empty((n_tok if normalize_output else 0,), dtype=torch.float32)
-    return out, w, inv
+    keep = normalize_output and save_weights
+    inv = v0.new_empty((n_tok if keep else 0,), dtype=torch.float32)
+    pre = v0.new_empty((n_tok, D) if keep else (0,))
+    return out, w, inv, pre
 
 
 @torch.library.custom_op("attnres_hip::read_backward", mutates_args=())
 def _read_backward_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], query_dyn: Optional[Tensor],
-                      gate: Optional[Tensor], bias: Optional[Tensor], grad_out: Tensor, out: Tensor,
+                      gate: Optional[Tensor], bias: Optional[Tensor], grad_out: Tensor, prenorm: Tensor,
                       inv_rms: Tensor, weights: Tensor, heads: int, logit_scale: float, key_norm: bool,
                       normalize_output: bool, mode: int, gate_act: int,
                       gate_per_token: bool) -> tuple[list[Tensor], list[Tensor], Tensor, Tensor, Tensor, Tensor]:
@@ -181,7 +183,7 @@ def _read_backward_op(values: list[Tensor], keys: list[Tensor], query: Optional[
     lr = len(keys) > 0
     with torch.cuda.device(dev):
         dvals, dkeys, dq, dqd, dg, db = _hip.backward(
-            desc, dev, v0.dtype, grad_out.contiguous(), out, inv_rms, weights,
+            desc, dev, v0.dtype, grad_out.contiguous(), prenorm, inv_rms, weights,
             want_dquery=query is not None and mode == _hip.MODE_SOFTMAX,
             want_dgate=gate is not None, want_dbias=bias is not None,
             query_shape=tuple(query.shape) if query is not None else (0,),
@@ -196,7 +198,7 @@ def _read_backward_op(values: list[Tensor], keys: list[Tensor], query: Optional[
 
 
 @_read_backward_op.register_fake
-def _read_backward_fake(values, keys, query, query_dyn, gate, bias, grad_out, out, inv_rms, weights, heads,
+def _read_backward_fake(values, keys, query, query_dyn, gate, bias, grad_out, prenorm, inv_rms, weights, heads,
                         logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token):
     e = lambda: values[0].new_empty((0,))  # noqa: E731
     return ([v.new_empty(v.shape) for v in values], [k.new_empty(k.shape) for k in keys],
@@ -209,16 +211,16 @@ def _read_backward_fake(values, keys, query, query_dyn, gate, bias, grad_out, ou
 def _read_setup_context(ctx, inputs, output):
     (values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode, gate_act,
      gate_per_token, save_weights) = inputs
-    out, w, inv = output
+    out, w, inv, pre = output
     ctx.n_values = len(values)
     ctx.n_keys = len(keys)
     ctx.has = (query is not None, query_dyn is not None, gate is not None, bias is not None)
     opt = [t for t in (query, query_dyn, gate, bias) if t is not None]
-    ctx.save_for_backward(*values, *keys, *opt, out, w, inv)
+    ctx.save_for_backward(*values, *keys, *opt, pre, w, inv)
     ctx.flags = (heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token)
 
 
-def _read_backward(ctx, grad_out, grad_w, grad_inv):
+def _read_backward(ctx, grad_out, grad_w, grad_inv, grad_pre):
     saved = list(ctx.saved_tensors)
     values = saved[:ctx.n_values]
     keys = saved[ctx.n_values:ctx.n_values + ctx.n_keys]
@@ -227,9 +229,9 @@ def _read_backward(ctx, grad_out, grad_w, grad_inv):
     for present in ctx.has:
         opt.append(rest.pop(0) if present else None)
     query, query_dyn, gate, bias = opt
-    out, w, inv = rest
+    pre, w, inv = rest
     heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token = ctx.flags
-    dvals, dkeys, dq, dqd, dg, db = _read_backward_op(values, keys, query, query_dyn, gate, bias, grad_out, out,
+    dvals, dkeys, dq, dqd, dg, db = _read_backward_op(values, keys, query, query_dyn, gate, bias, grad_out, pre,
                                                       inv, w, heads, logit_scale, key_norm, normalize_output, mode,
                                                       gate_act, gate_per_token)
     return (dvals, dkeys,
@@ -245,7 +247,7 @@ def _run(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_nor
          gate_act=_hip.GATE_NONE, gate_per_token=False):
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in [*values, *keys, query, query_dyn, gate, bias])
-    out, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, int(heads), float(logit_scale), bool(key_norm),
+    out, _, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, int(heads), float(logit_scale), bool(key_norm),
                          bool(normalize_output), int(mode), int(gate_act), bool(gate_per_token), bool(save))
     return out
 

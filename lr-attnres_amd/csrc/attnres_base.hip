@@ -90,28 +90,41 @@ __device__ __forceinline__ float norm_output(float (&acc)[CB][E], const Cols<CB,
   return inv;
 }
 
-// g <- d rms_norm backward, using the saved (normed, rounded) output y
+// g <- d rms_norm backward from the saved pre-norm output x (dtype-rounded, as
+// the reference's autograd keeps it) and 1/rms:
+//   dx = inv*g - x*inv^3*mean(g*x), one rounding to the dtype
 template <class DT, int CB, int E>
-__device__ __forceinline__ void norm_output_backward(float (&g)[CB][E], const typename DT::S* yp, float inv,
+__device__ __forceinline__ void norm_output_backward(float (&g)[CB][E], const typename DT::S* xp, float inv,
                                                      const Cols<CB, E>& cl, int D, float* s_red, int lane,
                                                      int wave, int wpt) {
-  float y[CB][E];
+  float x[CB][E];
   float dot = 0.f;
 #pragma unroll
   for (int c = 0; c < CB; ++c) {
-    if (cl.ok[c]) load_vec<DT, E>(yp + cl.eoff[c], y[c]);
+    if (cl.ok[c]) load_vec<DT, E>(xp + cl.eoff[c], x[c]);
     else
 #pragma unroll
-      for (int e = 0; e < E; ++e) y[c][e] = 0.f;
+      for (int e = 0; e < E; ++e) x[c][e] = 0.f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) dot += g[c][e] * y[c][e];
+    for (int e = 0; e < E; ++e) dot += g[c][e] * x[c][e];
   }
   dot = block_sum1(dot, s_red, lane, wave, wpt);
-  const float md = dot / (float)D;
+  const float k3 = inv * inv * inv * (dot / (float)D);
 #pragma unroll
   for (int c = 0; c < CB; ++c)
 #pragma unroll
-    for (int e = 0; e < E; ++e) g[c][e] = cl.ok[c] ? DT::rnd(inv * (g[c][e] - y[c][e] * md)) : 0.f;
+    for (int e = 0; e < E; ++e) g[c][e] = cl.ok[c] ? DT::rnd(inv * g[c][e] - x[c][e] * k3) : 0.f;
+}
+
+// store the pre-norm output (when a backward will need it)
+template <class DT, int CB, int E>
+__device__ __forceinline__ void store_prenorm(const ReadParams& p, int64_t tok, const float (&acc)[CB][E],
+                                              const Cols<CB, E>& cl) {
+  if (!p.out_prenorm) return;
+  typename DT::S* xp = (typename DT::S*)p.out_prenorm + tok * (int64_t)p.D;
+#pragma unroll
+  for (int c = 0; c < CB; ++c)
+    if (cl.ok[c]) store_vec<DT, E>(xp + cl.eoff[c], acc[c]);
 }
 
 // ============================================================== base forward
@@ -231,6 +244,7 @@ __global__ void __launch_bounds__(1024) base_fwd_kernel(const ReadParams p) {
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e]);
     if (p.norm_out) {
+      store_prenorm<DT, CB, E>(p, tok, acc, cl);
       const float inv = norm_output<DT, CB, E>(acc, cl, D, p.eps, s_red, lane, wave, wpt);
       if (tid == 0 && p.out_inv_rms) p.out_inv_rms[tok] = inv;
     }
@@ -242,15 +256,23 @@ __global__ void __launch_bounds__(1024) base_fwd_kernel(const ReadParams p) {
 }
 
 // ============================================================== base backward
+// A workgroup holds `teams` independent one-wave token streams when a token
+// fits one wave (every reduction is then a wave butterfly, no LDS, no
+// barrier); otherwise one team of wpt waves.  The teams' query/bias
+// accumulators are folded in team order at the end.
 template <class DT, int E, int CB, int NMAX>
 __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) {
   using S = typename DT::S;
   const ReadParams& p = bp.f;
   extern __shared__ float smem[];
-  float* s_red = smem;  // [wpt * NMAX]
+  float* s_red = smem;  // [wpt * NMAX] (only used when wpt > 1, then teams == 1)
   const int N = p.n_src, D = p.D;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int wpt = blockDim.x / kWave;
+  const int wpt = p.wpt;
+  const int team_threads = wpt * kWave;
+  const int teams = blockDim.x / team_threads;
+  const int team = threadIdx.x / team_threads;
+  const int tid = threadIdx.x - team * team_threads;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
   const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
 
   float q[CB][E], qacc[CB][E];
@@ -265,7 +287,8 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
   }
   float bacc = 0.f;  // bias slot `tid` (tid < N)
 
-  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+  const int64_t tstride = (int64_t)gridDim.x * teams;
+  for (int64_t tok = (int64_t)blockIdx.x * teams + team; tok < p.n_tok; tok += tstride) {
     float g[CB][E];
     const S* gp = (const S*)bp.gout + tok * (int64_t)D;
 #pragma unroll
@@ -289,7 +312,7 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
 #pragma unroll
     for (int s = 0; s < NMAX; ++s) pw[s] = s < N ? bp.saved_w[tok * N + s] : 0.f;
     if (p.norm_out)
-      norm_output_backward<DT, CB, E>(g, (const S*)p.out + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
+      norm_output_backward<DT, CB, E>(g, (const S*)p.out_prenorm + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
                                       wave, wpt);
 
     // stage 1: dW = <g, v> and (key_norm) sum of squares
@@ -375,7 +398,8 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
     }
   }
 
-  if (bp.partials) {
+  if (!bp.partials) return;
+  if (teams == 1) {
     float* part = bp.partials + (int64_t)blockIdx.x * bp.n_part;
     if (bp.part_q >= 0) {
 #pragma unroll
@@ -385,6 +409,24 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
           for (int e = 0; e < E; ++e) part[bp.part_q + cl.eoff[c] + e] = qacc[c][e];
     }
     if (bp.part_bias >= 0 && tid < N) part[bp.part_bias + tid] = bacc;
+    return;
+  }
+  // several teams: stage each team's accumulators in LDS, fold in team order
+  __syncthreads();
+  float* fold = smem + team * bp.n_part;
+  if (bp.part_q >= 0) {
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+      if (cl.ok[c])
+#pragma unroll
+        for (int e = 0; e < E; ++e) fold[bp.part_q + cl.eoff[c] + e] = qacc[c][e];
+  }
+  if (bp.part_bias >= 0 && tid < N) fold[bp.part_bias + tid] = bacc;
+  __syncthreads();
+  for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
+    float a = 0.f;
+    for (int t = 0; t < teams; ++t) a += smem[t * bp.n_part + i];
+    bp.partials[(int64_t)blockIdx.x * bp.n_part + i] = a;
   }
 }
 
@@ -467,6 +509,7 @@ __global__ void __launch_bounds__(1024) base_fwd_stream_kernel(const ReadParams 
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e]);
     if (p.norm_out) {
+      store_prenorm<DT, CB, E>(p, tok, acc, cl);
       const float inv = norm_output<DT, CB, E>(acc, cl, D, p.eps, s_red, lane, wave, wpt);
       if (tid == 0 && p.out_inv_rms) p.out_inv_rms[tok] = inv;
     }
@@ -512,7 +555,7 @@ __global__ void __launch_bounds__(1024) base_bwd_stream_kernel(const ReadBwdPara
         for (int e = 0; e < E; ++e) g[c][e] = 0.f;
     }
     if (p.norm_out)
-      norm_output_backward<DT, CB, E>(g, (const S*)p.out + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
+      norm_output_backward<DT, CB, E>(g, (const S*)p.out_prenorm + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
                                       wave, wpt);
     for (int s = 0; s < N; ++s) {
       const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
@@ -626,6 +669,7 @@ __global__ void __launch_bounds__(1024) avg_fwd_kernel(const ReadParams p) {
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e] / (float)N);
     if (p.norm_out) {
+      store_prenorm<DT, CB, E>(p, tok, acc, cl);
       const float inv = norm_output<DT, CB, E>(acc, cl, D, p.eps, s_red, lane, wave, wpt);
       if (tid == 0 && p.out_inv_rms) p.out_inv_rms[tok] = inv;
     }
@@ -657,7 +701,7 @@ __global__ void __launch_bounds__(1024) avg_bwd_kernel(const ReadBwdParams bp) {
         for (int e = 0; e < E; ++e) g[c][e] = 0.f;
     }
     if (p.norm_out)
-      norm_output_backward<DT, CB, E>(g, (const S*)p.out + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
+      norm_output_backward<DT, CB, E>(g, (const S*)p.out_prenorm + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
                                       wave, wpt);
 #pragma unroll
     for (int c = 0; c < CB; ++c)
@@ -708,7 +752,7 @@ static hipError_t base_fwd_t(const ReadParams& p, const Launch& L, hipStream_t s
 }
 template <class DT, int E, int CB, int NMAX>
 static hipError_t base_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((base_bwd_kernel<DT, E, CB, NMAX>), dim3(L.grid), dim3(L.wpt * kWave), L.lds, st, p);
+  hipLaunchKernelGGL((base_bwd_kernel<DT, E, CB, NMAX>), dim3(L.grid), dim3(L.wpt * kWave * L.teams), L.lds, st, p);
   return hipGetLastError();
 }
 

@@ -161,6 +161,7 @@ void fill_params(const attnres_read_desc* d, const Plan& pl, ReadParams* p) {
   p->rh = pl.lr ? d->rank / d->heads : 0;
   p->dh = d->dim / p->H;
   p->ncols = pl.ncols;
+  p->wpt = pl.wpt;
   p->key_norm = d->key_norm ? 1 : 0;
   p->norm_out = d->normalize_output ? 1 : 0;
   p->mode = d->mode;
@@ -199,6 +200,10 @@ PartLayout part_layout(const attnres_read_desc* d, bool want_q, bool want_gate, 
 
 int64_t bwd_groups(int64_t n_tok) { return n_tok < kMaxBwdGroups ? n_tok : kMaxBwdGroups; }
 
+// token teams per LR-backward workgroup: four independent one-wave teams when a
+// token fits one wave, else one team of wpt waves
+int lr_bwd_teams(const Plan& pl) { return pl.wpt == 1 ? 4 : 1; }
+
 size_t lr_bwd_lds(const attnres_read_desc* d, const Plan& pl, int n_part) {
   const int HN = d->heads * d->n_src;
   const int cph_full = (d->dim / d->heads) / pl.E;
@@ -207,7 +212,7 @@ size_t lr_bwd_lds(const attnres_read_desc* d, const Plan& pl, int n_part) {
   const int gpc = kWaveSize / gl;
   const size_t floats =
       5 * (size_t)HN + (size_t)d->n_src * pl.ncols * gpc + (size_t)d->n_src * d->rank + d->rank + n_part + 32;
-  return floats * sizeof(float);
+  return floats * sizeof(float) * lr_bwd_teams(pl);
 }
 
 }  // namespace
@@ -223,19 +228,20 @@ extern "C" size_t attnres_read_backward_workspace_size(const attnres_read_desc* 
   return (size_t)bwd_groups(d->n_tok) * L.n_part * sizeof(float);
 }
 
-extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, float* weights, float* out_inv_rms,
-                                    void* stream) {
+extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void* out_prenorm, float* weights,
+                                    float* out_inv_rms, void* stream) {
   int rc = check_desc(d);
   if (rc) return rc;
   if (d->n_tok == 0) return ATTNRES_OK;
   if (!out) return fail(ATTNRES_EINVAL, "out is NULL");
   Plan pl;
-  const void* extra[1] = {out};
-  rc = make_plan(d, extra, 1, nullptr, &pl);
+  const void* extra[2] = {out, d->normalize_output ? out_prenorm : nullptr};
+  rc = make_plan(d, extra, 2, nullptr, &pl);
   if (rc) return rc;
   ReadParams p;
   fill_params(d, pl, &p);
   p.out = out;
+  p.out_prenorm = d->normalize_output ? out_prenorm : nullptr;
   p.weights = weights;
   p.out_inv_rms = out_inv_rms;
 
@@ -243,6 +249,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, float
   L.vec = pl.vec;
   L.wpt = pl.wpt;
   L.nmax = pl.nmax;
+  L.teams = 1;
   L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;
@@ -273,8 +280,8 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     for (int s = 0; s < d->n_src; ++s)
       if (!g->dvalues[s]) return fail(ATTNRES_EINVAL, "dvalues[%d] is NULL", s);
     if (softmax && !g->weights) return fail(ATTNRES_EINVAL, "the backward needs the saved softmax weights");
-    if (d->normalize_output && (!g->out || !g->out_inv_rms))
-      return fail(ATTNRES_EINVAL, "normalize_output backward needs out and out_inv_rms");
+    if (d->normalize_output && (!g->out_prenorm || !g->out_inv_rms))
+      return fail(ATTNRES_EINVAL, "normalize_output backward needs out_prenorm and out_inv_rms");
     if (lr) {
       if (!g->dkeys) return fail(ATTNRES_EINVAL, "LR backward needs dkeys");
       for (int s = 0; s < d->n_src; ++s)
@@ -294,14 +301,14 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     return ATTNRES_OK;
   }
   Plan pl;
-  const void* extra[2] = {g->grad_out, d->normalize_output ? g->out : nullptr};
+  const void* extra[2] = {g->grad_out, d->normalize_output ? g->out_prenorm : nullptr};
   rc = make_plan(d, extra, 2, g->dvalues, &pl);
   if (rc) return rc;
 
   ReadBwdParams bp;
   memset(&bp, 0, sizeof(bp));
   fill_params(d, pl, &bp.f);
-  bp.f.out = const_cast<void*>(g->out);
+  bp.f.out_prenorm = const_cast<void*>(g->out_prenorm);
   bp.gout = g->grad_out;
   bp.saved_w = g->weights;
   bp.saved_inv = g->out_inv_rms;
@@ -330,7 +337,16 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   L.vec = pl.vec;
   L.wpt = pl.wpt;
   L.nmax = pl.nmax;
+  L.teams = 1;
   L.grid = (int)groups;
+  if (lr) L.teams = lr_bwd_teams(pl);
+  else if (softmax && pl.nmax <= 16 && pl.wpt == 1) L.teams = 4;  // resident base read, one wave per token
+  if (L.teams > 1) {
+    // workgroups carry `teams` tokens at a time; the workspace is sized for
+    // `groups` partials and the grid never exceeds it
+    const int64_t need = (d->n_tok + L.teams - 1) / L.teams;
+    L.grid = (int)(need < groups ? need : groups);
+  }
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;
   if (d->mode == ATTNRES_MODE_AVERAGE) {
@@ -342,7 +358,10 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS (limit %zu)", L.lds, lds_limit());
     err = launch_lr_backward(d->dtype, bp, L, st);
   } else {
-    L.lds = (pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : 2 * (size_t)d->n_src + 32) * sizeof(float);
+    size_t fl = pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : 2 * (size_t)d->n_src + 32;
+    if ((size_t)L.teams * PL.n_part > fl) fl = (size_t)L.teams * PL.n_part;
+    L.lds = fl * sizeof(float);
+    if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "base backward needs %zu bytes of LDS", L.lds);
     err = launch_base_backward(d->dtype, bp, L, st);
   }
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
@@ -350,7 +369,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   if (PL.n_part > 0) {
     ReduceParams rp;
     rp.partials = bp.partials;
-    rp.n_groups = (int32_t)groups;
+    rp.n_groups = L.grid;
     rp.n_part = PL.n_part;
     rp.part_q = PL.part_q;
     rp.n_q = PL.n_q;

@@ -13,7 +13,8 @@ struct Launch {
   int wpt;      // waves per token (workgroup = wpt * 64 threads)
   int grid;     // workgroups (persistent over tokens)
   size_t lds;   // dynamic LDS bytes
-  int nmax;     // base read: register-resident source slots (8/16/32/64)
+  int nmax;     // base read: register-resident source slots (8/16; more = streaming)
+  int teams;    // token teams per workgroup (LR backward)
 };
 
 hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);

@@ -199,6 +199,12 @@ __global__ void __launch_bounds__(1024) lr_fwd_kernel(const ReadParams p) {
         if (ok[c]) ss += acc[c][e] * acc[c][e];
       }
     if (p.norm_out) {
+      if (p.out_prenorm) {
+        S* xp = (S*)p.out_prenorm + tok * (int64_t)p.D;
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+          if (ok[c]) store_vec<DT, E>(xp + eoff[c], acc[c]);
+      }
       ss = wave_sum(ss);
       if (wpt > 1) {
         if (lane == 0) s_red[wave] = ss;
@@ -222,14 +228,34 @@ __global__ void __launch_bounds__(1024) lr_fwd_kernel(const ReadParams p) {
 }
 
 // ============================================================== backward
+// A workgroup holds `teams` token teams of `wpt` waves each.  With one wave
+// per token (wpt == 1) the teams run independent token streams and synchronise
+// at wavefront scope only, so a workgroup keeps several tokens in flight
+// without workgroup barriers; with wpt > 1 there is one team and the team
+// barrier is the workgroup barrier.  Each team owns an LDS region; the teams'
+// cross-token accumulators are summed in team order at the end.
+__device__ __forceinline__ void team_sync(int wpt) {
+  if (wpt == 1) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    __syncthreads();
+  }
+}
+
 template <class DT, int E, int CB>
 __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
   using S = typename DT::S;
   const ReadParams& p = bp.f;
   extern __shared__ float smem[];
   const int N = p.n_src, H = p.H, HN = H * N, R = p.R, rh = p.rh, D = p.D;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int wpt = blockDim.x / kWave;
+  const int wpt = p.wpt;
+  const int team_threads = wpt * kWave;
+  const int teams = blockDim.x / team_threads;
+  const int team = threadIdx.x / team_threads;
+  const int tid = threadIdx.x - team * team_threads;  // thread index inside the team
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
   // lanes per dW pre-reduction group: largest power of two dividing the
   // vectors per head, at most a wave
   const int cph_full = p.dh / E;
@@ -238,7 +264,8 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
   const int gpc = kWave / gl;       // groups per column
   const int cph = cph_full / gl;    // groups per head
 
-  float* s_p = smem;
+  const int team_floats = 5 * HN + N * p.ncols * gpc + N * R + R + bp.n_part + 32;
+  float* s_p = smem + team * team_floats;
   float* s_w = s_p + HN;
   float* s_dw = s_w + HN;
   float* s_ge = s_dw + HN;
@@ -249,7 +276,7 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
   float* s_acc = s_dq + R;                     // [n_part]
   float* s_red = s_acc + bp.n_part;            // [32]
 
-  for (int i = tid; i < bp.n_part; i += blockDim.x) s_acc[i] = 0.f;
+  for (int i = tid; i < bp.n_part; i += team_threads) s_acc[i] = 0.f;
 
   int eoff[CB], hd[CB];
   bool ok[CB];
@@ -261,11 +288,12 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
     eoff[c] = e;
     hd[c] = ok[c] ? e / p.dh : 0;
   }
-  __syncthreads();
+  team_sync(wpt);
 
-  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+  const int64_t stride = (int64_t)gridDim.x * teams;
+  for (int64_t tok = (int64_t)blockIdx.x * teams + team; tok < p.n_tok; tok += stride) {
     // ---- A: saved weights, upstream gradient (through the output norm)
-    for (int pi = tid; pi < HN; pi += blockDim.x) {
+    for (int pi = tid; pi < HN; pi += team_threads) {
       const float pr = bp.saved_w[tok * HN + pi];
       s_p[pi] = pr;
       s_w[pi] = DT::rnd(pr);
@@ -280,33 +308,34 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
         for (int e = 0; e < E; ++e) g[c][e] = 0.f;
     }
     if (p.norm_out) {
-      float y[CB][E];
-      const S* yp = (const S*)p.out + tok * (int64_t)D;
+      // rms-norm backward from the pre-norm output x: inv*g - x*inv^3*mean(g*x)
+      float x[CB][E];
+      const S* xp = (const S*)p.out_prenorm + tok * (int64_t)D;
       float dot = 0.f;
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
-        if (ok[c]) load_vec<DT, E>(yp + eoff[c], y[c]);
+        if (ok[c]) load_vec<DT, E>(xp + eoff[c], x[c]);
         else
 #pragma unroll
-          for (int e = 0; e < E; ++e) y[c][e] = 0.f;
+          for (int e = 0; e < E; ++e) x[c][e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) dot += g[c][e] * y[c][e];
+        for (int e = 0; e < E; ++e) dot += g[c][e] * x[c][e];
       }
       dot = wave_sum(dot);
       if (wpt > 1) {
         if (lane == 0) s_red[wave] = dot;
-        __syncthreads();
+        team_sync(wpt);
         dot = 0.f;
         for (int w = 0; w < wpt; ++w) dot += s_red[w];
       }
       const float inv = bp.saved_inv[tok];
-      const float md = dot / (float)D;
+      const float k3 = inv * inv * inv * (dot / (float)D);
 #pragma unroll
       for (int c = 0; c < CB; ++c)
 #pragma unroll
-        for (int e = 0; e < E; ++e) g[c][e] = ok[c] ? DT::rnd(inv * (g[c][e] - y[c][e] * md)) : 0.f;
+        for (int e = 0; e < E; ++e) g[c][e] = ok[c] ? DT::rnd(inv * g[c][e] - x[c][e] * k3) : 0.f;
     }
-    __syncthreads();
+    team_sync(wpt);
 
     // ---- B: stream the value rows: dW partials and dv = w * g
     for (int s0 = 0; s0 < N; s0 += kSrcGroup) {
@@ -347,20 +376,20 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
         }
       }
     }
-    __syncthreads();
+    team_sync(wpt);
 
     // ---- C: dW per (head, source)
-    for (int pi = tid; pi < HN; pi += blockDim.x) {
+    for (int pi = tid; pi < HN; pi += team_threads) {
       const int h = pi / N, s = pi - h * N;
       const float* sp = s_part + s * p.ncols * gpc + h * cph;
       float dw = 0.f;
       for (int j = 0; j < cph; ++j) dw += sp[j];
       s_dw[pi] = DT::rnd(dw);
     }
-    __syncthreads();
+    team_sync(wpt);
 
     // ---- D: softmax backward, key gradient, normalised keys for dq
-    for (int pi = tid; pi < HN; pi += blockDim.x) {
+    for (int pi = tid; pi < HN; pi += team_threads) {
       const int h = pi / N, s = pi - h * N;
       float dot = 0.f;
       for (int t = 0; t < N; ++t) dot += s_p[h * N + t] * s_dw[h * N + t];
@@ -392,10 +421,10 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
         DT::store1(dkp + j, dk);
       }
     }
-    __syncthreads();
+    team_sync(wpt);
 
     // ---- E: query gradient (per token or accumulated), bias accumulation
-    for (int j = tid; j < R; j += blockDim.x) {
+    for (int j = tid; j < R; j += team_threads) {
       const int h = j / rh;
       float a = 0.f;
       for (int s = 0; s < N; ++s) a += s_ge[h * N + s] * s_kh[s * R + j];
@@ -408,15 +437,15 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
       }
     }
     if (bp.part_bias >= 0) {
-      for (int s = tid; s < N; s += blockDim.x) {
+      for (int s = tid; s < N; s += team_threads) {
         float b = 0.f;
         for (int h = 0; h < H; ++h) b += s_dl[h * N + s];
         s_acc[bp.part_bias + s] += b;
       }
     }
     if (p.q_dyn && p.gate) {
-      __syncthreads();
-      for (int h = tid; h < H; h += blockDim.x) {
+      team_sync(wpt);
+      for (int h = tid; h < H; h += team_threads) {
         float c = 0.f;
         for (int j = 0; j < rh; ++j) c += s_dq[h * rh + j];
         const S* gptr = (const S*)p.gate + (p.gate_per_token ? tok * H : 0) + h;
@@ -431,11 +460,18 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
         }
       }
     }
-    __syncthreads();
+    team_sync(wpt);
   }
 
-  if (bp.partials)
-    for (int i = tid; i < bp.n_part; i += blockDim.x) bp.partials[(int64_t)blockIdx.x * bp.n_part + i] = s_acc[i];
+  // fold the teams' accumulators in team order into this workgroup's partials
+  __syncthreads();
+  if (bp.partials) {
+    for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
+      float a = 0.f;
+      for (int t = 0; t < teams; ++t) a += smem[t * team_floats + 5 * HN + N * p.ncols * gpc + N * R + R + i];
+      bp.partials[(int64_t)blockIdx.x * bp.n_part + i] = a;
+    }
+  }
 }
 
 // ============================================================== launchers
@@ -446,8 +482,8 @@ static hipError_t launch_lr_fwd_t(const ReadParams& p, int wpt, int grid, size_t
 }
 
 template <class DT, int E, int CB>
-static hipError_t launch_lr_bwd_t(const ReadBwdParams& p, int wpt, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((lr_bwd_kernel<DT, E, CB>), dim3(grid), dim3(wpt * kWave), lds, st, p);
+static hipError_t launch_lr_bwd_t(const ReadBwdParams& p, int threads, int grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((lr_bwd_kernel<DT, E, CB>), dim3(grid), dim3(threads), lds, st, p);
   return hipGetLastError();
 }
 
@@ -459,8 +495,9 @@ static hipError_t lr_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st
 
 template <class DT>
 static hipError_t lr_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  if (L.vec) return launch_lr_bwd_t<DT, 16 / sizeof(typename DT::S), 2>(p, L.wpt, L.grid, L.lds, st);
-  return launch_lr_bwd_t<DT, 1, 4>(p, L.wpt, L.grid, L.lds, st);
+  const int threads = L.wpt * kWave * L.teams;
+  if (L.vec) return launch_lr_bwd_t<DT, 16 / sizeof(typename DT::S), 2>(p, threads, L.grid, L.lds, st);
+  return launch_lr_bwd_t<DT, 1, 4>(p, threads, L.grid, L.lds, st);
 }
 
 hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {

@@ -26,12 +26,14 @@ struct ReadParams {
   const void* gate;      // [H] or [n_tok, H]
   const float* bias;     // [N]
   void* out;             // [n_tok, D]
+  void* out_prenorm;     // [n_tok, D] read before the output norm (forward write / backward read)
   float* weights;        // [n_tok, H, N]
   float* out_inv_rms;    // [n_tok]
   int64_t n_tok;
   int64_t q_dyn_stride;
   int32_t n_src, D, H, R, rh, dh;
   int32_t ncols;         // vector columns per row: ceil(D / (64*E))
+  int32_t wpt;           // waves per token
   int32_t key_norm, norm_out, mode;
   int32_t gate_per_token, gate_act;
   int32_t key_vec;       // keys / per-token queries allow 16-byte loads

@@ -44,8 +44,8 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 1
-    rc = lib.attnres_read_forward(None, None, None, None, None)
+    assert lib.attnres_abi_version() == 2
+    rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()
 
@@ -119,7 +119,7 @@ def test_host_validation_rejects_bad_descriptions_without_launching():
         d.n_src = n_src
         if "dtype" in kw:
             d.dtype = kw["dtype"]
-        rc = lib.attnres_read_forward(ctypes.byref(d), ctypes.c_void_p(0x4000), None, None, None)
+        rc = lib.attnres_read_forward(ctypes.byref(d), ctypes.c_void_p(0x4000), None, None, None, None)
         assert rc == code, (kw, rc, lib.attnres_last_error())
         assert msg in lib.attnres_last_error(), lib.attnres_last_error()
 

@@ -298,7 +298,7 @@ def test_weights_sum_to_one_and_match_oracle():
     q = randn(g, (Hh, R // Hh), torch.bfloat16, 0.5)
     vd, kd = [x.to(DEV) for x in vals], [x.to(DEV) for x in keys]
     desc = H.Desc(vd, kd, q.to(DEV), None, None, None, Hh, 0.25, True, False, H.MODE_SOFTMAX, 0, False)
-    out, w, _ = H.forward(desc, vd[0].device, torch.bfloat16, True, False)
+    out, w, _, _ = H.forward(desc, vd[0].device, torch.bfloat16, True, False, True)
     torch.cuda.synchronize()
     sums = w.double().sum(-1)
     assert float((sums - 1).abs().max()) <= 1e-6
