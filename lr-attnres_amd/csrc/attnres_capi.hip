@@ -200,6 +200,43 @@ PartLayout part_layout(const attnres_read_desc* d, bool want_q, bool want_gate, 
 
 int64_t bwd_groups(int64_t n_tok) { return n_tok < kMaxBwdGroups ? n_tok : kMaxBwdGroups; }
 
+// LR fast path: one wave per (token, head-aligned column group).  Returns false
+// when the shape is outside what the fast kernels support.
+struct FastPlan {
+  int cb, nb, rhc, n_items, nh, kch;
+};
+
+bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, FastPlan* f) {
+  if (!pl.lr || !pl.vec || !pl.key_vec) return false;
+  if (backward && d->gate) return false;
+  const int es = elem_size(d->dtype);
+  const int E = 16 / es;
+  const int colw = kWaveSize * E;
+  const int dh = d->dim / d->heads, rh = d->rank / d->heads;
+  if (dh <= colw) {
+    if (colw % dh) return false;
+    f->cb = 1;
+    f->nh = colw / dh;
+  } else if (dh == 2 * colw) {
+    f->cb = 2;
+    f->nh = 1;
+  } else {
+    return false;
+  }
+  if (f->nh > d->heads) f->nh = d->heads;
+  f->n_items = (d->dim + f->cb * colw - 1) / (f->cb * colw);
+  if (d->normalize_output && f->n_items != 1) return false;
+  const int N = d->n_src;
+  if (N > (f->cb == 2 ? 16 : 32)) return false;
+  f->nb = N <= 8 ? 8 : N <= 16 ? 16 : 32;
+  if (N * f->nh > 64 || f->nh * rh > 64) return false;
+  if ((rh * es) % 16) return false;
+  f->kch = rh * es / 16;
+  if (f->kch > 8) return false;
+  f->rhc = f->kch <= 2 ? 2 : 8;
+  return true;
+}
+
 // token teams per LR-backward workgroup: four independent one-wave teams when a
 // token fits one wave, else one team of wpt waves
 int lr_bwd_teams(const Plan& pl) { return pl.wpt == 1 ? 4 : 1; }
@@ -257,9 +294,24 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
     L.lds = 32 * sizeof(float);
     err = launch_average_forward(d->dtype, p, L, st);
   } else if (pl.lr) {
-    L.lds = (2 * (size_t)d->heads * d->n_src + 32) * sizeof(float);
-    if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LDS need %zu bytes", L.lds);
-    err = launch_lr_forward(d->dtype, p, L, st);
+    FastPlan f;
+    if (lr_fast_plan(d, pl, false, &f)) {
+      const int64_t streams = d->n_tok < 16384 / f.n_items ? d->n_tok : 16384 / f.n_items;
+      p.n_items = f.n_items;
+      p.nh = f.nh;
+      p.kch = f.kch;
+      p.streams = (int32_t)(streams > 0 ? streams : 1);
+      L.wpt = f.cb;
+      L.nmax = f.nb;
+      L.teams = f.rhc;
+      L.grid = (int)((f.n_items * (int64_t)p.streams + 3) / 4);
+      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 128) * sizeof(float);
+      err = launch_lr_fast_forward(d->dtype, p, L, st);
+    } else {
+      L.lds = (2 * (size_t)d->heads * d->n_src + 32) * sizeof(float);
+      if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LDS need %zu bytes", L.lds);
+      err = launch_lr_forward(d->dtype, p, L, st);
+    }
   } else {
     L.lds = (pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : (size_t)d->n_src + 32) * sizeof(float);
     err = launch_base_forward(d->dtype, p, L, st);
@@ -353,10 +405,33 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     L.lds = 32 * sizeof(float);
     err = launch_average_backward(d->dtype, bp, L, st);
   } else if (lr) {
-    L.lds = lr_bwd_lds(d, pl, PL.n_part);
-    if (L.lds > lds_limit())
-      return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS (limit %zu)", L.lds, lds_limit());
-    err = launch_lr_backward(d->dtype, bp, L, st);
+    FastPlan f;
+    int64_t streams = 0;
+    if (lr_fast_plan(d, pl, true, &f)) {
+      // at most `groups` workgroups of four waves (the workspace rows)
+      streams = 4 * groups / f.n_items;
+      if (streams > d->n_tok) streams = d->n_tok;
+    }
+    if (streams > 0) {
+      bp.f.n_items = f.n_items;
+      bp.f.nh = f.nh;
+      bp.f.kch = f.kch;
+      bp.f.streams = (int32_t)streams;
+      L.wpt = f.cb;
+      L.nmax = f.nb;
+      L.teams = f.rhc;
+      L.grid = (int)((f.n_items * streams + 3) / 4);
+      L.lds = lr_fast_table_bytes() +
+              ((size_t)d->rank + 4 * (192 + (size_t)d->n_src * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *
+                  sizeof(float);
+      if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS", L.lds);
+      err = launch_lr_fast_backward(d->dtype, bp, L, st);
+    } else {
+      L.lds = lr_bwd_lds(d, pl, PL.n_part);
+      if (L.lds > lds_limit())
+        return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS (limit %zu)", L.lds, lds_limit());
+      err = launch_lr_backward(d->dtype, bp, L, st);
+    }
   } else {
     size_t fl = pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : 2 * (size_t)d->n_src + 32;
     if ((size_t)L.teams * PL.n_part > fl) fl = (size_t)L.teams * PL.n_part;

@@ -163,6 +163,23 @@ __device__ __forceinline__ float group_sum(float x, int width) {
   return x;
 }
 
+// ---------------------------------------------------------------- addressing
+// Pointers rebuilt from integers (e.g. tables kept in LDS) are generic to the
+// compiler, which then emits flat accesses; casting through the global address
+// space keeps them on the global_load / global_store path.
+template <class S>
+__device__ __forceinline__ S* global_ptr(uint64_t a) {
+  return (S*)(__attribute__((address_space(1))) S*)(a);
+}
+
+// a wave-uniform 64-bit value, moved to scalar registers
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ int uniform_i32(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
 __device__ __forceinline__ float gate_value(float g, int act) {
   return act == 2 ? 1.0f / (1.0f + expf(-g)) : g;
 }

@@ -1,0 +1,586 @@
+// LR AttnRes read, fast path: one wave per (token, head-aligned column group).
+//
+// A "column" is 64 lanes x one 16-byte vector (512 bf16/fp16 or 256 fp32
+// elements).  When the head width divides the column width (or spans exactly
+// two columns), every wave can own whole heads of a token, so a wave computes
+// everything for its heads -- logits, softmax, mix, and in the backward dW,
+// the softmax and key-norm chains, dk and the query gradient -- with no
+// cross-wave synchronisation and no duplicated work.  Work items are
+// (token, item) with item in [0, n_items); a wave keeps one item index and
+// walks tokens with a fixed stride, so its heads (and static query) never
+// change and its query-gradient accumulators live in registers.
+//
+// Memory order: every load a token needs (keys, per-token query, upstream
+// gradient, all N value vectors) is issued first; stores go last.  On CDNA the
+// vector-memory counter also counts stores, so a load issued after a store
+// cannot be waited on without draining that store -- keeping stores at the end
+// removes those round trips from the token's critical path.
+//
+// Addressing: the per-source pointer / stride tables are copied to LDS once
+// and read back as wave-uniform scalars inside the token loop, so row
+// addresses are scalar (SGPR base + one VGPR lane offset) and the tables do
+// not pin dozens of SGPRs for the whole kernel.
+//
+// Requirements (checked on the host, else the general kernels run):
+// 16-byte vector path, N <= NB (8/16/32), N * heads_per_item <= 64 pairs,
+// key slice of a head = kch 16-byte chunks with kch <= RHC, heads_per_item *
+// (R/H) <= 64, no gate in the backward, output norm only when one item covers
+// the whole row.
+#include "attnres_device.h"
+#include "attnres_params.h"
+#include "attnres_launch.h"
+
+namespace attnres {
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kFastWaves = 4;  // waves per workgroup (independent token streams)
+
+// per-source tables in LDS
+struct SrcTab {
+  uint64_t vptr[kMaxSources];
+  uint64_t kptr[kMaxSources];
+  uint64_t dvptr[kMaxSources];
+  uint64_t dkptr[kMaxSources];
+  int32_t vstr[kMaxSources];
+  int32_t kstr[kMaxSources];
+};
+constexpr int kSrcTabFloats = (int)(sizeof(SrcTab) / sizeof(float));
+
+template <class DT, int RHC>
+struct KeySlice {
+  static constexpr int KV = 16 / (int)sizeof(typename DT::S);
+  Raw<DT, KV> r[RHC];
+};
+
+// query element j of the pair's head: static part from LDS, per-token part
+// (optionally gated) from registers, composed and rounded like the reference
+template <class DT, int RHC>
+__device__ __forceinline__ float fast_q(const float* s_qh, const KeySlice<DT, RHC>& qd, bool dyn, float gf,
+                                        bool has_static, int j) {
+  constexpr int KV = KeySlice<DT, RHC>::KV;
+  float q = has_static ? s_qh[j] : 0.f;
+  if (dyn) {
+    float t[KV];
+    unpack<DT, KV>(qd.r[j / KV], t);
+    q = DT::rnd(q + gf * t[j % KV]);
+  }
+  return q;
+}
+
+// byte address of source s's row for token tok (the table has kMaxSources
+// slots, so reading a slot past n_src is harmless; its value is never used)
+template <class S>
+__device__ __forceinline__ uint64_t row_base(const SrcTab* tab, int s, int64_t tok) {
+  return tab->vptr[s] + (uint64_t)(tok * (int64_t)tab->vstr[s]) * sizeof(S);
+}
+
+template <class DT, int RHC>
+__device__ __forceinline__ float key_inv_rms(const KeySlice<DT, RHC>& kr, int kch, int rh, float eps) {
+  constexpr int KV = KeySlice<DT, RHC>::KV;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < RHC; ++j) {
+    if (j < kch) {
+      float k[KV];
+      unpack<DT, KV>(kr.r[j], k);
+#pragma unroll
+      for (int i = 0; i < KV; ++i) ss += k[i] * k[i];
+    }
+  }
+  return 1.0f / sqrtf(ss / (float)rh + eps);
+}
+
+// ============================================================== forward
+template <class DT, int CB, int NB, int RHC>
+__global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
+  using S = typename DT::S;
+  constexpr int E = 16 / (int)sizeof(S);
+  constexpr int KV = E;
+  constexpr int colw = kWave * E;
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wslot = uniform_i32(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
+  // LDS: source tables | static query [R] | per wave: logits [64], rounded weights [64]
+  SrcTab* tab = (SrcTab*)smem;
+  float* s_q = smem + kSrcTabFloats;
+  float* s_l = s_q + R + wslot * (2 * 64);
+  float* s_w = s_l + 64;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    tab->vptr[i] = (uint64_t)p.val[i];
+    tab->vstr[i] = p.vstride[i];
+    tab->kptr[i] = (uint64_t)p.key[i];
+    tab->kstr[i] = p.kstride[i];
+  }
+  if (p.q_static)
+    for (int i = threadIdx.x; i < R; i += blockDim.x) s_q[i] = DT::load1((const S*)p.q_static + i);
+  __syncthreads();
+
+  const int wv = blockIdx.x * nwaves + wslot;
+  const int item = wv % p.n_items;
+  // waves past n_items * streams (the last workgroup's spare slots) stay idle
+  const int64_t t0 = wv < p.n_items * p.streams ? wv / p.n_items : p.n_tok;
+  const int h0 = (item * CB * colw) / dh;
+  const int nh = min(p.nh, H - h0);
+  const int npairs = N * nh;
+  const bool has_pair = lane < npairs;
+  const int ph = h0 + (has_pair ? lane / N : 0);
+  const int ps = has_pair ? lane % N : 0;
+  const int kch = p.kch;
+  const bool dyn = p.q_dyn != nullptr;
+  const bool has_static = p.q_static != nullptr;
+  const S* kbase = global_ptr<const S>(tab->kptr[ps]) + ph * rh;
+  const int64_t kstr = tab->kstr[ps];
+
+  // lanes past the row end load from the row start (valid memory) and store nothing
+  int eoff[CB], hd[CB];
+  bool ok[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    const int e = (item * CB + c) * colw + lane * E;
+    ok[c] = e < D;
+    eoff[c] = ok[c] ? e : 0;
+    hd[c] = ok[c] ? e / dh - h0 : 0;
+  }
+
+  for (int64_t tok = t0; tok < p.n_tok; tok += p.streams) {
+    // ---- issue every load of the token: keys (and per-token query), values
+    // (no branches here: every lane loads valid addresses -- lanes without a
+    // pair read pair 0's slice, slots past kch / N re-read the last chunk /
+    // row -- so the loads issue back to back)
+    KeySlice<DT, RHC> kr, qr;
+    S graw = 0;
+    {
+      const S* kp = kbase + tok * kstr;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(kp + min(j, kch - 1) * KV, kr.r[j]);
+    }
+    if (dyn) {
+      const S* qp = global_ptr<const S>((uint64_t)p.q_dyn) + tok * p.q_dyn_stride + ph * rh;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(qp + min(j, kch - 1) * KV, qr.r[j]);
+      if (p.gate) graw = *(global_ptr<const S>((uint64_t)p.gate) + (p.gate_per_token ? tok * H : 0) + ph);
+    }
+    Raw<DT, E> vr[NB][CB];
+    {
+      uint64_t base[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) base[s] = row_base<S>(tab, min(s, N - 1), tok);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+#pragma unroll
+        for (int c = 0; c < CB; ++c) load_raw<DT, E>(vp + eoff[c], vr[s][c]);
+      }
+    }
+
+    // ---- logits of this wave's (head, source) pairs
+    float pw = 0.f;
+    if (has_pair) {
+      const float gf = (dyn && p.gate) ? gate_value(DT::load1(&graw), p.gate_act) : 1.f;
+      const float inv = p.key_norm ? key_inv_rms<DT, RHC>(kr, kch, rh, p.eps) : 1.f;
+      const float* s_qh = s_q + ph * rh;
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) {
+        if (j < kch) {
+          float k[KV];
+          unpack<DT, KV>(kr.r[j], k);
+#pragma unroll
+          for (int i = 0; i < KV; ++i) {
+            const float kh = p.key_norm ? DT::rnd(k[i] * inv) : k[i];
+            dot += kh * fast_q<DT, RHC>(s_qh, qr, dyn, gf, has_static, j * KV + i);
+          }
+        }
+      }
+      float logit = DT::rnd(DT::rnd(dot) * p.scale);
+      if (p.bias) logit += p.bias[ps];
+      s_l[lane] = logit;
+    }
+    wave_sync();
+    if (has_pair) {
+      const float* lg = s_l + (lane / N) * N;
+      float m = lg[0];
+      for (int s = 1; s < N; ++s) m = fmaxf(m, lg[s]);
+      float den = 0.f;
+      for (int s = 0; s < N; ++s) den += expf(lg[s] - m);
+      pw = expf(s_l[lane] - m) / den;
+      s_w[lane] = DT::rnd(pw);
+    }
+    wave_sync();
+
+    // ---- mix
+    float acc[CB][E];
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[c][e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      if (s < N) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+          float v[E];
+          unpack<DT, E>(vr[s][c], v);
+          const float w = s_w[hd[c] * N + s];
+#pragma unroll
+          for (int e = 0; e < E; ++e) acc[c][e] += w * v[e];
+        }
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        acc[c][e] = DT::rnd(acc[c][e]);
+        if (ok[c]) ss += acc[c][e] * acc[c][e];
+      }
+
+    // ---- stores
+    if (p.norm_out) {  // one item covers the whole row here
+      if (p.out_prenorm) {
+        S* xp = global_ptr<S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+          if (ok[c]) store_vec<DT, E>(xp + eoff[c], acc[c]);
+      }
+      const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + p.eps);
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e] * inv);
+      if (lane == 0 && p.out_inv_rms) p.out_inv_rms[tok] = inv;
+    }
+    S* op = global_ptr<S>((uint64_t)p.out) + tok * (int64_t)D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+      if (ok[c]) store_vec<DT, E>(op + eoff[c], acc[c]);
+    if (has_pair && p.weights) p.weights[(tok * H + ph) * N + ps] = pw;
+  }
+}
+
+// ============================================================== backward
+template <class DT, int CB, int NB, int RHC>
+__global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp) {
+  using S = typename DT::S;
+  constexpr int E = 16 / (int)sizeof(S);
+  constexpr int KV = E;
+  constexpr int colw = kWave * E;
+  const ReadParams& p = bp.f;
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wslot = uniform_i32(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
+  // LDS: source tables | static query [R] | per wave: p [64], dW [64], dl [64],
+  // contributions [N*nh][rh] | fold [nwaves][n_part]
+  SrcTab* tab = (SrcTab*)smem;
+  float* s_q = smem + kSrcTabFloats;
+  const int wave_floats = 3 * 64 + N * p.nh * rh;
+  float* s_p = s_q + R + wslot * wave_floats;
+  float* s_dw = s_p + 64;
+  float* s_dl = s_dw + 64;
+  float* s_c = s_dl + 64;  // [npairs][rh] = ge * khat
+  float* s_fold = s_q + R + nwaves * wave_floats;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    tab->vptr[i] = (uint64_t)p.val[i];
+    tab->vstr[i] = p.vstride[i];
+    tab->kptr[i] = (uint64_t)p.key[i];
+    tab->kstr[i] = p.kstride[i];
+    tab->dvptr[i] = (uint64_t)bp.dval[i];
+    tab->dkptr[i] = (uint64_t)bp.dkey[i];
+  }
+  if (p.q_static)
+    for (int i = threadIdx.x; i < R; i += blockDim.x) s_q[i] = DT::load1((const S*)p.q_static + i);
+  __syncthreads();
+
+  const int wv = blockIdx.x * nwaves + wslot;
+  const int item = wv % p.n_items;
+  const int64_t t0 = wv < p.n_items * p.streams ? wv / p.n_items : p.n_tok;
+  const int h0 = (item * CB * colw) / dh;
+  const int nh = min(p.nh, H - h0);
+  const int npairs = N * nh;
+  const bool has_pair = lane < npairs;
+  const int ph = h0 + (has_pair ? lane / N : 0);
+  const int ps = has_pair ? lane % N : 0;
+  const int kch = p.kch;
+  const bool dyn = p.q_dyn != nullptr;
+  const bool has_static = p.q_static != nullptr;
+  // query-gradient owner lanes: (head h0 + lane / rh, element lane % rh)
+  const int nq = nh * rh;
+  const bool q_owner = lane < nq;
+  const int qh = lane / rh, qj = lane - (lane / rh) * rh;
+  // dW lane groups: lanes of one head inside a column
+  const int gl = CB == 2 ? kWave : (dh / E < kWave ? dh / E : kWave);
+  const S* kbase = global_ptr<const S>(tab->kptr[ps]) + ph * rh;
+  S* dkbase = global_ptr<S>(tab->dkptr[ps]) + ph * rh;
+  const int64_t kstr = tab->kstr[ps];
+
+  int eoff[CB], hd[CB];
+  bool ok[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    const int e = (item * CB + c) * colw + lane * E;
+    ok[c] = e < D;
+    eoff[c] = ok[c] ? e : 0;
+    hd[c] = ok[c] ? e / dh - h0 : 0;
+  }
+
+  float qacc = 0.f;  // static-query gradient of (h0 + qh, qj), over this wave's tokens
+  float bacc = 0.f;  // bias gradient of source `lane`
+
+  for (int64_t tok = t0; tok < p.n_tok; tok += p.streams) {
+    // ---- issue every load of the token
+    // (branch-free: see the forward)
+    KeySlice<DT, RHC> kr, qr;
+    float pr = bp.saved_w[(tok * H + ph) * N + ps];
+    {
+      const S* kp = kbase + tok * kstr;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(kp + min(j, kch - 1) * KV, kr.r[j]);
+    }
+    if (dyn) {
+      const S* qp = global_ptr<const S>((uint64_t)p.q_dyn) + tok * p.q_dyn_stride + ph * rh;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(qp + min(j, kch - 1) * KV, qr.r[j]);
+    }
+    Raw<DT, E> gr[CB];
+    const S* gp = global_ptr<const S>((uint64_t)bp.gout) + tok * (int64_t)D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) load_raw<DT, E>(gp + eoff[c], gr[c]);
+    Raw<DT, E> xr[CB];
+    if (p.norm_out) {
+      const S* xp = global_ptr<const S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) load_raw<DT, E>(xp + eoff[c], xr[c]);
+    }
+    Raw<DT, E> vr[NB][CB];
+    {
+      uint64_t base[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) base[s] = row_base<S>(tab, min(s, N - 1), tok);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+#pragma unroll
+        for (int c = 0; c < CB; ++c) load_raw<DT, E>(vp + eoff[c], vr[s][c]);
+      }
+    }
+    float g[CB][E];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      unpack<DT, E>(gr[c], g[c]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) g[c][e] = ok[c] ? g[c][e] : 0.f;
+    }
+
+    // ---- upstream gradient through the output norm (item = whole row)
+    if (p.norm_out) {
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        float x[E];
+        unpack<DT, E>(xr[c], x);
+#pragma unroll
+        for (int e = 0; e < E; ++e) dot += g[c][e] * x[e];
+      }
+      const float inv = bp.saved_inv[tok];
+      const float k3 = inv * inv * inv * (wave_sum(dot) / (float)D);
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        float x[E];
+        unpack<DT, E>(xr[c], x);
+#pragma unroll
+        for (int e = 0; e < E; ++e) g[c][e] = ok[c] ? DT::rnd(inv * g[c][e] - x[e] * k3) : 0.f;
+      }
+    }
+
+    if (has_pair) s_p[lane] = pr;
+
+    // ---- dW = <g, v> per (head, source), reduced over the head's lanes
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      if (s < N) {
+        float part[CB];
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+          float v[E];
+          unpack<DT, E>(vr[s][c], v);
+          part[c] = 0.f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) part[c] += g[c][e] * v[e];
+        }
+        if (CB == 2) {
+          const float t = wave_sum(part[0] + part[1]);  // one head spans both columns
+          if (lane == 0) s_dw[s] = t;
+        } else {
+          const float t = group_sum(part[0], gl);
+          if (ok[0] && (lane & (gl - 1)) == 0) s_dw[hd[0] * N + s] = t;
+        }
+      }
+    }
+    wave_sync();
+
+    // ---- per pair: softmax backward, key-norm backward state, contributions to dq
+    float ge = 0.f, kinv = 1.f, mr = 0.f;
+    if (has_pair) {
+      const int hr = lane / N;
+      float dot = 0.f;
+      for (int t = 0; t < N; ++t) dot += s_p[hr * N + t] * DT::rnd(s_dw[hr * N + t]);
+      const float dl = pr * (DT::rnd(s_dw[lane]) - dot);
+      s_dl[lane] = dl;
+      ge = DT::rnd(DT::rnd(dl) * p.scale);
+      if (p.key_norm) kinv = key_inv_rms<DT, RHC>(kr, kch, rh, p.eps);
+      const float* s_qh = s_q + ph * rh;
+      float m = 0.f;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) {
+        if (j < kch) {
+          float k[KV];
+          unpack<DT, KV>(kr.r[j], k);
+#pragma unroll
+          for (int i = 0; i < KV; ++i) {
+            const int jj = j * KV + i;
+            const float kh = p.key_norm ? DT::rnd(k[i] * kinv) : k[i];
+            s_c[lane * rh + jj] = ge * kh;
+            if (p.key_norm) {
+              const float dkh = DT::rnd(ge * fast_q<DT, RHC>(s_qh, qr, dyn, 1.f, has_static, jj));
+              m += dkh * (k[i] * kinv);
+            }
+          }
+        }
+      }
+      mr = m / (float)rh;
+    }
+    wave_sync();
+
+    // ---- query gradient and bias accumulation (owner lanes)
+    float dqt = 0.f;
+    if (q_owner) {
+      for (int s = 0; s < N; ++s) dqt += s_c[(qh * N + s) * rh + qj];
+      if (dyn) dqt = DT::rnd(dqt);
+      qacc += dqt;
+    }
+    if (p.bias && lane < N) {
+      float b = 0.f;
+      for (int h = 0; h < nh; ++h) b += s_dl[h * N + lane];
+      bacc += b;
+    }
+
+    // ---- stores: dv = w * g, dk, per-token dq
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      if (s < N) {
+        S* dvp = global_ptr<S>(uniform_u64(tab->dvptr[s])) + tok * (int64_t)D;
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+          if (ok[c]) {
+            const float w = DT::rnd(s_p[hd[c] * N + s]);
+            float dv[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) dv[e] = DT::rnd(w * g[c][e]);
+            store_vec<DT, E>(dvp + eoff[c], dv);
+          }
+        }
+      }
+    }
+    if (has_pair) {
+      // dk = inv * (dkhat - khat_f32 * <dkhat, khat_f32>/rh) (rms-norm backward), dkhat = rnd(ge * q)
+      const float* s_qh = s_q + ph * rh;
+      S* dkp = dkbase + tok * (int64_t)R;
+#pragma unroll
+      for (int j = 0; j < RHC; ++j) {
+        if (j < kch) {
+          float k[KV], t[KV];
+          unpack<DT, KV>(kr.r[j], k);
+#pragma unroll
+          for (int i = 0; i < KV; ++i) {
+            const float dkh = DT::rnd(ge * fast_q<DT, RHC>(s_qh, qr, dyn, 1.f, has_static, j * KV + i));
+            t[i] = p.key_norm ? DT::rnd(kinv * (dkh - k[i] * kinv * mr)) : dkh;
+          }
+          store_vec<DT, KV>(dkp + j * KV, t);
+        }
+      }
+    }
+    if (dyn && q_owner && bp.dq_dyn)
+      DT::store1(global_ptr<S>((uint64_t)bp.dq_dyn) + tok * (int64_t)R + h0 * rh + lane, dqt);
+    wave_sync();  // this token's LDS is read before the next token writes it
+  }
+
+  // ---- fold the waves' accumulators into this workgroup's partial row
+  if (!bp.partials) return;
+  for (int i = threadIdx.x; i < nwaves * bp.n_part; i += blockDim.x) s_fold[i] = 0.f;
+  __syncthreads();
+  float* fold = s_fold + wslot * bp.n_part;
+  if (bp.part_q >= 0 && q_owner) fold[bp.part_q + h0 * rh + lane] = qacc;
+  if (bp.part_bias >= 0 && lane < N) fold[bp.part_bias + lane] = bacc;
+  __syncthreads();
+  for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
+    float a = 0.f;
+    for (int w = 0; w < nwaves; ++w) a += s_fold[w * bp.n_part + i];
+    bp.partials[(int64_t)blockIdx.x * bp.n_part + i] = a;
+  }
+}
+
+// ============================================================== launchers
+template <class DT, int CB, int NB, int RHC>
+static hipError_t fast_fwd_t(const ReadParams& p, const Launch& L, hipStream_t st) {
+  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st, p);
+  return hipGetLastError();
+}
+template <class DT, int CB, int NB, int RHC>
+static hipError_t fast_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
+  hipLaunchKernelGGL((lr_bwd_fast_kernel<DT, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st, p);
+  return hipGetLastError();
+}
+
+// L.nmax selects NB (8/16/32), L.wpt carries CB (1/2), L.teams carries RHC (2/8)
+#define ATTNRES_FAST_SWITCH(fn, P)                   \
+  switch (L.wpt * 1000 + L.nmax * 10 + L.teams) {    \
+    case 1082: return fn<DT, 1, 8, 2>(P, L, st);     \
+    case 1162: return fn<DT, 1, 16, 2>(P, L, st);    \
+    case 1322: return fn<DT, 1, 32, 2>(P, L, st);    \
+    case 1088: return fn<DT, 1, 8, 8>(P, L, st);     \
+    case 1168: return fn<DT, 1, 16, 8>(P, L, st);    \
+    case 1328: return fn<DT, 1, 32, 8>(P, L, st);    \
+    case 2082: return fn<DT, 2, 8, 2>(P, L, st);     \
+    case 2162: return fn<DT, 2, 16, 2>(P, L, st);    \
+    case 2088: return fn<DT, 2, 8, 8>(P, L, st);     \
+    case 2168: return fn<DT, 2, 16, 8>(P, L, st);    \
+    default: return hipErrorInvalidValue;            \
+  }
+
+template <class DT>
+static hipError_t fast_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st) {
+  ATTNRES_FAST_SWITCH(fast_fwd_t, p)
+}
+template <class DT>
+static hipError_t fast_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
+  ATTNRES_FAST_SWITCH(fast_bwd_t, p)
+}
+
+size_t lr_fast_table_bytes() { return sizeof(SrcTab); }
+
+hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {
+  switch (dtype) {
+    case ATTNRES_DTYPE_F32: return fast_fwd_dt<F32>(p, L, st);
+    case ATTNRES_DTYPE_BF16: return fast_fwd_dt<BF16>(p, L, st);
+    default: return fast_fwd_dt<F16>(p, L, st);
+  }
+}
+hipError_t launch_lr_fast_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st) {
+  switch (dtype) {
+    case ATTNRES_DTYPE_F32: return fast_bwd_dt<F32>(p, L, st);
+    case ATTNRES_DTYPE_BF16: return fast_bwd_dt<BF16>(p, L, st);
+    default: return fast_bwd_dt<F16>(p, L, st);
+  }
+}
+
+}  // namespace attnres

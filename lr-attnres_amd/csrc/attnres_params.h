@@ -38,6 +38,10 @@ struct ReadParams {
   int32_t gate_per_token, gate_act;
   int32_t key_vec;       // keys / per-token queries allow 16-byte loads
   float scale, eps;
+  // head-aligned work items (LR fast path): a wave owns `item_cols` columns
+  // holding `nh` whole heads of one token; items per token = n_items; waves
+  // with the same item index walk the tokens with stride `streams`
+  int32_t n_items, nh, kch, streams;
 };
 
 struct ReadBwdParams {
