@@ -150,6 +150,8 @@ class Desc:
         v0 = values[0]
         B, T, D = v0.shape
         n = len(values)
+        # the descriptor holds raw device pointers: keep the tensors alive with it
+        self._tensors = (list(values), list(keys), query, query_dyn, gate, bias)
         self.n_src = n
         self.n_tok = B * T
         self.D = D

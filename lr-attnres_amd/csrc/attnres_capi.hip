@@ -2,6 +2,7 @@
 // launch geometry.  Declared in include/attnres_hip.h.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -203,21 +204,31 @@ int64_t bwd_groups(int64_t n_tok) { return n_tok < kMaxBwdGroups ? n_tok : kMaxB
 // LR fast path: one wave per (token, head-aligned column group).  Returns false
 // when the shape is outside what the fast kernels support.
 struct FastPlan {
-  int cb, nb, rhc, n_items, nh, kch;
+  int vb, cb, nb, rhc, n_items, nh, kch, np;
 };
+
+// value vector bytes of the fast kernels: 8-byte lane vectors make one-head
+// work items for heads of 64*4 bf16 elements (half the registers of 16-byte
+// vectors, so more waves in flight)
+int fast_vector_bytes(const attnres_read_desc* d) {
+  const char* env = getenv("ATTNRES_FAST_VB");
+  if (env && (atoi(env) == 8 || atoi(env) == 16)) return atoi(env);
+  return 16;
+}
 
 bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, FastPlan* f) {
   if (!pl.lr || !pl.vec || !pl.key_vec) return false;
   if (backward && d->gate) return false;
   const int es = elem_size(d->dtype);
-  const int E = 16 / es;
+  f->vb = fast_vector_bytes(d);
+  const int E = f->vb / es;
   const int colw = kWaveSize * E;
   const int dh = d->dim / d->heads, rh = d->rank / d->heads;
   if (dh <= colw) {
     if (colw % dh) return false;
     f->cb = 1;
     f->nh = colw / dh;
-  } else if (dh == 2 * colw) {
+  } else if (dh == 2 * colw && f->vb == 16) {
     f->cb = 2;
     f->nh = 1;
   } else {
@@ -229,11 +240,14 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   const int N = d->n_src;
   if (N > (f->cb == 2 ? 16 : 32)) return false;
   f->nb = N <= 8 ? 8 : N <= 16 ? 16 : 32;
-  if (N * f->nh > 64 || f->nh * rh > 64) return false;
+  f->np = 1;
+  while (f->np < N) f->np <<= 1;
+  if (f->np * f->nh > 64 || f->nh * rh > 64) return false;
   if ((rh * es) % 16) return false;
   f->kch = rh * es / 16;
   if (f->kch > 8) return false;
   f->rhc = f->kch <= 2 ? 2 : 8;
+  if (f->cb == 2 && f->rhc == 8 && f->nb == 16) return false;  // no register room
   return true;
 }
 
@@ -300,12 +314,14 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       p.n_items = f.n_items;
       p.nh = f.nh;
       p.kch = f.kch;
+      p.np = f.np;
       p.streams = (int32_t)(streams > 0 ? streams : 1);
+      L.vec = f.vb;
       L.wpt = f.cb;
       L.nmax = f.nb;
       L.teams = f.rhc;
       L.grid = (int)((f.n_items * (int64_t)p.streams + 3) / 4);
-      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 128) * sizeof(float);
+      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float);
       err = launch_lr_fast_forward(d->dtype, p, L, st);
     } else {
       L.lds = (2 * (size_t)d->heads * d->n_src + 32) * sizeof(float);
@@ -416,13 +432,15 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       bp.f.n_items = f.n_items;
       bp.f.nh = f.nh;
       bp.f.kch = f.kch;
+      bp.f.np = f.np;
       bp.f.streams = (int32_t)streams;
+      L.vec = f.vb;
       L.wpt = f.cb;
       L.nmax = f.nb;
       L.teams = f.rhc;
       L.grid = (int)((f.n_items * streams + 3) / 4);
       L.lds = lr_fast_table_bytes() +
-              ((size_t)d->rank + 4 * (192 + (size_t)d->n_src * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *
+              ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *
                   sizeof(float);
       if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS", L.lds);
       err = launch_lr_fast_backward(d->dtype, bp, L, st);

@@ -25,7 +25,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
-__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+// gfx950 converts to bf16 in hardware (v_cvt_pk_bf16_f32, round to nearest even)
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float round_bf16(float f) { return (float)(__bf16)f; }
+// two fp32 values -> one word of two bf16 (low element in the low half)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
@@ -125,6 +133,9 @@ __device__ __forceinline__ void store_vec(typename DT::S* __restrict__ p, const 
     if constexpr (E == 4) {
       u32x4 v = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
       *reinterpret_cast<u32x4*>(p) = v;
+    } else if constexpr (E == 2) {
+      u32x2 v = {__float_as_uint(x[0]), __float_as_uint(x[1])};
+      *reinterpret_cast<u32x2*>(p) = v;
     } else {
 #pragma unroll
       for (int i = 0; i < E; ++i) p[i] = x[i];
@@ -135,12 +146,31 @@ __device__ __forceinline__ void store_vec(typename DT::S* __restrict__ p, const 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         uint32_t lo, hi;
-        if constexpr (DT::kCode == 1) { lo = f32_to_bf16_bits(x[2 * i]); hi = f32_to_bf16_bits(x[2 * i + 1]); }
-        else { lo = f32_to_f16_bits(x[2 * i]); hi = f32_to_f16_bits(x[2 * i + 1]); }
-        w[i] = lo | (hi << 16);
+        if constexpr (DT::kCode == 1) {
+          w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+        } else {
+          lo = f32_to_f16_bits(x[2 * i]);
+          hi = f32_to_f16_bits(x[2 * i + 1]);
+          w[i] = lo | (hi << 16);
+        }
       }
       u32x4 v = {w[0], w[1], w[2], w[3]};
       *reinterpret_cast<u32x4*>(p) = v;
+    } else if constexpr (E == 4) {
+      uint32_t w[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        uint32_t lo, hi;
+        if constexpr (DT::kCode == 1) {
+          w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+        } else {
+          lo = f32_to_f16_bits(x[2 * i]);
+          hi = f32_to_f16_bits(x[2 * i + 1]);
+          w[i] = lo | (hi << 16);
+        }
+      }
+      u32x2 v = {w[0], w[1]};
+      *reinterpret_cast<u32x2*>(p) = v;
     } else {
 #pragma unroll
       for (int i = 0; i < E; ++i) DT::store1(p + i, x[i]);
@@ -160,6 +190,12 @@ __device__ __forceinline__ float wave_sum(float x) {
 // Butterfly all-reduce inside aligned groups of `width` lanes (power of two).
 __device__ __forceinline__ float group_sum(float x, int width) {
   for (int o = 1; o < width; o <<= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+// Butterfly max inside aligned groups of `width` lanes (power of two).
+__device__ __forceinline__ float group_max(float x, int width) {
+  for (int o = 1; o < width; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
   return x;
 }
 

@@ -96,22 +96,21 @@ __device__ __forceinline__ float key_inv_rms(const KeySlice<DT, RHC>& kr, int kc
 }
 
 // ============================================================== forward
-template <class DT, int CB, int NB, int RHC>
+template <class DT, int VB, int CB, int NB, int RHC>
 __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   using S = typename DT::S;
-  constexpr int E = 16 / (int)sizeof(S);
-  constexpr int KV = E;
+  constexpr int E = VB / (int)sizeof(S);        // value elements per lane vector
+  constexpr int KV = 16 / (int)sizeof(S);       // key elements per 16-byte chunk
   constexpr int colw = kWave * E;
   extern __shared__ float smem[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wslot = uniform_i32(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
-  // LDS: source tables | static query [R] | per wave: logits [64], rounded weights [64]
+  // LDS: source tables | static query [R] | per wave: rounded weights [64]
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
-  float* s_l = s_q + R + wslot * (2 * 64);
-  float* s_w = s_l + 64;
+  float* s_w = s_q + R + wslot * 64;
   for (int i = threadIdx.x; i < N; i += blockDim.x) {
     tab->vptr[i] = (uint64_t)p.val[i];
     tab->vstr[i] = p.vstride[i];
@@ -128,10 +127,13 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   const int64_t t0 = wv < p.n_items * p.streams ? wv / p.n_items : p.n_tok;
   const int h0 = (item * CB * colw) / dh;
   const int nh = min(p.nh, H - h0);
-  const int npairs = N * nh;
-  const bool has_pair = lane < npairs;
-  const int ph = h0 + (has_pair ? lane / N : 0);
-  const int ps = has_pair ? lane % N : 0;
+  // (head, source) pairs: lane = head_in_item * np + source, np = pow2 >= N,
+  // so per-head softmax reductions are butterflies inside np-lane groups
+  const int np = p.np;
+  const int lh = lane / np, lsrc = lane - (lane / np) * np;
+  const bool has_pair = lh < nh && lsrc < N;
+  const int ph = h0 + (lh < nh ? lh : 0);
+  const int ps = has_pair ? lsrc : 0;
   const int kch = p.kch;
   const bool dyn = p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
@@ -181,7 +183,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     }
 
     // ---- logits of this wave's (head, source) pairs
-    float pw = 0.f;
+    float logit = -INFINITY;
     if (has_pair) {
       const float gf = (dyn && p.gate) ? gate_value(DT::load1(&graw), p.gate_act) : 1.f;
       const float inv = p.key_norm ? key_inv_rms<DT, RHC>(kr, kch, rh, p.eps) : 1.f;
@@ -199,20 +201,14 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
           }
         }
       }
-      float logit = DT::rnd(DT::rnd(dot) * p.scale);
+      logit = DT::rnd(DT::rnd(dot) * p.scale);
       if (p.bias) logit += p.bias[ps];
-      s_l[lane] = logit;
     }
-    wave_sync();
-    if (has_pair) {
-      const float* lg = s_l + (lane / N) * N;
-      float m = lg[0];
-      for (int s = 1; s < N; ++s) m = fmaxf(m, lg[s]);
-      float den = 0.f;
-      for (int s = 0; s < N; ++s) den += expf(lg[s] - m);
-      pw = expf(s_l[lane] - m) / den;
-      s_w[lane] = DT::rnd(pw);
-    }
+    // softmax over each head's np-lane group (lanes without a pair carry -inf / 0)
+    const float lmax = group_max(logit, np);
+    const float ex = has_pair ? expf(logit - lmax) : 0.f;
+    const float pw = ex / group_sum(ex, np);
+    if (has_pair) s_w[lane] = DT::rnd(pw);
     wave_sync();
 
     // ---- mix
@@ -228,7 +224,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
         for (int c = 0; c < CB; ++c) {
           float v[E];
           unpack<DT, E>(vr[s][c], v);
-          const float w = s_w[hd[c] * N + s];
+          const float w = s_w[hd[c] * np + s];
 #pragma unroll
           for (int e = 0; e < E; ++e) acc[c][e] += w * v[e];
         }
@@ -267,11 +263,11 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
 }
 
 // ============================================================== backward
-template <class DT, int CB, int NB, int RHC>
+template <class DT, int VB, int CB, int NB, int RHC>
 __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp) {
   using S = typename DT::S;
-  constexpr int E = 16 / (int)sizeof(S);
-  constexpr int KV = E;
+  constexpr int E = VB / (int)sizeof(S);
+  constexpr int KV = 16 / (int)sizeof(S);
   constexpr int colw = kWave * E;
   const ReadParams& p = bp.f;
   extern __shared__ float smem[];
@@ -280,10 +276,10 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   const int nwaves = blockDim.x / kWave;
   const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
   // LDS: source tables | static query [R] | per wave: p [64], dW [64], dl [64],
-  // contributions [N*nh][rh] | fold [nwaves][n_part]
+  // contributions [nh*np][rh] | fold [nwaves][n_part]
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
-  const int wave_floats = 3 * 64 + N * p.nh * rh;
+  const int wave_floats = 3 * 64 + p.np * p.nh * rh;
   float* s_p = s_q + R + wslot * wave_floats;
   float* s_dw = s_p + 64;
   float* s_dl = s_dw + 64;
@@ -306,10 +302,11 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   const int64_t t0 = wv < p.n_items * p.streams ? wv / p.n_items : p.n_tok;
   const int h0 = (item * CB * colw) / dh;
   const int nh = min(p.nh, H - h0);
-  const int npairs = N * nh;
-  const bool has_pair = lane < npairs;
-  const int ph = h0 + (has_pair ? lane / N : 0);
-  const int ps = has_pair ? lane % N : 0;
+  const int np = p.np;
+  const int lh = lane / np, lsrc = lane - (lane / np) * np;
+  const bool has_pair = lh < nh && lsrc < N;
+  const int ph = h0 + (lh < nh ? lh : 0);
+  const int ps = has_pair ? lsrc : 0;
   const int kch = p.kch;
   const bool dyn = p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
@@ -422,7 +419,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
           if (lane == 0) s_dw[s] = t;
         } else {
           const float t = group_sum(part[0], gl);
-          if (ok[0] && (lane & (gl - 1)) == 0) s_dw[hd[0] * N + s] = t;
+          if (ok[0] && (lane & (gl - 1)) == 0) s_dw[hd[0] * np + s] = t;
         }
       }
     }
@@ -430,11 +427,11 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 
     // ---- per pair: softmax backward, key-norm backward state, contributions to dq
     float ge = 0.f, kinv = 1.f, mr = 0.f;
+    // softmax backward: dl = p (dW - sum_s p dW), the sum a butterfly over the head's group
+    const float dwr = has_pair ? DT::rnd(s_dw[lane]) : 0.f;
+    const float pdot = group_sum(has_pair ? pr * dwr : 0.f, np);
     if (has_pair) {
-      const int hr = lane / N;
-      float dot = 0.f;
-      for (int t = 0; t < N; ++t) dot += s_p[hr * N + t] * DT::rnd(s_dw[hr * N + t]);
-      const float dl = pr * (DT::rnd(s_dw[lane]) - dot);
+      const float dl = pr * (dwr - pdot);
       s_dl[lane] = dl;
       ge = DT::rnd(DT::rnd(dl) * p.scale);
       if (p.key_norm) kinv = key_inv_rms<DT, RHC>(kr, kch, rh, p.eps);
@@ -464,13 +461,13 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     // ---- query gradient and bias accumulation (owner lanes)
     float dqt = 0.f;
     if (q_owner) {
-      for (int s = 0; s < N; ++s) dqt += s_c[(qh * N + s) * rh + qj];
+      for (int s = 0; s < N; ++s) dqt += s_c[(qh * np + s) * rh + qj];
       if (dyn) dqt = DT::rnd(dqt);
       qacc += dqt;
     }
     if (p.bias && lane < N) {
       float b = 0.f;
-      for (int h = 0; h < nh; ++h) b += s_dl[h * N + lane];
+      for (int h = 0; h < nh; ++h) b += s_dl[h * np + lane];
       bacc += b;
     }
 
@@ -482,7 +479,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
           if (ok[c]) {
-            const float w = DT::rnd(s_p[hd[c] * N + s]);
+            const float w = DT::rnd(s_p[hd[c] * np + s]);
             float dv[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) dv[e] = DT::rnd(w * g[c][e]);
@@ -530,31 +527,38 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 }
 
 // ============================================================== launchers
-template <class DT, int CB, int NB, int RHC>
+template <class DT, int VB, int CB, int NB, int RHC>
 static hipError_t fast_fwd_t(const ReadParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st, p);
+  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, VB, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st,
+                     p);
   return hipGetLastError();
 }
-template <class DT, int CB, int NB, int RHC>
+template <class DT, int VB, int CB, int NB, int RHC>
 static hipError_t fast_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((lr_bwd_fast_kernel<DT, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st, p);
+  hipLaunchKernelGGL((lr_bwd_fast_kernel<DT, VB, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st,
+                     p);
   return hipGetLastError();
 }
 
-// L.nmax selects NB (8/16/32), L.wpt carries CB (1/2), L.teams carries RHC (2/8)
-#define ATTNRES_FAST_SWITCH(fn, P)                   \
-  switch (L.wpt * 1000 + L.nmax * 10 + L.teams) {    \
-    case 1082: return fn<DT, 1, 8, 2>(P, L, st);     \
-    case 1162: return fn<DT, 1, 16, 2>(P, L, st);    \
-    case 1322: return fn<DT, 1, 32, 2>(P, L, st);    \
-    case 1088: return fn<DT, 1, 8, 8>(P, L, st);     \
-    case 1168: return fn<DT, 1, 16, 8>(P, L, st);    \
-    case 1328: return fn<DT, 1, 32, 8>(P, L, st);    \
-    case 2082: return fn<DT, 2, 8, 2>(P, L, st);     \
-    case 2162: return fn<DT, 2, 16, 2>(P, L, st);    \
-    case 2088: return fn<DT, 2, 8, 8>(P, L, st);     \
-    case 2168: return fn<DT, 2, 16, 8>(P, L, st);    \
-    default: return hipErrorInvalidValue;            \
+// L.vec = value vector bytes (16 / 8), L.wpt = columns per item (1/2),
+// L.nmax = source slots (8/16/32), L.teams = key chunks per head slot (2/8)
+#define ATTNRES_FAST_SWITCH(fn, P)                        \
+  switch (L.vec * 10000 + L.wpt * 1000 + L.nmax * 10 + L.teams) { \
+    case 161082: return fn<DT, 16, 1, 8, 2>(P, L, st);    \
+    case 161162: return fn<DT, 16, 1, 16, 2>(P, L, st);   \
+    case 161322: return fn<DT, 16, 1, 32, 2>(P, L, st);   \
+    case 161088: return fn<DT, 16, 1, 8, 8>(P, L, st);    \
+    case 161168: return fn<DT, 16, 1, 16, 8>(P, L, st);   \
+    case 162082: return fn<DT, 16, 2, 8, 2>(P, L, st);    \
+    case 162162: return fn<DT, 16, 2, 16, 2>(P, L, st);   \
+    case 162088: return fn<DT, 16, 2, 8, 8>(P, L, st);    \
+    case 81082: return fn<DT, 8, 1, 8, 2>(P, L, st);      \
+    case 81162: return fn<DT, 8, 1, 16, 2>(P, L, st);     \
+    case 81322: return fn<DT, 8, 1, 32, 2>(P, L, st);     \
+    case 81088: return fn<DT, 8, 1, 8, 8>(P, L, st);      \
+    case 81168: return fn<DT, 8, 1, 16, 8>(P, L, st);     \
+    case 81328: return fn<DT, 8, 1, 32, 8>(P, L, st);     \
+    default: return hipErrorInvalidValue;                 \
   }
 
 template <class DT>

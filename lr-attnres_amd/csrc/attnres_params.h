@@ -42,6 +42,7 @@ struct ReadParams {
   // holding `nh` whole heads of one token; items per token = n_items; waves
   // with the same item index walk the tokens with stride `streams`
   int32_t n_items, nh, kch, streams;
+  int32_t np;  // lanes per head in the (head, source) pair layout: next power of two >= n_src
 };
 
 struct ReadBwdParams {

@@ -296,8 +296,8 @@ def test_weights_sum_to_one_and_match_oracle():
     vals = [randn(g, (B, T, D), torch.bfloat16) for _ in range(S)]
     keys = [randn(g, (B, T, R), torch.bfloat16) for _ in range(S)]
     q = randn(g, (Hh, R // Hh), torch.bfloat16, 0.5)
-    vd, kd = [x.to(DEV) for x in vals], [x.to(DEV) for x in keys]
-    desc = H.Desc(vd, kd, q.to(DEV), None, None, None, Hh, 0.25, True, False, H.MODE_SOFTMAX, 0, False)
+    vd, kd, qd = [x.to(DEV) for x in vals], [x.to(DEV) for x in keys], q.to(DEV)
+    desc = H.Desc(vd, kd, qd, None, None, None, Hh, 0.25, True, False, H.MODE_SOFTMAX, 0, False)
     out, w, _, _ = H.forward(desc, vd[0].device, torch.bfloat16, True, False, True)
     torch.cuda.synchronize()
     sums = w.double().sum(-1)
@@ -379,3 +379,27 @@ def test_config3_full_size_token_subset():
     full = qd.grad.float().cpu()
     summed = (halves[0].float() + halves[1].float()).cpu()
     assert float((full - summed).abs().max()) <= 2e-2 * max(1.0, float(full.abs().max()))
+
+
+def test_bf16_rounding_ties_match_torch():
+    """The kernels round to bf16 in hardware (v_cvt_pk_bf16_f32); check exact
+    round-half-to-even ties against torch's rounding.  With a zero query the
+    two-source weights are exactly 0.5, so out = (a + b) / 2 is exact in fp32
+    and lands on a bf16 tie when a and b differ by one ulp."""
+    base = torch.tensor([1.0, 1.0078125, -3.0, 0.5, 2.0 ** -20, 1.5, 100.0, 7.0], dtype=torch.float32)
+    a = base.to(torch.bfloat16)
+    ulp = torch.ldexp(torch.ones_like(base), torch.frexp(base)[1] - 8)  # one bf16 ulp of |base|
+    b = (base + ulp).to(torch.bfloat16)
+    D = 64
+    va = a.repeat(D // a.numel()).view(1, 1, D)
+    vb = b.repeat(D // b.numel()).view(1, 1, D)
+    keys = [torch.zeros(1, 1, 16, dtype=torch.bfloat16) for _ in range(2)]
+    q = torch.zeros(1, 16)
+    out = ops.lrid_attention_residual_read([va.to(DEV), vb.to(DEV)], [k.to(DEV) for k in keys], q.to(DEV), 1, 1.0,
+                                           False)
+    ref = O.lrid_attention_residual_read_ref([va, vb], keys, q, 1, 1.0, False)
+    assert torch.equal(out.cpu(), ref), (out.cpu(), ref)
+    # the same through the output rounding of the base read
+    out_b = ops.attention_residual_read([va.to(DEV), vb.to(DEV)], torch.zeros(D, device=DEV), False)
+    ref_b = O.attention_residual_read_ref([va, vb], torch.zeros(D), False)
+    assert torch.equal(out_b.cpu(), ref_b)
