@@ -299,6 +299,16 @@ def main():
     fwd_gbs = fwd_b * n_tok / (f_ms / 1e3) / 1e9
     bwd_gbs = bwd_b * n_tok / (b_ms / 1e3) / 1e9 if bwd_b else 0.0
     dom_gbs, dom_name, dom_bytes = (bwd_gbs, "backward", bwd_b) if bwd_b else (fwd_gbs, "forward", fwd_b)
+    # HBM bytes per launch of the dominant kernel, measured with rocprofv3
+    # FETCH_SIZE / WRITE_SIZE (scaled by a copy of known size) and kept in
+    # profiles/traffic_<config>.json; null when no measurement is recorded
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            rec = json.load(f).get("kernels", {}).get("bwd" if bwd_b else "fwd")
+        if rec:
+            traffic = rec["bytes_per_launch"]
 
     res = {
         "metric": "AttnRes fwd+bwd tokens/s (d=1024,N=13,r=64,bf16); HBM GB/s as % of peak",
@@ -321,7 +331,8 @@ def main():
         "hbm_gbs_step": round(gbs_step, 1),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
-                     "bytes_per_token": dom_bytes, "traffic": None},
+                     "bytes_per_token": dom_bytes, "algorithmic_bytes_per_launch": dom_bytes * n_tok,
+                     "traffic": traffic},
         "kernels": {"forward_ms": round(f_ms, 5), "forward_gbs": round(fwd_gbs, 1),
                     "backward_ms": round(b_ms, 5), "backward_gbs": round(bwd_gbs, 1),
                     "bytes_per_token": {"fwd": fwd_b, "bwd": bwd_b}},
