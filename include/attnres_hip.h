@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 2
+#define ATTNRES_ABI_VERSION 3
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -139,6 +139,133 @@ int attnres_read_backward(const attnres_read_desc* desc, const attnres_read_grad
 /* Bytes of workspace attnres_read_backward needs for this description
  * (0 when no cross-token reduction is required).  Host-only; no GPU call. */
 size_t attnres_read_backward_workspace_size(const attnres_read_desc* desc);
+
+/* ------------------------------------------------------------------------
+ * Cached-logit block-training schedule (two phases).
+ *
+ * Phase 1 reads the S completed block summaries once for Q upcoming read
+ * sites whose logits were computed ahead (logits[q, s, t]); it returns each
+ * site's partial read and the log-sum-exp of its logits.  Phase 2 merges a
+ * site's phase-1 result with the still-growing partial block:
+ *   prob = sigmoid(logit_partial + bias - lse),  out = merge(inter, partial, prob)
+ * where the partial block's logit comes from its key and the site's query
+ * (base: key = rms_norm(partial value); LR: key = rms_norm(partial key) and
+ * `* logit_scale`) or is given.
+ * ------------------------------------------------------------------------ */
+
+#define ATTNRES_PHASE1_MAX_QUERIES 16
+#define ATTNRES_PHASE_MAX_DIM 4096
+
+typedef struct attnres_phase1_desc {
+  int32_t n_src;            /* S completed sources, 1..ATTNRES_MAX_SOURCES */
+  int32_t n_q;              /* Q read sites, 1..ATTNRES_PHASE1_MAX_QUERIES */
+  int32_t dtype;            /* values and outputs (ATTNRES_DTYPE_*) */
+  int32_t logits_dtype;     /* logits and their gradient (ATTNRES_DTYPE_*) */
+  int64_t n_tok;            /* B*T */
+  int32_t dim;              /* D <= ATTNRES_PHASE_MAX_DIM */
+  int32_t normalize_output; /* rms-norm every [dim] output row */
+  float norm_eps;
+  const void* const* values;       /* [S] device pointers, rows of dim elements */
+  const int64_t* value_row_stride; /* [S] elements */
+  const void* logits;              /* device; (q, s, t) at q*logit_q_stride + s*logit_s_stride + t */
+  int64_t logit_q_stride;
+  int64_t logit_s_stride;
+} attnres_phase1_desc;
+
+/*
+ * Phase 1 forward.  out [Q, n_tok, dim] (dtype), lse [Q, n_tok] (fp32).  With
+ * normalize_output, out is rms-normed per row and out_prenorm [Q, n_tok, dim]
+ * / out_inv_rms [Q, n_tok] receive what the backward needs (may be NULL when
+ * no backward follows).
+ *
+ * Replaces: _attnres_phase1_logits_read_triton (attnres_ops.py:2742-2777) and
+ *   _attnres_phase1_logits_read_list_triton (:2931-2969), behind
+ *   attention_residual_phase1_from_logits (:3910-3961).
+ */
+int attnres_phase1_forward(const attnres_phase1_desc* desc, void* out, void* out_prenorm, float* lse,
+                           float* out_inv_rms, void* stream);
+
+/*
+ * Phase 1 backward.  grad_out [Q, n_tok, dim] dense; grad_lse [Q, n_tok] fp32
+ * or NULL (zero).  Writes dvalues[s] [n_tok, dim] dense and dlogits
+ * [Q, S, n_tok] dense in logits_dtype.  Needs no workspace.
+ *
+ * Replaces: _attnres_phase1_logits_backward_weights_triton
+ *   (attnres_ops.py:2882-2928) and _attnres_phase1_logits_backward_list_weights_triton
+ *   (:2972-3022).
+ */
+int attnres_phase1_backward(const attnres_phase1_desc* desc, const void* grad_out, const float* grad_lse,
+                            const void* out_prenorm, const float* out_inv_rms, void* const* dvalues,
+                            void* dlogits, void* stream);
+
+#define ATTNRES_MERGE_ADDCMUL 0 /* inter + (partial - inter) * prob   (attnres_ops.py:2642, 4066) */
+#define ATTNRES_MERGE_LERP 1    /* torch.lerp(inter, partial, prob)   (attnres_ops.py:4159) */
+
+typedef struct attnres_phase2_desc {
+  int32_t dtype;            /* partial value / key, query, interblock output, out */
+  int64_t n_tok;
+  int32_t dim;              /* D <= ATTNRES_PHASE_MAX_DIM */
+  int32_t rank;             /* 0: key = the partial value (base); > 0: LR partial key width (one head) */
+  int32_t logit_given;      /* 1: use partial_logit; 0: score key against query */
+  int32_t merge;            /* ATTNRES_MERGE_* */
+  int32_t key_norm;
+  int32_t normalize_output;
+  float logit_scale;        /* LR logit multiplier */
+  float norm_eps;
+  float logit_bias;               /* constant fp32 logit bias (used when logit_bias_dev is NULL) */
+  const float* logit_bias_dev;    /* device fp32 scalar bias (learned), or NULL */
+  float value_scale;              /* block-summary multiplier of the partial value (1 = none) */
+  const float* value_scale_dev;   /* device fp32 scalar multiplier (learned), or NULL */
+  int32_t scale_key;              /* LR: multiply the partial key by the same scale */
+  const void* partial_value;      /* [n_tok] rows of dim */
+  int64_t partial_value_row_stride;
+  const void* partial_key;        /* LR: [n_tok] rows of rank */
+  int64_t partial_key_row_stride;
+  const void* query;              /* [dim] (base) or [rank] (LR), dtype */
+  const void* partial_logit;      /* [n_tok] when logit_given */
+  int32_t partial_logit_dtype;
+  const void* interblock_output;  /* [n_tok] rows of dim */
+  int64_t interblock_row_stride;
+  const float* interblock_lse;    /* [n_tok] fp32 */
+} attnres_phase2_desc;
+
+typedef struct attnres_phase2_grads {
+  const void* grad_out;        /* [n_tok, dim] dense */
+  void* dpartial_value;        /* [n_tok, dim] dense */
+  void* dpartial_key;          /* [n_tok, rank] dense (LR) */
+  void* dquery;                /* dtype, or NULL */
+  void* dinterblock_output;    /* [n_tok, dim] dense */
+  float* dinterblock_lse;      /* [n_tok] */
+  void* dpartial_logit;        /* [n_tok] in partial_logit_dtype (logit_given) */
+  float* dlogit_bias;          /* fp32 scalar, or NULL */
+  float* dvalue_scale;         /* fp32 scalar, or NULL */
+  void* workspace;             /* for the cross-token sums */
+  size_t workspace_bytes;
+} attnres_phase2_grads;
+
+/*
+ * Phase 2 forward: out [n_tok, dim] (rms-normed when normalize_output).
+ *
+ * Replaces: _attnres_phase2_merge_triton (attnres_ops.py:3227-3263),
+ *   _attnres_phase2_logits_merge_triton (:3348-3382), _lrid_phase2_merge_triton
+ *   (:3429-3474) and the eager merges behind attention_residual_phase2[_torch],
+ *   attention_residual_phase2_from_logit and lrid_attention_residual_phase2[_torch]
+ *   (:3964-4160, :2630-2642).  value_scale folds the block summary
+ *   partial * count^-alpha (model.py:990-1018) into the read.
+ */
+int attnres_phase2_forward(const attnres_phase2_desc* desc, void* out, void* stream);
+
+/*
+ * Phase 2 backward (recomputes the forward's per-token quantities).
+ *
+ * Replaces: _attnres_phase2_backward_triton (attnres_ops.py:3266-3345),
+ *   _attnres_phase2_logits_backward_triton (:3385-3426),
+ *   _lrid_phase2_backward_triton (:3477-3532).
+ */
+int attnres_phase2_backward(const attnres_phase2_desc* desc, const attnres_phase2_grads* grads, void* stream);
+
+/* Workspace bytes attnres_phase2_backward needs (host-only). */
+size_t attnres_phase2_backward_workspace_size(const attnres_phase2_desc* desc);
 
 #ifdef __cplusplus
 }

@@ -16,12 +16,15 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_SOURCES = 64
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 MODE_SOFTMAX, MODE_AVERAGE = 0, 1
 GATE_NONE, GATE_LINEAR, GATE_SIGMOID = 0, 1, 2
+MERGE_ADDCMUL, MERGE_LERP = 0, 1
+PHASE1_MAX_QUERIES = 16
+PHASE_MAX_DIM = 4096
 FLT_EPSILON = float(torch.finfo(torch.float32).eps)
 
 
@@ -73,6 +76,76 @@ class ReadGrads(ctypes.Structure):
     ]
 
 
+class Phase1Desc(ctypes.Structure):
+    """attnres_phase1_desc."""
+
+    _fields_ = [
+        ("n_src", c_int32),
+        ("n_q", c_int32),
+        ("dtype", c_int32),
+        ("logits_dtype", c_int32),
+        ("n_tok", c_int64),
+        ("dim", c_int32),
+        ("normalize_output", c_int32),
+        ("norm_eps", c_float),
+        ("values", POINTER(c_void_p)),
+        ("value_row_stride", POINTER(c_int64)),
+        ("logits", c_void_p),
+        ("logit_q_stride", c_int64),
+        ("logit_s_stride", c_int64),
+    ]
+
+
+class Phase2Desc(ctypes.Structure):
+    """attnres_phase2_desc."""
+
+    _fields_ = [
+        ("dtype", c_int32),
+        ("n_tok", c_int64),
+        ("dim", c_int32),
+        ("rank", c_int32),
+        ("logit_given", c_int32),
+        ("merge", c_int32),
+        ("key_norm", c_int32),
+        ("normalize_output", c_int32),
+        ("logit_scale", c_float),
+        ("norm_eps", c_float),
+        ("logit_bias", c_float),
+        ("logit_bias_dev", POINTER(c_float)),
+        ("value_scale", c_float),
+        ("value_scale_dev", POINTER(c_float)),
+        ("scale_key", c_int32),
+        ("partial_value", c_void_p),
+        ("partial_value_row_stride", c_int64),
+        ("partial_key", c_void_p),
+        ("partial_key_row_stride", c_int64),
+        ("query", c_void_p),
+        ("partial_logit", c_void_p),
+        ("partial_logit_dtype", c_int32),
+        ("interblock_output", c_void_p),
+        ("interblock_row_stride", c_int64),
+        ("interblock_lse", POINTER(c_float)),
+    ]
+
+
+class Phase2Grads(ctypes.Structure):
+    """attnres_phase2_grads."""
+
+    _fields_ = [
+        ("grad_out", c_void_p),
+        ("dpartial_value", c_void_p),
+        ("dpartial_key", c_void_p),
+        ("dquery", c_void_p),
+        ("dinterblock_output", c_void_p),
+        ("dinterblock_lse", POINTER(c_float)),
+        ("dpartial_logit", c_void_p),
+        ("dlogit_bias", POINTER(c_float)),
+        ("dvalue_scale", POINTER(c_float)),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
 _lib = None
 
 
@@ -99,6 +172,18 @@ def load() -> ctypes.CDLL:
     lib.attnres_read_backward.argtypes = [POINTER(ReadDesc), POINTER(ReadGrads), c_void_p]
     lib.attnres_read_backward_workspace_size.restype = c_size_t
     lib.attnres_read_backward_workspace_size.argtypes = [POINTER(ReadDesc)]
+    lib.attnres_phase1_forward.restype = c_int
+    lib.attnres_phase1_forward.argtypes = [POINTER(Phase1Desc), c_void_p, c_void_p, POINTER(c_float),
+                                           POINTER(c_float), c_void_p]
+    lib.attnres_phase1_backward.restype = c_int
+    lib.attnres_phase1_backward.argtypes = [POINTER(Phase1Desc), c_void_p, POINTER(c_float), c_void_p,
+                                            POINTER(c_float), POINTER(c_void_p), c_void_p, c_void_p]
+    lib.attnres_phase2_forward.restype = c_int
+    lib.attnres_phase2_forward.argtypes = [POINTER(Phase2Desc), c_void_p, c_void_p]
+    lib.attnres_phase2_backward.restype = c_int
+    lib.attnres_phase2_backward.argtypes = [POINTER(Phase2Desc), POINTER(Phase2Grads), c_void_p]
+    lib.attnres_phase2_backward_workspace_size.restype = c_size_t
+    lib.attnres_phase2_backward_workspace_size.argtypes = [POINTER(Phase2Desc)]
     v = lib.attnres_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libattnres_hip ABI {v} != expected {ABI_VERSION}; rebuild the library")
@@ -244,3 +329,151 @@ def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, wan
     rc = lib.attnres_read_backward(ctypes.byref(desc.c), ctypes.byref(g), _stream(device))
     _check(rc, "backward")
     return dvals, dkeys, dq, dqd, dg, db
+
+
+# ---------------------------------------------------------------------------
+# cached-logit phases
+# ---------------------------------------------------------------------------
+
+class Phase1:
+    """Descriptor of one phase-1 call: S value row tensors [n_tok, D] (any
+    uniform row stride) and dense logits [Q, S, n_tok]."""
+
+    def __init__(self, values, logits, normalize_output, eps=FLT_EPSILON):
+        n = len(values)
+        self._tensors = (list(values), logits)
+        self.n_src = n
+        self.n_q = logits.size(0)
+        self.n_tok = values[0].size(0)
+        self.D = values[0].size(1)
+        self._vals = (c_void_p * n)(*[t.data_ptr() for t in values])
+        self._vstr = (c_int64 * n)(*[t.stride(0) for t in values])
+        d = Phase1Desc()
+        d.n_src = n
+        d.n_q = self.n_q
+        d.dtype = DTYPE_CODE[values[0].dtype]
+        d.logits_dtype = DTYPE_CODE[logits.dtype]
+        d.n_tok = self.n_tok
+        d.dim = self.D
+        d.normalize_output = int(bool(normalize_output))
+        d.norm_eps = float(eps)
+        d.values = self._vals
+        d.value_row_stride = self._vstr
+        d.logits = logits.data_ptr()
+        d.logit_q_stride = n * self.n_tok
+        d.logit_s_stride = self.n_tok
+        self.c = d
+
+
+def phase1_forward(desc: Phase1, device, dtype, for_backward: bool):
+    """Returns (out [Q, n_tok, D], lse [Q, n_tok], prenorm | empty, inv_rms | empty)."""
+    lib = load()
+    Q, n, D = desc.n_q, desc.n_tok, desc.D
+    out = torch.empty((Q, n, D), device=device, dtype=dtype)
+    lse = torch.empty((Q, n), device=device, dtype=torch.float32)
+    keep = bool(desc.c.normalize_output) and for_backward
+    pre = torch.empty((Q, n, D) if keep else (0,), device=device, dtype=dtype)
+    inv = torch.empty((Q, n) if keep else (0,), device=device, dtype=torch.float32)
+    rc = lib.attnres_phase1_forward(ctypes.byref(desc.c), _ptr(out), _ptr(pre) if keep else None, _fptr(lse),
+                                    _fptr(inv) if keep else None, _stream(device))
+    _check(rc, "phase-1 forward")
+    return out, lse, pre, inv
+
+
+def phase1_backward(desc: Phase1, device, dtype, logits_dtype, grad_out, grad_lse, prenorm, inv_rms):
+    """Returns (dvalues list of [n_tok, D], dlogits [Q, S, n_tok])."""
+    lib = load()
+    n = desc.n_src
+    dvals = [torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype) for _ in range(n)]
+    dlog = torch.empty((desc.n_q, n, desc.n_tok), device=device, dtype=logits_dtype)
+    dv_arr = (c_void_p * n)(*[t.data_ptr() for t in dvals])
+    keep = prenorm is not None and prenorm.numel() > 0
+    rc = lib.attnres_phase1_backward(ctypes.byref(desc.c), _ptr(grad_out),
+                                     _fptr(grad_lse) if grad_lse is not None else None,
+                                     _ptr(prenorm) if keep else None, _fptr(inv_rms) if keep else None, dv_arr,
+                                     _ptr(dlog), _stream(device))
+    _check(rc, "phase-1 backward")
+    return dvals, dlog
+
+
+class Phase2:
+    """Descriptor of one phase-2 merge over [n_tok] rows."""
+
+    def __init__(self, partial_value, partial_key, query, partial_logit, inter, lse, merge, key_norm,
+                 normalize_output, logit_scale, bias_value, bias_tensor, scale_value, scale_tensor, scale_key,
+                 eps=FLT_EPSILON):
+        self._tensors = (partial_value, partial_key, query, partial_logit, inter, lse, bias_tensor, scale_tensor)
+        self.n_tok = partial_value.size(0)
+        self.D = partial_value.size(1)
+        self.R = partial_key.size(1) if partial_key is not None else 0
+        d = Phase2Desc()
+        d.dtype = DTYPE_CODE[partial_value.dtype]
+        d.n_tok = self.n_tok
+        d.dim = self.D
+        d.rank = self.R
+        d.logit_given = int(partial_logit is not None)
+        d.merge = merge
+        d.key_norm = int(bool(key_norm))
+        d.normalize_output = int(bool(normalize_output))
+        d.logit_scale = float(logit_scale)
+        d.norm_eps = float(eps)
+        d.logit_bias = float(bias_value)
+        d.logit_bias_dev = _fptr(bias_tensor)
+        d.value_scale = float(scale_value)
+        d.value_scale_dev = _fptr(scale_tensor)
+        d.scale_key = int(bool(scale_key))
+        d.partial_value = partial_value.data_ptr()
+        d.partial_value_row_stride = partial_value.stride(0)
+        if partial_key is not None:
+            d.partial_key = partial_key.data_ptr()
+            d.partial_key_row_stride = partial_key.stride(0)
+        d.query = query.data_ptr() if query is not None else None
+        if partial_logit is not None:
+            d.partial_logit = partial_logit.data_ptr()
+            d.partial_logit_dtype = DTYPE_CODE[partial_logit.dtype]
+        d.interblock_output = inter.data_ptr()
+        d.interblock_row_stride = inter.stride(0)
+        d.interblock_lse = _fptr(lse)
+        self.c = d
+
+
+def phase2_forward(desc: Phase2, device, dtype):
+    lib = load()
+    out = torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype)
+    rc = lib.attnres_phase2_forward(ctypes.byref(desc.c), _ptr(out), _stream(device))
+    _check(rc, "phase-2 forward")
+    return out
+
+
+def phase2_backward(desc: Phase2, device, dtype, grad_out, want_dquery, query_shape, logit_dtype, want_dbias,
+                    want_dscale):
+    """Returns (dpartial, dpartial_key | None, dquery | None, dinter, dlse, dlogit | None, dbias | None,
+    dscale | None)."""
+    lib = load()
+    n, D, R = desc.n_tok, desc.D, desc.R
+    lr = R > 0
+    dp = torch.empty((n, D), device=device, dtype=dtype)
+    dpk = torch.empty((n, R), device=device, dtype=dtype) if lr else None
+    dq = torch.empty(query_shape, device=device, dtype=dtype) if want_dquery else None
+    di = torch.empty((n, D), device=device, dtype=dtype)
+    dl = torch.empty((n,), device=device, dtype=torch.float32)
+    dlg = torch.empty((n,), device=device, dtype=logit_dtype) if logit_dtype is not None else None
+    db = torch.empty((1,), device=device, dtype=torch.float32) if want_dbias else None
+    ds = torch.empty((1,), device=device, dtype=torch.float32) if want_dscale else None
+    g = Phase2Grads()
+    g.grad_out = grad_out.data_ptr()
+    g.dpartial_value = dp.data_ptr()
+    g.dpartial_key = dpk.data_ptr() if dpk is not None else None
+    g.dquery = dq.data_ptr() if dq is not None else None
+    g.dinterblock_output = di.data_ptr()
+    g.dinterblock_lse = _fptr(dl)
+    g.dpartial_logit = dlg.data_ptr() if dlg is not None else None
+    g.dlogit_bias = _fptr(db)
+    g.dvalue_scale = _fptr(ds)
+    ws_bytes = lib.attnres_phase2_backward_workspace_size(ctypes.byref(desc.c))
+    ws = torch.empty((max(int(ws_bytes), 1),), device=device, dtype=torch.uint8)
+    g.workspace = ws.data_ptr()
+    g.workspace_bytes = int(ws_bytes)
+    rc = lib.attnres_phase2_backward(ctypes.byref(desc.c), ctypes.byref(g), _stream(device))
+    _check(rc, "phase-2 backward")
+    return dp, dpk, dq, di, dl, dlg, db, ds

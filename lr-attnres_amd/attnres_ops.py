@@ -412,19 +412,304 @@ def lrid_attention_residual_read_torch(values, keys, query: Tensor, num_heads: i
                                         source_counts=source_counts, source_logit_biases=source_logit_biases)
 
 
-# ---------------------------------------------------------------- cached-logit phases (not yet built)
+# ---------------------------------------------------------------- cached-logit phases
 
-def _not_built(name):
-    def f(*args, **kwargs):
-        raise NotImplementedError(f"{name} (cached-logit block schedule) is not implemented in the HIP build yet")
-    f.__name__ = name
-    return f
+def _rows2d(t: Tensor) -> Tensor:
+    """[B, T, W] -> [B*T, W] row view (copied only when tokens are not uniformly strided)."""
+    t = _hip.as_rows(t)
+    return t.view(t.size(0) * t.size(1), t.size(2))
 
 
-attention_residual_phase1 = _not_built("attention_residual_phase1")
-attention_residual_phase1_from_logits = _not_built("attention_residual_phase1_from_logits")
-attention_residual_phase2 = _not_built("attention_residual_phase2")
-attention_residual_phase2_from_logit = _not_built("attention_residual_phase2_from_logit")
-attention_residual_phase2_torch = _not_built("attention_residual_phase2_torch")
-lrid_attention_residual_phase2 = _not_built("lrid_attention_residual_phase2")
-lrid_attention_residual_phase2_torch = _not_built("lrid_attention_residual_phase2_torch")
+@torch.library.custom_op("attnres_hip::phase1", mutates_args=())
+def _phase1_op(values: list[Tensor], logits: Tensor, normalize_output: bool,
+               save: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    desc = _hip.Phase1(values, logits, normalize_output)
+    v0 = values[0]
+    with torch.cuda.device(v0.device):
+        out, lse, pre, inv = _hip.phase1_forward(desc, v0.device, v0.dtype, save)
+    return out, lse, pre, inv
+
+
+@_phase1_op.register_fake
+def _phase1_fake(values, logits, normalize_output, save):
+    v0 = values[0]
+    Q, n, D = logits.size(0), v0.size(0), v0.size(1)
+    keep = normalize_output and save
+    return (v0.new_empty((Q, n, D)), v0.new_empty((Q, n), dtype=torch.float32),
+            v0.new_empty((Q, n, D) if keep else (0,)), v0.new_empty((Q, n) if keep else (0,), dtype=torch.float32))
+
+
+@torch.library.custom_op("attnres_hip::phase1_backward", mutates_args=())
+def _phase1_backward_op(values: list[Tensor], logits: Tensor, grad_out: Tensor, grad_lse: Optional[Tensor],
+                        prenorm: Tensor, inv_rms: Tensor, normalize_output: bool) -> tuple[list[Tensor], Tensor]:
+    desc = _hip.Phase1(values, logits, normalize_output)
+    v0 = values[0]
+    with torch.cuda.device(v0.device):
+        dvals, dlog = _hip.phase1_backward(desc, v0.device, v0.dtype, logits.dtype, grad_out, grad_lse, prenorm,
+                                           inv_rms)
+    return dvals, dlog
+
+
+@_phase1_backward_op.register_fake
+def _phase1_backward_fake(values, logits, grad_out, grad_lse, prenorm, inv_rms, normalize_output):
+    return [v.new_empty((v.size(0), v.size(1))) for v in values], logits.new_empty(logits.shape)
+
+
+def _phase1_setup_context(ctx, inputs, output):
+    values, logits, normalize_output, save = inputs
+    out, lse, pre, inv = output
+    ctx.n_values = len(values)
+    ctx.normalize_output = normalize_output
+    ctx.save_for_backward(*values, logits, pre, inv)
+
+
+def _phase1_backward(ctx, grad_out, grad_lse, grad_pre, grad_inv):
+    saved = list(ctx.saved_tensors)
+    values = saved[:ctx.n_values]
+    logits, pre, inv = saved[ctx.n_values:]
+    v0 = values[0]
+    if grad_out is None:
+        grad_out = v0.new_zeros((logits.size(0), v0.size(0), v0.size(1)))
+    grad_lse = grad_lse.float().contiguous() if grad_lse is not None else None
+    dvals, dlog = _phase1_backward_op(values, logits, grad_out.contiguous(), grad_lse, pre, inv,
+                                      ctx.normalize_output)
+    return dvals, dlog, None, None
+
+
+_phase1_op.register_autograd(_phase1_backward, setup_context=_phase1_setup_context)
+
+
+def attention_residual_phase1_from_logits(values, logits: Tensor, force_triton: bool = False,
+                                          normalize_output: bool = False):
+    """Cached-logit read of completed sources for Q read sites (reference: attnres_ops.py:3910-3961).
+
+    values: S x [B,T,D] (list or stacked [S,B,T,D]); logits [Q,S,B,T] (any
+    float dtype; softmax in fp32).  Returns (out [Q,B,T,D] in the value dtype,
+    lse [Q,B,T] fp32).  Up to 64 sources and 16 read sites, D <= 4096.
+    """
+    srcs = _sources(values)
+    if len(srcs) == 0:
+        raise RuntimeError("Cached-logit AttnRes phase1 requires at least one source")
+    _check_sources(srcs, "attention_residual_phase1_from_logits")
+    B, T, D = srcs[0].shape
+    S = len(srcs)
+    if logits.dim() != 4 or logits.size(1) != S or tuple(logits.shape[2:]) != (B, T):
+        raise RuntimeError(f"attention_residual_phase1_from_logits: logits must be [Q, {S}, {B}, {T}], "
+                           f"got {tuple(logits.shape)}")
+    Q = logits.size(0)
+    if Q < 1 or Q > _hip.PHASE1_MAX_QUERIES:
+        raise RuntimeError(f"attention_residual_phase1_from_logits: 1 <= Q <= {_hip.PHASE1_MAX_QUERIES}, got {Q}")
+    if D > _hip.PHASE_MAX_DIM:
+        raise RuntimeError(f"attention_residual_phase1_from_logits: D={D} exceeds {_hip.PHASE_MAX_DIM}")
+    if logits.dtype not in _ALLOWED:
+        raise RuntimeError(f"attention_residual_phase1_from_logits: logits dtype {logits.dtype} is not supported")
+    _check_gpu(srcs + [logits], "attention_residual_phase1_from_logits")
+    rows = [_rows2d(t) for t in srcs]
+    lg = logits.contiguous().view(Q, S, B * T)
+    save = torch.is_grad_enabled() and (logits.requires_grad or any(t.requires_grad for t in srcs))
+    out, lse, _, _ = _phase1_op(rows, lg, bool(normalize_output), bool(save))
+    return out.view(Q, B, T, D), lse.view(Q, B, T)
+
+
+def attention_residual_phase1(values, queries: Tensor, key_norm: bool, force_triton: bool = False):
+    """Phase 1 with logits from a query bank (reference: attnres_ops.py:3862-3907).
+
+    Not used by the reference model's training path (which caches logits and
+    calls ``attention_residual_phase1_from_logits``); not implemented here.
+    """
+    raise NotImplementedError("attention_residual_phase1 (query-bank form) is not implemented in the HIP build; "
+                              "use attention_residual_phase1_from_logits")
+
+
+@torch.library.custom_op("attnres_hip::phase2", mutates_args=())
+def _phase2_op(partial_value: Tensor, partial_key: Optional[Tensor], query: Optional[Tensor],
+               partial_logit: Optional[Tensor], inter: Tensor, lse: Tensor, bias_t: Optional[Tensor],
+               scale_t: Optional[Tensor], merge: int, key_norm: bool, normalize_output: bool, logit_scale: float,
+               bias_value: float, scale_value: float, scale_key: bool) -> Tensor:
+    desc = _hip.Phase2(partial_value, partial_key, query, partial_logit, inter, lse, merge, key_norm,
+                       normalize_output, logit_scale, bias_value, bias_t, scale_value, scale_t, scale_key)
+    with torch.cuda.device(partial_value.device):
+        return _hip.phase2_forward(desc, partial_value.device, partial_value.dtype)
+
+
+@_phase2_op.register_fake
+def _phase2_fake(partial_value, partial_key, query, partial_logit, inter, lse, bias_t, scale_t, merge, key_norm,
+                 normalize_output, logit_scale, bias_value, scale_value, scale_key):
+    return partial_value.new_empty(partial_value.shape)
+
+
+@torch.library.custom_op("attnres_hip::phase2_backward", mutates_args=())
+def _phase2_backward_op(partial_value: Tensor, partial_key: Optional[Tensor], query: Optional[Tensor],
+                        partial_logit: Optional[Tensor], inter: Tensor, lse: Tensor, bias_t: Optional[Tensor],
+                        scale_t: Optional[Tensor], grad_out: Tensor, merge: int, key_norm: bool,
+                        normalize_output: bool, logit_scale: float, bias_value: float, scale_value: float,
+                        scale_key: bool, want_dbias: bool, want_dscale: bool) -> list[Tensor]:
+    desc = _hip.Phase2(partial_value, partial_key, query, partial_logit, inter, lse, merge, key_norm,
+                       normalize_output, logit_scale, bias_value, bias_t, scale_value, scale_t, scale_key)
+    dev = partial_value.device
+    with torch.cuda.device(dev):
+        dp, dpk, dq, di, dl, dlg, db, ds = _hip.phase2_backward(
+            desc, dev, partial_value.dtype, grad_out,
+            want_dquery=query is not None and partial_logit is None,
+            query_shape=tuple(query.shape) if query is not None else (0,),
+            logit_dtype=partial_logit.dtype if partial_logit is not None else None,
+            want_dbias=want_dbias, want_dscale=want_dscale)
+    e = lambda: torch.empty((0,), device=dev)  # noqa: E731
+    return [dp, dpk if dpk is not None else e(), dq if dq is not None else e(), di, dl,
+            dlg if dlg is not None else e(), db if db is not None else e(), ds if ds is not None else e()]
+
+
+@_phase2_backward_op.register_fake
+def _phase2_backward_fake(partial_value, partial_key, query, partial_logit, inter, lse, bias_t, scale_t, grad_out,
+                          merge, key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key,
+                          want_dbias, want_dscale):
+    e = lambda: partial_value.new_empty((0,))  # noqa: E731
+    n = partial_value.size(0)
+    return [partial_value.new_empty(partial_value.shape),
+            partial_key.new_empty(partial_key.shape) if partial_key is not None else e(),
+            query.new_empty(query.shape) if query is not None and partial_logit is None else e(),
+            inter.new_empty(inter.shape), partial_value.new_empty((n,), dtype=torch.float32),
+            partial_logit.new_empty(partial_logit.shape) if partial_logit is not None else e(),
+            partial_value.new_empty((1,), dtype=torch.float32) if want_dbias else e(),
+            partial_value.new_empty((1,), dtype=torch.float32) if want_dscale else e()]
+
+
+def _phase2_setup_context(ctx, inputs, output):
+    (partial_value, partial_key, query, partial_logit, inter, lse, bias_t, scale_t, merge, key_norm,
+     normalize_output, logit_scale, bias_value, scale_value, scale_key) = inputs
+    ctx.has = tuple(t is not None for t in (partial_key, query, partial_logit, bias_t, scale_t))
+    opt = [t for t in (partial_key, query, partial_logit, bias_t, scale_t) if t is not None]
+    ctx.save_for_backward(partial_value, inter, lse, *opt)
+    ctx.flags = (merge, key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key)
+
+
+def _phase2_backward(ctx, grad_out):
+    saved = list(ctx.saved_tensors)
+    partial_value, inter, lse = saved[:3]
+    rest = saved[3:]
+    partial_key, query, partial_logit, bias_t, scale_t = [rest.pop(0) if h else None for h in ctx.has]
+    merge, key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key = ctx.flags
+    want_dbias = bias_t is not None and ctx.needs_input_grad[6]
+    want_dscale = scale_t is not None and ctx.needs_input_grad[7]
+    dp, dpk, dq, di, dl, dlg, db, ds = _phase2_backward_op(
+        partial_value, partial_key, query, partial_logit, inter, lse, bias_t, scale_t, grad_out.contiguous(), merge,
+        key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key, want_dbias, want_dscale)
+    return (dp, dpk if partial_key is not None else None,
+            dq if query is not None and partial_logit is None else None,
+            dlg if partial_logit is not None else None, di, dl,
+            db.reshape(bias_t.shape) if want_dbias else None,
+            ds.reshape(scale_t.shape) if want_dscale else None,
+            None, None, None, None, None, None, None)
+
+
+_phase2_op.register_autograd(_phase2_backward, setup_context=_phase2_setup_context)
+
+
+def _scalar_arg(x, device, what):
+    """(float value, fp32 [1] tensor or None) for a float-or-tensor argument."""
+    if x is None:
+        return 0.0, None
+    if isinstance(x, Tensor):
+        if x.numel() != 1:
+            raise RuntimeError(f"{what} must be a scalar")
+        return 0.0, x.to(device=device, dtype=torch.float32).reshape(1)
+    return float(x), None
+
+
+def _phase2(partial_value, partial_key, query, partial_logit, interblock_output, interblock_lse, merge, key_norm,
+            normalize_output, logit_scale, logit_bias, partial_scale, scale_key, what):
+    if partial_value.dim() != 3:
+        raise RuntimeError(f"{what}: partial_value must be [B, T, D]")
+    B, T, D = partial_value.shape
+    dtype = partial_value.dtype
+    if dtype not in _ALLOWED:
+        raise RuntimeError(f"{what}: dtype {dtype} is not supported (fp32, bf16, fp16)")
+    if D > _hip.PHASE_MAX_DIM:
+        raise RuntimeError(f"{what}: D={D} exceeds {_hip.PHASE_MAX_DIM}")
+    if tuple(interblock_output.shape) != (B, T, D):
+        raise RuntimeError(f"{what}: interblock_output must be {(B, T, D)}, got {tuple(interblock_output.shape)}")
+    if interblock_lse.numel() != B * T:
+        raise RuntimeError(f"{what}: interblock_lse must be [B, T]")
+    dev = _check_gpu([partial_value, interblock_output, interblock_lse], what)
+    bias_value, bias_t = _scalar_arg(logit_bias, dev, "logit_bias")
+    if partial_scale is None:
+        scale_value, scale_t = 1.0, None
+    else:
+        scale_value, scale_t = _scalar_arg(partial_scale, dev, "partial_scale")
+    pv = _rows2d(partial_value)
+    it = _rows2d(interblock_output.to(dtype))
+    lse = interblock_lse.float().reshape(B * T).contiguous()
+    pk = q = pl = None
+    if partial_logit is not None:
+        if partial_logit.numel() != B * T:
+            raise RuntimeError(f"{what}: partial_logit must be [B, T]")
+        pl = partial_logit.reshape(B * T).contiguous()
+    elif partial_key is not None:
+        pk = _rows2d(partial_key.reshape(B, T, -1).to(dtype))
+        q = query.reshape(-1).to(dtype).contiguous()
+        if q.numel() != pk.size(1):
+            raise RuntimeError(f"{what}: query must have {pk.size(1)} elements, got {q.numel()}")
+    else:
+        q = query.reshape(-1).to(dtype).contiguous()
+        if q.numel() != D:
+            raise RuntimeError(f"{what}: query must have {D} elements, got {q.numel()}")
+    out = _phase2_op(pv, pk, q, pl, it, lse, bias_t, scale_t, int(merge), bool(key_norm), bool(normalize_output),
+                     float(logit_scale), bias_value, scale_value, bool(scale_key))
+    return out.view(B, T, D)
+
+
+def attention_residual_phase2(partial_value: Tensor, query: Tensor, interblock_output: Tensor,
+                              interblock_lse: Tensor, key_norm: bool, force_triton: bool = False,
+                              normalize_output: bool = False, logit_bias=0.0, partial_scale=None) -> Tensor:
+    """Merge of the live partial block into a phase-1 read (reference: attnres_ops.py:3964-4019).
+
+    ``prob = sigmoid(<key(partial), query> + logit_bias - lse)``, ``out =
+    inter + (partial - inter) * prob``; ``key = rms_norm(partial)`` when
+    ``key_norm``.  ``partial_scale`` (float or scalar tensor, not in the
+    reference) multiplies the partial value first, which folds the block
+    summary ``partial_block * count**-alpha`` (model.py:990-1001) into the
+    kernel.
+    """
+    return _phase2(partial_value, None, query, None, interblock_output, interblock_lse, _hip.MERGE_ADDCMUL, key_norm,
+                   normalize_output, 1.0, logit_bias, partial_scale, False, "attention_residual_phase2")
+
+
+def attention_residual_phase2_torch(partial_value: Tensor, query: Tensor, interblock_output: Tensor,
+                                    interblock_lse: Tensor, key_norm: bool, normalize_output: bool = False,
+                                    logit_bias=0.0, partial_scale=None) -> Tensor:
+    """Name kept for import compatibility (reference: attnres_ops.py:4022-4040); runs the HIP kernel."""
+    return attention_residual_phase2(partial_value, query, interblock_output, interblock_lse, key_norm,
+                                     normalize_output=normalize_output, logit_bias=logit_bias,
+                                     partial_scale=partial_scale)
+
+
+def attention_residual_phase2_from_logit(partial_value: Tensor, partial_logit: Tensor, interblock_output: Tensor,
+                                         interblock_lse: Tensor, force_triton: bool = False,
+                                         normalize_output: bool = False, partial_scale=None) -> Tensor:
+    """Merge with a precomputed partial logit (reference: attnres_ops.py:4043-4072)."""
+    return _phase2(partial_value, None, None, partial_logit, interblock_output, interblock_lse, _hip.MERGE_ADDCMUL,
+                   False, normalize_output, 1.0, None, partial_scale, False, "attention_residual_phase2_from_logit")
+
+
+def lrid_attention_residual_phase2(partial_value: Tensor, partial_key: Tensor, query: Tensor,
+                                   interblock_output: Tensor, interblock_lse: Tensor, logit_scale: float,
+                                   key_norm: bool, force_triton: bool = False, normalize_output: bool = False,
+                                   logit_bias=0.0, partial_scale=None, scale_key: bool = False) -> Tensor:
+    """LR merge, ``addcmul`` form (reference: attnres_ops.py:4075-4139; single head).
+
+    ``partial_scale`` multiplies the partial value (and, with ``scale_key``,
+    the partial key) first: the LR block source of model.py:1003-1018.
+    """
+    return _phase2(partial_value, partial_key, query, None, interblock_output, interblock_lse, _hip.MERGE_ADDCMUL,
+                   key_norm, normalize_output, logit_scale, logit_bias, partial_scale, scale_key,
+                   "lrid_attention_residual_phase2")
+
+
+def lrid_attention_residual_phase2_torch(partial_value: Tensor, partial_key: Tensor, query: Tensor,
+                                         interblock_output: Tensor, interblock_lse: Tensor, logit_scale: float,
+                                         key_norm: bool, normalize_output: bool = False, logit_bias=0.0,
+                                         partial_scale=None, scale_key: bool = False) -> Tensor:
+    """LR merge, ``torch.lerp`` form (reference: attnres_ops.py:4142-4160), on the HIP kernel."""
+    return _phase2(partial_value, partial_key, query, None, interblock_output, interblock_lse, _hip.MERGE_LERP,
+                   key_norm, normalize_output, logit_scale, logit_bias, partial_scale, scale_key,
+                   "lrid_attention_residual_phase2_torch")

@@ -473,6 +473,359 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     rp.dquery = g->dquery;
     rp.dgate = g->dgate;
     rp.dbias = g->dbias;
+    rp.part_extra = -1;
+    rp.n_extra = 0;
+    rp.dextra = nullptr;
+    err = launch_reduce_partials(d->dtype, rp, st);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
+  }
+  return ATTNRES_OK;
+}
+
+// ====================================================================== phases
+namespace {
+
+struct PhasePlan {
+  int vec, E, cb, ncols, wpt;
+};
+
+// Row geometry of the phase kernels: one 16-byte vector per column when every
+// row is aligned (fp32: two columns per lane), else eight single-element
+// columns per lane; at most 8 waves per token.
+int phase_plan(int dtype, int dim, const void* const* rows, const int64_t* strides, int n_rows, PhasePlan* pl) {
+  const int es = elem_size(dtype);
+  const int EV = 16 / es;
+  bool vec = dim % EV == 0;
+  for (int i = 0; vec && i < n_rows; ++i)
+    vec = (!rows[i] || aligned16(rows[i])) && ((strides[i] * es) % 16 == 0);
+  pl->vec = vec ? 1 : 0;
+  pl->E = vec ? EV : 1;
+  pl->cb = vec ? (es == 4 ? 2 : 1) : 8;
+  pl->ncols = (dim + kWaveSize * pl->E - 1) / (kWaveSize * pl->E);
+  pl->wpt = (pl->ncols + pl->cb - 1) / pl->cb;
+  if (pl->wpt > 8) return fail(ATTNRES_EUNSUPPORTED, "dim=%d exceeds the phase kernels' row width", dim);
+  return ATTNRES_OK;
+}
+
+int check_phase1(const attnres_phase1_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->n_src < 1 || d->n_src > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_src=%d outside [1, %d]", d->n_src, ATTNRES_MAX_SOURCES);
+  if (d->n_q < 1 || d->n_q > ATTNRES_PHASE1_MAX_QUERIES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_q=%d outside [1, %d]", d->n_q, ATTNRES_PHASE1_MAX_QUERIES);
+  if (d->dtype < 0 || d->dtype > 2 || d->logits_dtype < 0 || d->logits_dtype > 2)
+    return fail(ATTNRES_EINVAL, "unknown dtype %d / logits dtype %d", d->dtype, d->logits_dtype);
+  if (d->n_tok < 0) return fail(ATTNRES_EINVAL, "n_tok=%lld < 0", (long long)d->n_tok);
+  if (d->dim < 1 || d->dim > ATTNRES_PHASE_MAX_DIM)
+    return fail(ATTNRES_EUNSUPPORTED, "dim=%d outside [1, %d]", d->dim, ATTNRES_PHASE_MAX_DIM);
+  if (!d->values || !d->value_row_stride) return fail(ATTNRES_EINVAL, "values / value_row_stride is NULL");
+  const bool live = d->n_tok > 0;
+  for (int s = 0; s < d->n_src; ++s) {
+    if (live && !d->values[s]) return fail(ATTNRES_EINVAL, "values[%d] is NULL", s);
+    if (d->value_row_stride[s] < d->dim || d->value_row_stride[s] > INT32_MAX)
+      return fail(ATTNRES_EINVAL, "value_row_stride[%d]=%lld must be in [dim, 2^31)", s,
+                  (long long)d->value_row_stride[s]);
+  }
+  if (live && !d->logits) return fail(ATTNRES_EINVAL, "logits is NULL");
+  if (d->logit_s_stride < d->n_tok || d->logit_q_stride < (int64_t)d->n_src * d->n_tok)
+    return fail(ATTNRES_EINVAL, "logit strides (%lld, %lld) overlap for n_tok=%lld, S=%d", (long long)d->logit_q_stride,
+                (long long)d->logit_s_stride, (long long)d->n_tok, d->n_src);
+  return ATTNRES_OK;
+}
+
+void fill_phase1(const attnres_phase1_desc* d, const PhasePlan& pl, Phase1Params* p) {
+  memset(p, 0, sizeof(*p));
+  for (int s = 0; s < d->n_src; ++s) {
+    p->val[s] = d->values[s];
+    p->vstride[s] = (int32_t)d->value_row_stride[s];
+  }
+  p->logits = d->logits;
+  p->lq = d->logit_q_stride;
+  p->ls = d->logit_s_stride;
+  p->n_tok = d->n_tok;
+  p->n_src = d->n_src;
+  p->n_q = d->n_q;
+  p->D = d->dim;
+  p->ncols = pl.ncols;
+  p->ldt = d->logits_dtype;
+  p->norm_out = d->normalize_output ? 1 : 0;
+  p->np = 1;
+  while (p->np < d->n_src) p->np <<= 1;
+  p->eps = d->norm_eps;
+}
+
+int check_phase2(const attnres_phase2_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->dtype < 0 || d->dtype > 2) return fail(ATTNRES_EINVAL, "unknown dtype %d", d->dtype);
+  if (d->n_tok < 0) return fail(ATTNRES_EINVAL, "n_tok=%lld < 0", (long long)d->n_tok);
+  if (d->dim < 1 || d->dim > ATTNRES_PHASE_MAX_DIM)
+    return fail(ATTNRES_EUNSUPPORTED, "dim=%d outside [1, %d]", d->dim, ATTNRES_PHASE_MAX_DIM);
+  if (d->merge != ATTNRES_MERGE_ADDCMUL && d->merge != ATTNRES_MERGE_LERP)
+    return fail(ATTNRES_EINVAL, "unknown merge %d", d->merge);
+  if (d->rank < 0 || d->rank > 4 * 64 * 8) return fail(ATTNRES_EUNSUPPORTED, "rank=%d outside [0, 2048]", d->rank);
+  const bool live = d->n_tok > 0;
+  if (live && (!d->partial_value || !d->interblock_output || !d->interblock_lse))
+    return fail(ATTNRES_EINVAL, "partial_value / interblock_output / interblock_lse is NULL");
+  if (d->partial_value_row_stride < d->dim || d->partial_value_row_stride > INT32_MAX ||
+      d->interblock_row_stride < d->dim || d->interblock_row_stride > INT32_MAX)
+    return fail(ATTNRES_EINVAL, "row strides must be in [dim, 2^31)");
+  if (d->logit_given) {
+    if (live && !d->partial_logit) return fail(ATTNRES_EINVAL, "logit_given needs partial_logit");
+    if (d->partial_logit_dtype < 0 || d->partial_logit_dtype > 2)
+      return fail(ATTNRES_EINVAL, "unknown partial_logit dtype %d", d->partial_logit_dtype);
+  } else {
+    if (live && !d->query) return fail(ATTNRES_EINVAL, "query is NULL");
+    if (d->rank > 0) {
+      if (live && !d->partial_key) return fail(ATTNRES_EINVAL, "LR merge needs partial_key");
+      if (d->partial_key_row_stride < d->rank) return fail(ATTNRES_EINVAL, "partial_key_row_stride < rank");
+    }
+  }
+  return ATTNRES_OK;
+}
+
+struct P2Layout {
+  int n_part, part_q, n_q, part_bias, part_scale;
+};
+
+P2Layout phase2_layout(const attnres_phase2_desc* d, bool want_q, bool want_bias, bool want_scale) {
+  P2Layout L{0, -1, 0, -1, -1};
+  if (want_q && !d->logit_given) {
+    L.part_q = 0;
+    L.n_q = d->rank > 0 ? d->rank : d->dim;
+    L.n_part = L.n_q;
+  }
+  if (want_bias) L.part_bias = L.n_part++;
+  if (want_scale) {
+    L.part_scale = L.n_part;
+    L.n_part += (d->rank > 0 && d->scale_key && !d->logit_given) ? 2 : 1;
+  }
+  return L;
+}
+
+void fill_phase2(const attnres_phase2_desc* d, const PhasePlan& pl, Phase2Params* p) {
+  memset(p, 0, sizeof(*p));
+  p->pv = d->partial_value;
+  p->pk = d->rank > 0 ? d->partial_key : nullptr;
+  p->q = d->logit_given ? nullptr : d->query;
+  p->plogit = d->logit_given ? d->partial_logit : nullptr;
+  p->inter = d->interblock_output;
+  p->lse = d->interblock_lse;
+  p->bias_dev = d->logit_bias_dev;
+  p->scale_dev = d->value_scale_dev;
+  p->n_tok = d->n_tok;
+  p->pv_stride = d->partial_value_row_stride;
+  p->pk_stride = d->partial_key_row_stride;
+  p->inter_stride = d->interblock_row_stride;
+  p->part_q = p->part_bias = p->part_scale = -1;
+  p->D = d->dim;
+  p->R = d->rank;
+  p->ncols = pl.ncols;
+  p->logit_given = d->logit_given ? 1 : 0;
+  p->merge = d->merge;
+  p->key_norm = d->key_norm ? 1 : 0;
+  p->norm_out = d->normalize_output ? 1 : 0;
+  p->scale_key = (d->rank > 0 && d->scale_key && !d->logit_given) ? 1 : 0;
+  p->pl_dt = d->partial_logit_dtype;
+  p->scale = d->logit_scale;
+  p->eps = d->norm_eps;
+  p->bias = d->logit_bias;
+  p->vscale = d->value_scale;
+}
+
+// waves per phase-2 workgroup: the row's columns, and enough threads for the
+// LR key (four elements per thread)
+int phase2_waves(const attnres_phase2_desc* d, const PhasePlan& pl) {
+  int w = pl.wpt;
+  const int kw = (d->rank + 4 * kWaveSize - 1) / (4 * kWaveSize);
+  return kw > w ? kw : w;
+}
+
+}  // namespace
+
+extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, void* out_prenorm, float* lse,
+                                      float* out_inv_rms, void* stream) {
+  int rc = check_phase1(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!out || !lse) return fail(ATTNRES_EINVAL, "out / lse is NULL");
+  PhasePlan pl;
+  const void* rows[ATTNRES_MAX_SOURCES + 2];
+  int64_t strides[ATTNRES_MAX_SOURCES + 2];
+  for (int s = 0; s < d->n_src; ++s) {
+    rows[s] = d->values[s];
+    strides[s] = d->value_row_stride[s];
+  }
+  rows[d->n_src] = out;
+  rows[d->n_src + 1] = d->normalize_output ? out_prenorm : nullptr;
+  strides[d->n_src] = strides[d->n_src + 1] = d->dim;
+  rc = phase_plan(d->dtype, d->dim, rows, strides, d->n_src + 2, &pl);
+  if (rc) return rc;
+  Phase1Params p;
+  fill_phase1(d, pl, &p);
+  p.out = out;
+  p.out_prenorm = d->normalize_output ? out_prenorm : nullptr;
+  p.lse = lse;
+  p.out_inv_rms = d->normalize_output ? out_inv_rms : nullptr;
+  Launch L;
+  memset(&L, 0, sizeof(L));
+  L.vec = pl.vec;
+  L.wpt = pl.wpt;
+  L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
+  L.lds = (2 * (size_t)d->n_q * d->n_src + 8 * (size_t)pl.wpt) * sizeof(float);
+  if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "phase-1 forward needs %zu bytes of LDS", L.lds);
+  hipError_t err = launch_phase1_forward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void* grad_out, const float* grad_lse,
+                                       const void* out_prenorm, const float* out_inv_rms, void* const* dvalues,
+                                       void* dlogits, void* stream) {
+  int rc = check_phase1(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!grad_out || !dvalues || !dlogits) return fail(ATTNRES_EINVAL, "grad_out / dvalues / dlogits is NULL");
+  if (d->normalize_output && (!out_prenorm || !out_inv_rms))
+    return fail(ATTNRES_EINVAL, "normalize_output backward needs out_prenorm and out_inv_rms");
+  PhasePlan pl;
+  const void* rows[2 * ATTNRES_MAX_SOURCES + 2];
+  int64_t strides[2 * ATTNRES_MAX_SOURCES + 2];
+  int n = 0;
+  for (int s = 0; s < d->n_src; ++s) {
+    if (!dvalues[s]) return fail(ATTNRES_EINVAL, "dvalues[%d] is NULL", s);
+    rows[n] = d->values[s];
+    strides[n++] = d->value_row_stride[s];
+    rows[n] = dvalues[s];
+    strides[n++] = d->dim;
+  }
+  rows[n] = grad_out;
+  strides[n++] = d->dim;
+  rows[n] = d->normalize_output ? out_prenorm : nullptr;
+  strides[n++] = d->dim;
+  rc = phase_plan(d->dtype, d->dim, rows, strides, n, &pl);
+  if (rc) return rc;
+  Phase1Params p;
+  fill_phase1(d, pl, &p);
+  for (int s = 0; s < d->n_src; ++s) p.dval[s] = dvalues[s];
+  p.gout = grad_out;
+  p.glse = grad_lse;
+  p.out_prenorm = d->normalize_output ? const_cast<void*>(out_prenorm) : nullptr;
+  p.out_inv_rms = d->normalize_output ? const_cast<float*>(out_inv_rms) : nullptr;
+  p.dlogits = dlogits;
+  Launch L;
+  memset(&L, 0, sizeof(L));
+  L.vec = pl.vec;
+  L.wpt = pl.wpt;
+  L.nmax = d->n_q <= 4 ? 4 : d->n_q <= 8 ? 8 : ATTNRES_PHASE1_MAX_QUERIES;
+  L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
+  const size_t qn = (size_t)d->n_q * d->n_src;
+  L.lds = (2 * qn + 2 * (size_t)pl.wpt * qn + (size_t)pl.wpt * L.nmax) * sizeof(float);
+  if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "phase-1 backward needs %zu bytes of LDS", L.lds);
+  hipError_t err = launch_phase1_backward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 backward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" size_t attnres_phase2_backward_workspace_size(const attnres_phase2_desc* d) {
+  if (check_phase2(d) != ATTNRES_OK || d->n_tok == 0) return 0;
+  const P2Layout PL = phase2_layout(d, true, true, true);
+  return (size_t)bwd_groups(d->n_tok) * PL.n_part * sizeof(float);
+}
+
+extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, void* stream) {
+  int rc = check_phase2(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!out) return fail(ATTNRES_EINVAL, "out is NULL");
+  PhasePlan pl;
+  const void* rows[4] = {d->partial_value, d->interblock_output, out,
+                         (d->rank == 0 && !d->logit_given) ? d->query : nullptr};
+  const int64_t strides[4] = {d->partial_value_row_stride, d->interblock_row_stride, d->dim, d->dim};
+  rc = phase_plan(d->dtype, d->dim, rows, strides, 4, &pl);
+  if (rc) return rc;
+  Phase2Params p;
+  fill_phase2(d, pl, &p);
+  p.out = out;
+  Launch L;
+  memset(&L, 0, sizeof(L));
+  L.vec = pl.vec;
+  L.wpt = phase2_waves(d, pl);
+  L.nmax = (d->rank > 0 && !d->logit_given) ? 1 : 0;
+  L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
+  L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
+  hipError_t err = launch_phase2_forward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnres_phase2_grads* g, void* stream) {
+  int rc = check_phase2(d);
+  if (rc) return rc;
+  if (!g) return fail(ATTNRES_EINVAL, "grads is NULL");
+  const bool lr = d->rank > 0 && !d->logit_given;
+  hipStream_t st = (hipStream_t)stream;
+  if (d->n_tok == 0) {
+    if (g->dquery && !d->logit_given)
+      (void)hipMemsetAsync(g->dquery, 0, (size_t)(lr ? d->rank : d->dim) * elem_size(d->dtype), st);
+    if (g->dlogit_bias) (void)hipMemsetAsync(g->dlogit_bias, 0, sizeof(float), st);
+    if (g->dvalue_scale) (void)hipMemsetAsync(g->dvalue_scale, 0, sizeof(float), st);
+    return ATTNRES_OK;
+  }
+  if (!g->grad_out || !g->dpartial_value || !g->dinterblock_output || !g->dinterblock_lse)
+    return fail(ATTNRES_EINVAL, "grad_out / dpartial_value / dinterblock_output / dinterblock_lse is NULL");
+  if (lr && !g->dpartial_key) return fail(ATTNRES_EINVAL, "LR merge backward needs dpartial_key");
+  PhasePlan pl;
+  const void* rows[6] = {d->partial_value, d->interblock_output, g->grad_out, g->dpartial_value,
+                         g->dinterblock_output, (d->rank == 0 && !d->logit_given) ? d->query : nullptr};
+  const int64_t strides[6] = {d->partial_value_row_stride, d->interblock_row_stride, d->dim, d->dim, d->dim, d->dim};
+  rc = phase_plan(d->dtype, d->dim, rows, strides, 6, &pl);
+  if (rc) return rc;
+  Phase2Params p;
+  fill_phase2(d, pl, &p);
+  p.gout = g->grad_out;
+  p.dpv = g->dpartial_value;
+  p.dpk = lr ? g->dpartial_key : nullptr;
+  p.dinter = g->dinterblock_output;
+  p.dlse = g->dinterblock_lse;
+  p.dplogit = d->logit_given ? g->dpartial_logit : nullptr;
+  const P2Layout PL = phase2_layout(d, g->dquery != nullptr, g->dlogit_bias != nullptr, g->dvalue_scale != nullptr);
+  const int64_t groups = bwd_groups(d->n_tok);
+  if (PL.n_part > 0) {
+    const size_t need = (size_t)groups * PL.n_part * sizeof(float);
+    if (!g->workspace || g->workspace_bytes < need)
+      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
+                  g->workspace ? g->workspace_bytes : (size_t)0);
+    p.partials = (float*)g->workspace;
+  }
+  p.n_part = PL.n_part;
+  p.part_q = PL.part_q;
+  p.part_bias = PL.part_bias;
+  p.part_scale = PL.part_scale;
+  Launch L;
+  memset(&L, 0, sizeof(L));
+  L.vec = pl.vec;
+  L.wpt = phase2_waves(d, pl);
+  L.nmax = lr ? 1 : 0;
+  L.grid = (int)groups;
+  L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
+  hipError_t err = launch_phase2_backward(d->dtype, p, L, st);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 backward launch failed: %s", hipGetErrorString(err));
+  if (PL.n_part > 0) {
+    ReduceParams rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.partials = p.partials;
+    rp.n_groups = L.grid;
+    rp.n_part = PL.n_part;
+    rp.part_q = PL.part_q;
+    rp.n_q = PL.n_q;
+    rp.part_gate = -1;
+    rp.part_bias = PL.part_bias;
+    rp.n_bias = PL.part_bias >= 0 ? 1 : 0;
+    rp.part_extra = PL.part_scale;
+    rp.n_extra = PL.part_scale >= 0 ? PL.n_part - PL.part_scale : 0;
+    rp.dquery = g->dquery;
+    rp.dbias = g->dlogit_bias;
+    rp.dextra = g->dvalue_scale;
     err = launch_reduce_partials(d->dtype, rp, st);
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
   }

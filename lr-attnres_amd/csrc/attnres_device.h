@@ -178,6 +178,39 @@ __device__ __forceinline__ void store_vec(typename DT::S* __restrict__ p, const 
   }
 }
 
+// E fp32 values (already rounded to DT) back into packed raw words
+template <class DT, int E>
+__device__ __forceinline__ void pack_raw(const float (&x)[E], Raw<DT, E>& r) {
+  if constexpr (sizeof(typename DT::S) == 4) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) r.w[i] = __float_as_uint(x[i]);
+  } else if constexpr (E == 1) {
+    if constexpr (DT::kCode == 1) r.w[0] = __float_as_uint(x[0]) >> 16;
+    else r.w[0] = f32_to_f16_bits(x[0]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+      if constexpr (DT::kCode == 1) r.w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+      else r.w[i] = f32_to_f16_bits(x[2 * i]) | (f32_to_f16_bits(x[2 * i + 1]) << 16);
+    }
+  }
+}
+
+// scalar access to a buffer whose dtype is only known at run time
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int code) {
+  if (code == 0) return ((const float*)p)[i];
+  const uint32_t b = ((const uint16_t*)p)[i];
+  return code == 1 ? __uint_as_float(b << 16) : f16_bits_to_f32(b);
+}
+__device__ __forceinline__ float round_any(float x, int code) {
+  return code == 0 ? x : code == 1 ? round_bf16(x) : round_f16(x);
+}
+__device__ __forceinline__ void store_any(void* p, int64_t i, int code, float x) {
+  if (code == 0) ((float*)p)[i] = x;
+  else if (code == 1) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(x);
+  else ((uint16_t*)p)[i] = (uint16_t)f32_to_f16_bits(x);
+}
+
 // ---------------------------------------------------------------- reductions
 // Butterfly all-reduce over the 64 lanes of a wave (every lane gets the sum;
 // the association order is fixed, so results are deterministic).

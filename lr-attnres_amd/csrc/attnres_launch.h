@@ -29,5 +29,11 @@ hipError_t launch_reduce_partials(int dtype, const ReduceParams& p, hipStream_t 
 hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_lr_fast_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
 size_t lr_fast_table_bytes();  // LDS bytes of the fast kernels' per-source tables
+// cached-logit phases: L.wpt = waves per workgroup; phase-1 backward L.nmax =
+// register slots for the read sites (4, 8 or 16); phase-2 L.nmax = 1 for LR keys
+hipError_t launch_phase1_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
+hipError_t launch_phase1_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
+hipError_t launch_phase2_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
+hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 
 }  // namespace attnres

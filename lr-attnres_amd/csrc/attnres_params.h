@@ -65,9 +65,59 @@ struct ReduceParams {
   int32_t part_q, n_q;        // static query slots
   int32_t part_gate, n_gate;  // per-site gate slots
   int32_t part_bias, n_bias;
+  int32_t part_extra, n_extra;  // further fp32 slots (phase 2: value-scale gradient)
   void* dquery;               // dtype
   void* dgate;                // dtype
   float* dbias;
+  float* dextra;
+};
+
+// Phase 1 (cached-logit read of completed sources for Q read sites)
+constexpr int kPhase1MaxQ = ATTNRES_PHASE1_MAX_QUERIES;
+struct Phase1Params {
+  const void* val[kMaxSources];
+  void* dval[kMaxSources];     // backward: [n_tok, D] dense
+  int32_t vstride[kMaxSources];
+  const void* logits;          // (q, s, t) at q*lq + s*ls + t
+  int64_t lq, ls;
+  void* out;                   // [Q, n_tok, D]
+  void* out_prenorm;           // [Q, n_tok, D] or null
+  float* lse;                  // [Q, n_tok]
+  float* out_inv_rms;          // [Q, n_tok] or null
+  const void* gout;            // backward: [Q, n_tok, D]
+  const float* glse;           // backward: [Q, n_tok] or null
+  void* dlogits;               // backward: [Q, S, n_tok] dense, logits dtype
+  int64_t n_tok;
+  int32_t n_src, n_q, D, ncols;
+  int32_t ldt;                 // logits dtype code
+  int32_t norm_out;
+  int32_t np;                  // lanes per softmax row: next power of two >= n_src
+  float eps;
+};
+
+// Phase 2 (merge of a read site's phase-1 result with the partial block)
+struct Phase2Params {
+  const void* pv;              // partial value rows
+  const void* pk;              // LR partial key rows
+  const void* q;               // [D] or [R]
+  const void* plogit;          // [n_tok] given logits
+  const void* inter;           // interblock output rows
+  const float* lse;            // [n_tok]
+  const float* bias_dev;       // fp32 scalar or null
+  const float* scale_dev;      // fp32 scalar or null
+  void* out;                   // [n_tok, D]
+  const void* gout;            // backward: [n_tok, D]
+  void* dpv;                   // [n_tok, D]
+  void* dpk;                   // [n_tok, R]
+  void* dinter;                // [n_tok, D]
+  float* dlse;                 // [n_tok]
+  void* dplogit;               // [n_tok]
+  float* partials;             // [gridDim.x, n_part]
+  int64_t n_tok, pv_stride, pk_stride, inter_stride;
+  int32_t n_part, part_q, part_bias, part_scale;  // slot offsets (-1 = unused)
+  int32_t D, R, ncols;
+  int32_t logit_given, merge, key_norm, norm_out, scale_key, pl_dt;
+  float scale, eps, bias, vscale;
 };
 
 }  // namespace attnres

@@ -1,0 +1,436 @@
+// Phase 2 of the cached-logit block-training schedule: merge of one read
+// site's phase-1 result (interblock output + its log-sum-exp) with the live
+// partial block.  Forward and backward, base and LR keys, or a given logit.
+//
+// Semantics follow the reference's eager merges at the same rounding points
+// (attnres_ops.py:2630-2642, 4041-4068, 4085-4160):
+//   p     = rnd(partial * value_scale)          block summary (model.py:990-1018)
+//   key   = base: key_norm ? rnd(p / rms(p)) : p
+//           LR:   key_norm ? rnd(k / rms(k)) : k   (k = partial key, fp32 norm)
+//   logit = rnd(sum_i rnd(key_i * q_i))          torch.sum(key * query)
+//           LR: rnd(logit * logit_scale)
+//   prob  = rnd(sigmoid(logit + bias - lse))     fp32 sigmoid
+//   out   = addcmul: rnd(inter + rnd(p - inter) * prob)
+//           lerp:    rnd(torch.lerp(inter, p, prob))
+//   optional out = rnd(out / rms(out))
+// The backward recomputes these per token and follows the autograd graph of
+// the same expressions (every dtype-tensor product rounded, fp32 sigmoid and
+// norm backward).  Cross-token sums (query, learned bias and scale) go to
+// per-workgroup partial rows, reduced in a fixed order afterwards.
+//
+// One workgroup of wpt waves owns one token at a time; a lane owns CB vectors
+// of E elements of the D-wide rows, and thread t owns LR key elements
+// t + j * blockDim (j < kP2KPT).
+#include "attnres_block.h"
+#include "attnres_device.h"
+#include "attnres_launch.h"
+#include "attnres_params.h"
+
+namespace attnres {
+
+constexpr int kP2KPT = 4;  // LR key elements per thread
+
+// Per-token forward state shared by both kernels.
+template <int CB, int E>
+struct P2State {
+  float p[CB][E];    // scaled partial value (dtype-rounded)
+  float pr[CB][E];   // partial value as loaded
+  float it[CB][E];   // interblock output
+  float key[CB][E];  // base key (dtype-rounded)
+  float kl[kP2KPT];  // LR key (dtype-rounded)
+  float kv[kP2KPT];  // LR key before the norm (scaled)
+  float kr[kP2KPT];  // LR key as loaded
+  float inv_key;     // 1/rms of the key (key_norm)
+  float sg, prob;    // sigmoid and its dtype-rounded value
+};
+
+template <class DT, int E, int CB, bool LR>
+__device__ __forceinline__ void p2_token(const Phase2Params& p, int64_t tok, const float (&qv)[CB][E],
+                                         const float (&qk)[kP2KPT], float vs, float bias, const Cols<CB, E>& cl,
+                                         float* s_red, int tid, int lane, int wave, int wpt, P2State<CB, E>& st) {
+  using S = typename DT::S;
+  const int D = p.D, bd = blockDim.x;
+  const S* pvp = (const S*)p.pv + tok * p.pv_stride;
+  const S* itp = (const S*)p.inter + tok * p.inter_stride;
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    if (cl.ok[c]) {
+      load_vec<DT, E>(pvp + cl.eoff[c], st.pr[c]);
+      load_vec<DT, E>(itp + cl.eoff[c], st.it[c]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) st.pr[c][e] = st.it[c][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) st.p[c][e] = DT::rnd(st.pr[c][e] * vs);
+  }
+  if (LR) {
+    const S* kp = (const S*)p.pk + tok * p.pk_stride;
+#pragma unroll
+    for (int j = 0; j < kP2KPT; ++j) {
+      const int r = tid + j * bd;
+      st.kr[j] = (!p.logit_given && r < p.R) ? DT::load1(kp + r) : 0.f;
+    }
+  }
+  const float lse = p.lse[tok];
+
+  float logit;
+  if (p.logit_given) {
+    logit = load_any(p.plogit, tok, p.pl_dt);
+  } else if (LR) {
+#pragma unroll
+    for (int j = 0; j < kP2KPT; ++j) st.kv[j] = p.scale_key ? DT::rnd(st.kr[j] * vs) : st.kr[j];
+    st.inv_key = 1.f;
+    if (p.key_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kP2KPT; ++j) ss += st.kv[j] * st.kv[j];
+      ss = block_sum1(ss, s_red, lane, wave, wpt);
+      st.inv_key = 1.0f / sqrtf(ss / (float)p.R + p.eps);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < kP2KPT; ++j) {
+      st.kl[j] = p.key_norm ? DT::rnd(st.kv[j] * st.inv_key) : st.kv[j];
+      dot += DT::rnd(st.kl[j] * qk[j]);
+    }
+    dot = block_sum1(dot, s_red, lane, wave, wpt);
+    logit = DT::rnd(DT::rnd(dot) * p.scale);
+  } else {
+    st.inv_key = 1.f;
+    if (p.key_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += st.p[c][e] * st.p[c][e];
+      ss = block_sum1(ss, s_red, lane, wave, wpt);
+      st.inv_key = 1.0f / sqrtf(ss / (float)D + p.eps);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        st.key[c][e] = p.key_norm ? DT::rnd(st.p[c][e] * st.inv_key) : st.p[c][e];
+        dot += DT::rnd(st.key[c][e] * qv[c][e]);
+      }
+    logit = DT::rnd(block_sum1(dot, s_red, lane, wave, wpt));
+  }
+  const float x = (logit + bias) - lse;
+  st.sg = 1.0f / (1.0f + expf(-x));
+  st.prob = DT::rnd(st.sg);
+}
+
+// merged output (dtype-rounded, before the optional norm)
+template <class DT, int E, int CB>
+__device__ __forceinline__ void p2_merge(const Phase2Params& p, const P2State<CB, E>& st, float (&o)[CB][E]) {
+  const float w = st.prob;
+#pragma unroll
+  for (int c = 0; c < CB; ++c)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float a = st.it[c][e], b = st.p[c][e];
+      if (p.merge == ATTNRES_MERGE_LERP) o[c][e] = DT::rnd(fabsf(w) < 0.5f ? a + w * (b - a) : b - (b - a) * (1.0f - w));
+      else o[c][e] = DT::rnd(a + DT::rnd(b - a) * w);
+    }
+}
+
+// ============================================================== forward
+template <class DT, int E, int CB, bool LR>
+__global__ void __launch_bounds__(512) phase2_fwd_kernel(const Phase2Params p) {
+  using S = typename DT::S;
+  extern __shared__ float smem[];
+  float* s_red = smem;  // [wpt]
+  const int D = p.D, bd = blockDim.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave, wpt = bd / kWave;
+  const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
+  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float bias = p.bias_dev ? *p.bias_dev : p.bias;
+
+  float qv[CB][E], qk[kP2KPT];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    if (!LR && !p.logit_given && cl.ok[c]) load_vec<DT, E>((const S*)p.q + cl.eoff[c], qv[c]);
+    else
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[c][e] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < kP2KPT; ++j) {
+    const int r = tid + j * bd;
+    qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
+  }
+
+  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    P2State<CB, E> st;
+    p2_token<DT, E, CB, LR>(p, tok, qv, qk, vs, bias, cl, s_red, tid, lane, wave, wpt, st);
+    float o[CB][E];
+    p2_merge<DT, E, CB>(p, st, o);
+    if (p.norm_out) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += o[c][e] * o[c][e];
+      ss = block_sum1(ss, s_red, lane, wave, wpt);
+      const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[c][e] = DT::rnd(o[c][e] * inv);
+    }
+    S* op = (S*)p.out + tok * (int64_t)D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+      if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], o[c]);
+  }
+}
+
+// ============================================================== backward
+template <class DT, int E, int CB, bool LR>
+__global__ void __launch_bounds__(512) phase2_bwd_kernel(const Phase2Params p) {
+  using S = typename DT::S;
+  extern __shared__ float smem[];
+  float* s_red = smem;  // [wpt]
+  const int D = p.D, bd = blockDim.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave, wpt = bd / kWave;
+  const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
+  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float bias = p.bias_dev ? *p.bias_dev : p.bias;
+
+  float qv[CB][E], qk[kP2KPT];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    if (!LR && !p.logit_given && cl.ok[c]) load_vec<DT, E>((const S*)p.q + cl.eoff[c], qv[c]);
+    else
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[c][e] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < kP2KPT; ++j) {
+    const int r = tid + j * bd;
+    qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
+  }
+  float dq_b[CB][E], dq_l[kP2KPT];
+#pragma unroll
+  for (int c = 0; c < CB; ++c)
+#pragma unroll
+    for (int e = 0; e < E; ++e) dq_b[c][e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < kP2KPT; ++j) dq_l[j] = 0.f;
+  float acc_bias = 0.f, acc_sv = 0.f, acc_sk = 0.f;  // bias, value-scale and key-scale gradient sums
+
+  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    P2State<CB, E> st;
+    p2_token<DT, E, CB, LR>(p, tok, qv, qk, vs, bias, cl, s_red, tid, lane, wave, wpt, st);
+    float G[CB][E];
+    const S* gp = (const S*)p.gout + tok * (int64_t)D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      if (cl.ok[c]) load_vec<DT, E>(gp + cl.eoff[c], G[c]);
+      else
+#pragma unroll
+        for (int e = 0; e < E; ++e) G[c][e] = 0.f;
+    }
+    if (p.norm_out) {
+      // G <- rms-norm backward from the recomputed pre-norm output o
+      float o[CB][E];
+      p2_merge<DT, E, CB>(p, st, o);
+      float a[2] = {0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          a[0] += o[c][e] * o[c][e];
+          a[1] += G[c][e] * o[c][e];
+        }
+      block_allreduce<2>(a, 2, s_red, lane, wave, wpt);
+      const float inv = 1.0f / sqrtf(a[0] / (float)D + p.eps);
+      const float k3 = inv * inv * inv * (a[1] / (float)D);
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) G[c][e] = cl.ok[c] ? DT::rnd(inv * G[c][e] - o[c][e] * k3) : 0.f;
+    }
+
+    // merge backward: gradients of the interblock output and of p through the
+    // merge, and the per-element terms of d prob
+    float dint[CB][E], dpm[CB][E];
+    float dprob = 0.f;
+    const float w = st.prob;
+    const float omw = DT::rnd(1.0f - w);
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float diff = DT::rnd(st.p[c][e] - st.it[c][e]);
+        if (p.merge == ATTNRES_MERGE_LERP) {
+          dint[c][e] = DT::rnd(G[c][e] * omw);
+          dpm[c][e] = DT::rnd(G[c][e] * w);
+        } else {
+          dpm[c][e] = DT::rnd(G[c][e] * w);
+          dint[c][e] = DT::rnd(G[c][e] - dpm[c][e]);
+        }
+        dprob += DT::rnd(G[c][e] * diff);
+      }
+    dprob = DT::rnd(block_sum1(dprob, s_red, lane, wave, wpt));
+    const float dx = dprob * (1.0f - st.sg) * st.sg;
+    if (tid == 0) {
+      p.dlse[tok] = -dx;
+      acc_bias += dx;
+      if (p.logit_given && p.dplogit) store_any(p.dplogit, tok, p.pl_dt, round_any(dx, p.pl_dt));
+    }
+
+    float dpk[CB][E];  // base: gradient of p through the key
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) dpk[c][e] = 0.f;
+    if (!p.logit_given) {
+      const float dlb = DT::rnd(dx);
+      if (LR) {
+        const float dsum = DT::rnd(dlb * p.scale);
+        float dk[kP2KPT];
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < kP2KPT; ++j) {
+          const bool in = tid + j * bd < p.R;
+          dk[j] = in ? DT::rnd(dsum * qk[j]) : 0.f;
+          if (in) dq_l[j] += DT::rnd(dsum * st.kl[j]);
+          dot += dk[j] * st.kv[j];
+        }
+        if (p.key_norm) {
+          dot = block_sum1(dot, s_red, lane, wave, wpt);
+          const float iv = st.inv_key;
+          const float k3 = iv * iv * iv * (dot / (float)p.R);
+#pragma unroll
+          for (int j = 0; j < kP2KPT; ++j) dk[j] = DT::rnd(iv * dk[j] - st.kv[j] * k3);
+        }
+        S* dkp = (S*)p.dpk + tok * (int64_t)p.R;
+#pragma unroll
+        for (int j = 0; j < kP2KPT; ++j) {
+          const int r = tid + j * bd;
+          if (r < p.R) {
+            float g = dk[j];
+            if (p.scale_key) {
+              acc_sk += DT::rnd(g * st.kr[j]);
+              g = DT::rnd(g * vs);
+            }
+            DT::store1(dkp + r, g);
+          }
+        }
+      } else {
+        float dot = 0.f;
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const float dk = DT::rnd(dlb * qv[c][e]);
+            if (cl.ok[c]) dq_b[c][e] += DT::rnd(dlb * st.key[c][e]);
+            dpk[c][e] = dk;
+            dot += dk * st.p[c][e];
+          }
+        if (p.key_norm) {
+          dot = block_sum1(dot, s_red, lane, wave, wpt);
+          const float iv = st.inv_key;
+          const float k3 = iv * iv * iv * (dot / (float)D);
+#pragma unroll
+          for (int c = 0; c < CB; ++c)
+#pragma unroll
+            for (int e = 0; e < E; ++e) dpk[c][e] = DT::rnd(iv * dpk[c][e] - st.p[c][e] * k3);
+        }
+      }
+    }
+
+    S* dpvp = (S*)p.dpv + tok * (int64_t)D;
+    S* dip = (S*)p.dinter + tok * (int64_t)D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      float dp[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float g = (!LR && !p.logit_given) ? DT::rnd(dpm[c][e] + dpk[c][e]) : dpm[c][e];
+        if (cl.ok[c]) acc_sv += DT::rnd(g * st.pr[c][e]);
+        dp[e] = DT::rnd(g * vs);
+      }
+      if (cl.ok[c]) {
+        store_vec<DT, E>(dpvp + cl.eoff[c], dp);
+        store_vec<DT, E>(dip + cl.eoff[c], dint[c]);
+      }
+    }
+  }
+
+  // this workgroup's partial sums
+  float* part = p.partials ? p.partials + (int64_t)blockIdx.x * p.n_part : nullptr;
+  if (part && p.part_q >= 0) {
+    if (LR) {
+#pragma unroll
+      for (int j = 0; j < kP2KPT; ++j) {
+        const int r = tid + j * bd;
+        if (r < p.R) part[p.part_q + r] = dq_l[j];
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+        if (cl.ok[c])
+#pragma unroll
+          for (int e = 0; e < E; ++e) part[p.part_q + cl.eoff[c] + e] = dq_b[c][e];
+    }
+  }
+  if (part && p.part_bias >= 0 && tid == 0) part[p.part_bias] = acc_bias;
+  if (part && p.part_scale >= 0) {
+    // the value and key products are separate autograd edges of the scale:
+    // kept apart so that each sum is rounded to the dtype on its own
+    float a[2] = {acc_sv, acc_sk};
+    block_allreduce<2>(a, 2, s_red, lane, wave, wpt);
+    if (tid == 0) {
+      part[p.part_scale] = a[0];
+      if (p.scale_key) part[p.part_scale + 1] = a[1];
+    }
+  }
+}
+
+// ============================================================== launchers
+template <class DT, bool LR>
+static hipError_t phase2_fwd_t(const Phase2Params& p, const Launch& L, hipStream_t st) {
+  constexpr int EV = 16 / sizeof(typename DT::S);
+  constexpr int CBV = sizeof(typename DT::S) == 4 ? 2 : 1;
+  const dim3 g(L.grid), b(L.wpt * kWave);
+  if (L.vec) hipLaunchKernelGGL((phase2_fwd_kernel<DT, EV, CBV, LR>), g, b, L.lds, st, p);
+  else hipLaunchKernelGGL((phase2_fwd_kernel<DT, 1, 8, LR>), g, b, L.lds, st, p);
+  return hipGetLastError();
+}
+template <class DT, bool LR>
+static hipError_t phase2_bwd_t(const Phase2Params& p, const Launch& L, hipStream_t st) {
+  constexpr int EV = 16 / sizeof(typename DT::S);
+  constexpr int CBV = sizeof(typename DT::S) == 4 ? 2 : 1;
+  const dim3 g(L.grid), b(L.wpt * kWave);
+  if (L.vec) hipLaunchKernelGGL((phase2_bwd_kernel<DT, EV, CBV, LR>), g, b, L.lds, st, p);
+  else hipLaunchKernelGGL((phase2_bwd_kernel<DT, 1, 8, LR>), g, b, L.lds, st, p);
+  return hipGetLastError();
+}
+template <class DT>
+static hipError_t phase2_fwd_dt(const Phase2Params& p, const Launch& L, hipStream_t st) {
+  return L.nmax ? phase2_fwd_t<DT, true>(p, L, st) : phase2_fwd_t<DT, false>(p, L, st);
+}
+template <class DT>
+static hipError_t phase2_bwd_dt(const Phase2Params& p, const Launch& L, hipStream_t st) {
+  return L.nmax ? phase2_bwd_t<DT, true>(p, L, st) : phase2_bwd_t<DT, false>(p, L, st);
+}
+
+#define ATTNRES_P2_DISPATCH(dtype, fn, ...)                \
+  switch (dtype) {                                         \
+    case ATTNRES_DTYPE_F32: return fn<F32>(__VA_ARGS__);   \
+    case ATTNRES_DTYPE_BF16: return fn<BF16>(__VA_ARGS__); \
+    default: return fn<F16>(__VA_ARGS__);                  \
+  }
+
+hipError_t launch_phase2_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st) {
+  ATTNRES_P2_DISPATCH(dtype, phase2_fwd_dt, p, L, st);
+}
+hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st) {
+  ATTNRES_P2_DISPATCH(dtype, phase2_bwd_dt, p, L, st);
+}
+
+}  // namespace attnres

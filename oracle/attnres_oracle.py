@@ -39,7 +39,9 @@ attention_residual_average_read_ref       closed form (mean) and fp64
 gated_query_ref                           closed form (zero gate -> static)
 block_* helpers                           the reference tests' known answers
 phase1_from_logits_ref / phase2_*_ref     phase1+phase2 == full read identity
-                                          (tests/test_attnres_ops.py:582-610)
+                                          (tests/test_attnres_ops.py:582-610),
+                                          golden fixtures with gradients,
+                                          fp64 gradcheck
 ========================================  ======================================
 """
 
@@ -340,8 +342,14 @@ def attention_residual_phase2_ref(partial_value: Tensor, query: Tensor, interblo
 def lrid_attention_residual_phase2_ref(partial_value: Tensor, partial_key: Tensor, query: Tensor,
                                        interblock_output: Tensor, interblock_lse: Tensor,
                                        logit_scale: float, key_norm: bool, normalize_output: bool = False,
-                                       logit_bias=0.0) -> Tensor:
-    """LR two-way merge, ``attnres_ops.py:4142-4160`` (single head)."""
+                                       logit_bias=0.0, merge: str = "lerp") -> Tensor:
+    """LR two-way merge (single head).
+
+    ``merge="lerp"`` is ``lrid_attention_residual_phase2_torch``
+    (``attnres_ops.py:4142-4160``); ``merge="addcmul"`` is the eager path of
+    ``lrid_attention_residual_phase2`` (``:4085-4139``), which hands the logit
+    to ``attention_residual_phase2_from_logit`` (``:4041-4068``).
+    """
     q = query.reshape(-1).to(partial_key.dtype)
     pk = partial_key.reshape(partial_key.size(0), partial_key.size(1), -1)
     key = norm(pk.float()).to(partial_value.dtype) if key_norm else pk
@@ -351,8 +359,19 @@ def lrid_attention_residual_phase2_ref(partial_value: Tensor, partial_key: Tenso
         logit = logit + logit_bias.to(device=logit.device, dtype=torch.float32)
     elif float(logit_bias) != 0.0:
         logit = logit + float(logit_bias)
+    if merge == "addcmul":
+        return phase2_from_logit_ref(partial_value, logit, interblock_output, interblock_lse,
+                                     normalize_output=normalize_output)
     prob = torch.sigmoid(logit - interblock_lse.float()).to(partial_value.dtype)
     out = torch.lerp(interblock_output, partial_value, prob.unsqueeze(-1))
+    return norm(out) if normalize_output else out
+
+
+def phase2_from_logit_ref(partial_value: Tensor, partial_logit: Tensor, interblock_output: Tensor,
+                          interblock_lse: Tensor, normalize_output: bool = False) -> Tensor:
+    """Merge with a given partial logit, ``attnres_ops.py:4041-4068`` (eager branch)."""
+    prob = torch.sigmoid(partial_logit.float() - interblock_lse.float()).to(partial_value.dtype)
+    out = torch.addcmul(interblock_output, partial_value - interblock_output, prob.unsqueeze(-1))
     return norm(out) if normalize_output else out
 
 

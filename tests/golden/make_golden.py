@@ -134,6 +134,83 @@ def phase_case(ref, name, seed, dtype, B, T, D, S, Q):
                   "lrid_phase2_out": lp2}, meta
 
 
+def phase1_case(ref, name, seed, dtype, logits_dtype, B, T, D, S, Q, normalize_output):
+    """``attention_residual_phase1_from_logits`` (eager branch) with its gradients."""
+    gen = torch.Generator().manual_seed(seed)
+    dt = DT[dtype]
+    values = _randn(gen, (S, B, T, D), dt)
+    logits = _randn(gen, (Q, S, B, T), DT[logits_dtype], 1.5)
+    g = _randn(gen, (Q, B, T, D), dt)
+    glse = _randn(gen, (Q, B, T), torch.float32)
+    v = values.clone().requires_grad_(True)
+    lg = logits.clone().requires_grad_(True)
+    out, lse = ref.attention_residual_phase1_from_logits(v, lg, normalize_output=normalize_output)
+    torch.autograd.backward([out, lse], [g, glse])
+    meta = dict(kind="phase1", dtype=dtype, logits_dtype=logits_dtype, B=B, T=T, D=D, S=S, Q=Q,
+                normalize_output=normalize_output, seed=seed)
+    return name, {"values": values, "logits": logits, "grad_out": g, "grad_lse": glse, "out": out.detach(),
+                  "lse": lse.detach(), "dvalues": v.grad, "dlogits": lg.grad}, meta
+
+
+def phase2_case(ref, name, seed, dtype, B, T, D, variant, key_norm=True, bias=None, bias_tensor=False,
+                normalize_output=False, R=16, scale=0.25):
+    """Phase-2 merges with gradients.
+
+    variant: "base" = ``attention_residual_phase2_torch`` (:4023),
+    "lrid" = ``lrid_attention_residual_phase2_torch`` (:4142),
+    "lrid_addcmul" = ``lrid_attention_residual_phase2`` (:4085; eager on CPU),
+    "logit" = ``attention_residual_phase2_from_logit`` (:4041; eager on CPU).
+    """
+    gen = torch.Generator().manual_seed(seed)
+    dt = DT[dtype]
+    partial = _randn(gen, (B, T, D), dt)
+    inter = _randn(gen, (B, T, D), dt)
+    lse = _randn(gen, (B, T), torch.float32)
+    g = _randn(gen, (B, T, D), dt)
+    tensors = {"partial": partial, "inter": inter, "lse": lse, "grad_out": g}
+    p = partial.clone().requires_grad_(True)
+    it = inter.clone().requires_grad_(True)
+    ls = lse.clone().requires_grad_(True)
+    b = bias if bias is not None else 0.0
+    bt = None
+    if bias is not None and bias_tensor:
+        bt = torch.tensor(float(bias), dtype=torch.float32).requires_grad_(True)
+        b = bt
+    if variant == "base":
+        query = _randn(gen, (D,), dt, 0.5)
+        q = query.clone().requires_grad_(True)
+        out = ref.attention_residual_phase2_torch(p, q, it, ls, key_norm, normalize_output=normalize_output,
+                                                  logit_bias=b)
+        tensors["query"] = query
+    elif variant in ("lrid", "lrid_addcmul"):
+        pkey = _randn(gen, (B, T, R), dt)
+        query = _randn(gen, (1, R), dt, 0.5)
+        k = pkey.clone().requires_grad_(True)
+        q = query.clone().requires_grad_(True)
+        fn = ref.lrid_attention_residual_phase2_torch if variant == "lrid" else ref.lrid_attention_residual_phase2
+        out = fn(p, k, q, it, ls, scale, key_norm, normalize_output=normalize_output, logit_bias=b)
+        tensors.update(partial_key=pkey, query=query)
+    else:
+        logit = _randn(gen, (B, T), torch.float32, 2.0)
+        q = logit.clone().requires_grad_(True)
+        out = ref.attention_residual_phase2_from_logit(p, q, it, ls, normalize_output=normalize_output)
+        tensors["logit"] = logit
+    out.backward(g)
+    tensors.update(out=out.detach(), dpartial=p.grad, dinter=it.grad, dlse=ls.grad)
+    if variant == "logit":
+        tensors["dlogit"] = q.grad
+    else:
+        tensors["dquery"] = q.grad
+    if variant in ("lrid", "lrid_addcmul"):
+        tensors["dpartial_key"] = k.grad
+    if bt is not None:
+        tensors["dbias"] = bt.grad.reshape(1)
+    meta = dict(kind="phase2", variant=variant, dtype=dtype, B=B, T=T, D=D, R=R, scale=scale, key_norm=key_norm,
+                bias=0.0 if bias is None else float(bias), bias_tensor=bt is not None,
+                normalize_output=normalize_output, seed=seed)
+    return name, tensors, meta
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
@@ -167,6 +244,24 @@ def main():
         average_case(ref, "avg_bf16", 301, "bf16", 2, 3, 64, 5, False),
         average_case(ref, "avg_fp32_norm", 302, "fp32", 1, 4, 32, 3, True),
         phase_case(ref, "phase_fp32", 401, "fp32", 2, 3, 32, 4, 3),
+        phase1_case(ref, "p1_fp32", 411, "fp32", "fp32", 2, 3, 32, 4, 3, False),
+        phase1_case(ref, "p1_bf16_f32logits", 412, "bf16", "fp32", 2, 3, 64, 5, 4, False),
+        phase1_case(ref, "p1_bf16_bf16logits", 413, "bf16", "bf16", 1, 4, 64, 3, 2, False),
+        phase1_case(ref, "p1_bf16_normout", 414, "bf16", "fp32", 1, 4, 128, 6, 3, True),
+        phase1_case(ref, "p1_fp16", 415, "fp16", "fp32", 1, 3, 64, 4, 5, False),
+        phase2_case(ref, "p2_base_bf16_kn", 421, "bf16", 2, 3, 64, "base"),
+        phase2_case(ref, "p2_base_bf16_nokn_bias", 422, "bf16", 1, 4, 64, "base", key_norm=False, bias=0.693),
+        phase2_case(ref, "p2_base_fp32_tbias_norm", 423, "fp32", 1, 4, 32, "base", bias=0.4, bias_tensor=True,
+                    normalize_output=True),
+        phase2_case(ref, "p2_base_bf16_tbias", 424, "bf16", 2, 3, 64, "base", bias=1.1, bias_tensor=True),
+        phase2_case(ref, "p2_lrid_bf16", 431, "bf16", 2, 3, 64, "lrid"),
+        phase2_case(ref, "p2_lrid_bf16_bias_norm", 432, "bf16", 1, 4, 128, "lrid", bias=0.693, bias_tensor=True,
+                    normalize_output=True, R=32, scale=0.125),
+        phase2_case(ref, "p2_lrid_fp32_nokn", 433, "fp32", 1, 4, 32, "lrid", key_norm=False),
+        phase2_case(ref, "p2_lridadd_bf16", 434, "bf16", 2, 3, 64, "lrid_addcmul"),
+        phase2_case(ref, "p2_lridadd_bf16_bias", 435, "bf16", 1, 4, 64, "lrid_addcmul", bias=0.5),
+        phase2_case(ref, "p2_logit_bf16", 441, "bf16", 2, 3, 64, "logit"),
+        phase2_case(ref, "p2_logit_fp16_norm", 442, "fp16", 1, 4, 64, "logit", normalize_output=True),
     ]
     index = {}
     for name, tensors, meta in cases:

@@ -22,7 +22,7 @@ import attnres_ops as ops  # noqa: E402
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(attnres_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(attnres_[a-z0-9_]+)\s*\(", text)))
 
 
 needs_lib = pytest.mark.skipif(not os.path.exists(H.LIB_PATH), reason="libattnres_hip.so not built")
@@ -33,7 +33,9 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(H.LIB_PATH)
     names = _declared_functions()
     assert names == sorted(["attnres_abi_version", "attnres_last_error", "attnres_read_backward",
-                            "attnres_read_backward_workspace_size", "attnres_read_forward"])
+                            "attnres_read_backward_workspace_size", "attnres_read_forward",
+                            "attnres_phase1_forward", "attnres_phase1_backward", "attnres_phase2_forward",
+                            "attnres_phase2_backward", "attnres_phase2_backward_workspace_size"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -44,24 +46,30 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 2
+    assert lib.attnres_abi_version() == 3
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()
+    assert lib.attnres_phase1_forward(None, None, None, None, None, None) == -1
+    assert lib.attnres_phase2_forward(None, None, None) == -1
+    assert b"desc is NULL" in lib.attnres_last_error()
+
+
+STRUCTS = ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads"),
+           (H.Phase1Desc, "attnres_phase1_desc"), (H.Phase2Desc, "attnres_phase2_desc"),
+           (H.Phase2Grads, "attnres_phase2_grads"))
 
 
 def _c_layout():
-    """offsetof / sizeof of the two structs, from a C compile of the header."""
+    """offsetof / sizeof of the C-ABI structs, from a C compile of the header."""
     src = r'''
 #include <stdio.h>
 #include <stddef.h>
 #include "attnres_hip.h"
 #define P(s, f) printf(#s " " #f " %zu\n", offsetof(s, f));
 int main(void) {
-  printf("attnres_read_desc sizeof %zu\n", sizeof(attnres_read_desc));
-  printf("attnres_read_grads sizeof %zu\n", sizeof(attnres_read_grads));
-''' + "".join(f"  P(attnres_read_desc, {f})\n" for f, _ in H.ReadDesc._fields_) + \
-        "".join(f"  P(attnres_read_grads, {f})\n" for f, _ in H.ReadGrads._fields_) + "  return 0;\n}\n"
+''' + "".join(f'  printf("{n} sizeof %zu\\n", sizeof({n}));\n' for _, n in STRUCTS) + \
+        "".join(f"  P({n}, {f})\n" for cls, n in STRUCTS for f, _ in cls._fields_) + "  return 0;\n}\n"
     import tempfile
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "p.c")
@@ -78,7 +86,7 @@ int main(void) {
 
 def test_ctypes_structs_match_the_header():
     lay = _c_layout()
-    for cls, name in ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads")):
+    for cls, name in STRUCTS:
         assert ctypes.sizeof(cls) == lay[(name, "sizeof")]
         for f, _ in cls._fields_:
             assert getattr(cls, f).offset == lay[(name, f)], (name, f)

@@ -102,3 +102,60 @@ def test_phase_oracle_matches_reference_vectors(name):
     lp2 = O.lrid_attention_residual_phase2_ref(t["partial"], t["partial_key"], t["lrid_query"], out[0], lse[0],
                                                0.25, True)
     _close(lp2, t["lrid_phase2_out"], m["dtype"])
+
+
+def _phase2_oracle(t, m, dev="cpu"):
+    """Run the oracle's phase-2 merge on a golden case; returns (out, grads dict)."""
+    p = t["partial"].to(dev).clone().requires_grad_(True)
+    it = t["inter"].to(dev).clone().requires_grad_(True)
+    ls = t["lse"].to(dev).clone().requires_grad_(True)
+    bias = m["bias"]
+    bt = None
+    if m["bias_tensor"] and m["variant"] != "logit":
+        bt = torch.tensor(bias, dtype=torch.float32, device=dev).requires_grad_(True)
+        bias = bt
+    grads = {}
+    if m["variant"] == "base":
+        q = t["query"].to(dev).clone().requires_grad_(True)
+        out = O.attention_residual_phase2_ref(p, q, it, ls, m["key_norm"], logit_bias=bias,
+                                              normalize_output=m["normalize_output"])
+    elif m["variant"] in ("lrid", "lrid_addcmul"):
+        k = t["partial_key"].to(dev).clone().requires_grad_(True)
+        q = t["query"].to(dev).clone().requires_grad_(True)
+        out = O.lrid_attention_residual_phase2_ref(p, k, q, it, ls, m["scale"], m["key_norm"],
+                                                   normalize_output=m["normalize_output"], logit_bias=bias,
+                                                   merge="lerp" if m["variant"] == "lrid" else "addcmul")
+    else:
+        q = t["logit"].to(dev).clone().requires_grad_(True)
+        out = O.phase2_from_logit_ref(p, q, it, ls, normalize_output=m["normalize_output"])
+    out.backward(t["grad_out"].to(dev))
+    grads.update(dpartial=p.grad, dinter=it.grad, dlse=ls.grad)
+    grads["dlogit" if m["variant"] == "logit" else "dquery"] = q.grad
+    if m["variant"] in ("lrid", "lrid_addcmul"):
+        grads["dpartial_key"] = k.grad
+    if bt is not None:
+        grads["dbias"] = bt.grad.reshape(1)
+    return out.detach(), grads
+
+
+@pytest.mark.parametrize("name", names("phase1"))
+def test_phase1_oracle_matches_reference_vectors(name):
+    t, m = load(name)
+    v = t["values"].clone().requires_grad_(True)
+    lg = t["logits"].clone().requires_grad_(True)
+    out, lse = O.phase1_from_logits_ref(v, lg, normalize_output=m["normalize_output"])
+    torch.autograd.backward([out, lse], [t["grad_out"], t["grad_lse"]])
+    _close(out.detach(), t["out"], m["dtype"])
+    _close(lse.detach(), t["lse"], "fp32")
+    _close(v.grad, t["dvalues"], m["dtype"])
+    _close(lg.grad, t["dlogits"], m["logits_dtype"])
+
+
+@pytest.mark.parametrize("name", names("phase2"))
+def test_phase2_oracle_matches_reference_vectors(name):
+    t, m = load(name)
+    out, grads = _phase2_oracle(t, m)
+    _close(out, t["out"], m["dtype"])
+    for key, g in grads.items():
+        ref_dtype = "fp32" if key in ("dlse", "dbias", "dlogit") else m["dtype"]
+        _close(g, t[key], ref_dtype)
