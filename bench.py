@@ -46,6 +46,141 @@ CONFIGS = {
 }
 
 
+# cached-logit block schedule at the reference model's shape (12 layers, d768,
+# 6 blocks: up to 6 completed sources read by the 4 sites of the next block);
+# a step is phase 1 once + phase 2 at each of the Q sites, forward and backward
+PHASE_CONFIGS = {
+    "p5": dict(B=16, T=1024, D=768, S=6, Q=4, dtype=torch.bfloat16),
+}
+
+
+def phase_bytes_per_token(c):
+    """Algorithmic HBM bytes per token of each phase kernel (fp32 logits, lse)."""
+    s = torch.finfo(c["dtype"]).bits // 8
+    S, Q, D = c["S"], c["Q"], c["D"]
+    p1f = S * D * s + Q * S * 4 + Q * D * s + Q * 4
+    p1b = Q * D * s + Q * 4 + S * D * s + Q * S * 4 + S * D * s + Q * S * 4
+    p2f = 2 * D * s + 4 + D * s
+    p2b = 3 * D * s + 4 + 2 * D * s + 4
+    return dict(phase1_fwd=p1f, phase1_bwd=p1b, phase2_fwd=p2f, phase2_bwd=p2b)
+
+
+class PhaseWorkload:
+    """Phase-1 + phase-2 (base keys, key_norm, count bias, block-summary scale)
+    descriptors over resident synthetic inputs, launched through the C ABI."""
+
+    def __init__(self, c, device, seed=0):
+        import _attnres_hip as H
+
+        self.H = H
+        lib = H.load()
+        self.lib = lib
+        g = torch.Generator(device=device).manual_seed(seed)
+        B, T, D, S, Q, dt = c["B"], c["T"], c["D"], c["S"], c["Q"], c["dtype"]
+        n = B * T
+        self.n_tok, self.Q = n, Q
+        rn = lambda *shape, std=1.0, dtype=dt: (torch.randn(shape, generator=g, device=device) * std).to(dtype)
+        self.values = [rn(n, D) for _ in range(S)]
+        self.logits = rn(Q, S, n, std=2.0, dtype=torch.float32)
+        self.p1 = H.Phase1(self.values, self.logits, False)
+        self.out = torch.empty((Q, n, D), device=device, dtype=dt)
+        self.lse = torch.empty((Q, n), device=device, dtype=torch.float32)
+        self.gout = rn(Q, n, D)
+        self.glse = rn(Q, n, dtype=torch.float32)
+        self.dvals = [torch.empty((n, D), device=device, dtype=dt) for _ in range(S)]
+        self._dv = (ctypes.c_void_p * S)(*[t.data_ptr() for t in self.dvals])
+        self.dlog = torch.empty((Q, S, n), device=device, dtype=torch.float32)
+        self.partial = rn(n, D)
+        self.query = rn(D, std=0.02)
+        self.p2 = [H.Phase2(self.partial, None, self.query, None, self.out[q], self.lse[q], H.MERGE_ADDCMUL, True,
+                            False, 1.0, 0.693, None, 0.5, None, False) for q in range(Q)]
+        self.out2 = torch.empty((n, D), device=device, dtype=dt)
+        self.g2 = rn(n, D)
+        self.dp = torch.empty((n, D), device=device, dtype=dt)
+        self.di = torch.empty((n, D), device=device, dtype=dt)
+        self.dl = torch.empty((n,), device=device, dtype=torch.float32)
+        self.dq = torch.empty((D,), device=device, dtype=dt)
+        ws = lib.attnres_phase2_backward_workspace_size(ctypes.byref(self.p2[0].c))
+        self.ws = torch.empty((max(1, ws),), device=device, dtype=torch.uint8)
+        gr = H.Phase2Grads()
+        gr.grad_out = self.g2.data_ptr()
+        gr.dpartial_value = self.dp.data_ptr()
+        gr.dquery = self.dq.data_ptr()
+        gr.dinterblock_output = self.di.data_ptr()
+        gr.dinterblock_lse = ctypes.cast(ctypes.c_void_p(self.dl.data_ptr()), ctypes.POINTER(ctypes.c_float))
+        gr.workspace = self.ws.data_ptr()
+        gr.workspace_bytes = ws
+        self.gr = gr
+        self.f = lambda t: ctypes.cast(ctypes.c_void_p(t.data_ptr()), ctypes.POINTER(ctypes.c_float))
+
+    def _ok(self, rc):
+        if rc:
+            raise RuntimeError(self.lib.attnres_last_error().decode())
+
+    def phase1_fwd(self, sv):
+        self._ok(self.lib.attnres_phase1_forward(ctypes.byref(self.p1.c), ctypes.c_void_p(self.out.data_ptr()),
+                                                 None, self.f(self.lse), None, sv))
+
+    def phase1_bwd(self, sv):
+        self._ok(self.lib.attnres_phase1_backward(ctypes.byref(self.p1.c), ctypes.c_void_p(self.gout.data_ptr()),
+                                                  self.f(self.glse), None, None, self._dv,
+                                                  ctypes.c_void_p(self.dlog.data_ptr()), sv))
+
+    def phase2_fwd(self, sv):
+        for d in self.p2:
+            self._ok(self.lib.attnres_phase2_forward(ctypes.byref(d.c), ctypes.c_void_p(self.out2.data_ptr()), sv))
+
+    def phase2_bwd(self, sv):
+        for d in self.p2:
+            self._ok(self.lib.attnres_phase2_backward(ctypes.byref(d.c), ctypes.byref(self.gr), sv))
+
+
+def bench_phase(args, dev):
+    c = PHASE_CONFIGS[args.config]
+    wl = PhaseWorkload(c, dev)
+    stream = torch.cuda.current_stream(dev)
+    sv = ctypes.c_void_p(stream.cuda_stream)
+    parts = ("phase1_fwd", "phase1_bwd", "phase2_fwd", "phase2_bwd")
+    for _ in range(args.warmup):
+        for k in parts:
+            getattr(wl, k)(sv)
+    torch.cuda.synchronize()
+    ev = {k: [] for k in parts}
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        for k in parts:
+            getattr(wl, k)(sv)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t0.elapsed_time(t1) / args.steps
+    for _ in range(args.steps):
+        for k in parts:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            getattr(wl, k)(sv)
+            b.record(stream)
+            ev[k].append((a, b))
+    torch.cuda.synchronize()
+    bpt = phase_bytes_per_token(c)
+    kern = {}
+    for k in parts:
+        ms = sum(a.elapsed_time(b) for a, b in ev[k]) / args.steps
+        calls = c["Q"] if k.startswith("phase2") else 1
+        gbs = bpt[k] * wl.n_tok * calls / (ms / 1e3) / 1e9
+        kern[k] = {"ms": round(ms, 5), "calls": calls, "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                   "bytes_per_token": bpt[k]}
+    print(json.dumps({
+        "metric": "cached-logit block schedule (phase 1 + Q phase-2 merges) fwd+bwd tokens/s",
+        "value": round(wl.n_tok / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q']} x phase2 (base, key_norm) "
+                               f"B{c['B']} T{c['T']} d{c['D']}", "tokens": wl.n_tok},
+        "kernels": kern}))
+
+
 def bytes_per_token(c):
     """Algorithmic HBM bytes per token (fwd, bwd): every tensor the op must
     touch, once.  s = element size; saved softmax weights are fp32."""
@@ -266,7 +401,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(PHASE_CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-api", action="store_true")
@@ -282,6 +417,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.config in PHASE_CONFIGS:
+        bench_phase(args, dev)
         return
     c = CONFIGS[args.config]
     wl = Workload(c, dev)

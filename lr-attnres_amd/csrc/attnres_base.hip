@@ -620,52 +620,62 @@ __global__ void __launch_bounds__(1024) avg_bwd_kernel(const ReadBwdParams bp) {
 }
 
 // ============================================================== partial-sum reduction
-// One workgroup per output slot; the workgroup partials are summed in a fixed
-// order (strided per thread, then a fixed tree), so the result is
-// bit-reproducible run to run.
+// A workgroup owns 64 consecutive slots and reads the partial rows as
+// coalesced 256-byte segments; every slot is summed in a fixed order (16
+// strided row sums, added in row order), so the result is bit-reproducible
+// run to run.
+constexpr int kRedSlots = 64;  // slots per workgroup (one coalesced 256-byte row segment)
+constexpr int kRedRows = 16;   // partial rows summed in parallel per slot
+
 template <class DT>
-__global__ void __launch_bounds__(256) reduce_partials_kernel(const ReduceParams rp) {
-  __shared__ float sh[256];
-  const int slot = blockIdx.x, tid = threadIdx.x;
-  float a = 0.f;
-  for (int w = tid; w < rp.n_groups; w += 256) a += rp.partials[(int64_t)w * rp.n_part + slot];
-  sh[tid] = a;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (tid < o) sh[tid] += sh[tid + o];
-    __syncthreads();
-  }
-  if (slot >= rp.part_extra && slot < rp.part_extra + rp.n_extra) {
-    // extra slots are the summands of one fp32 gradient, each rounded to the
-    // dtype first (separate autograd edges reduced in the dtype); the block of
-    // the first slot adds them up in slot order
-    if (slot != rp.part_extra) return;
-    float tot = DT::rnd(sh[0]);
-    for (int k = 1; k < rp.n_extra; ++k) {
-      __syncthreads();
-      float b = 0.f;
-      for (int w = tid; w < rp.n_groups; w += 256) b += rp.partials[(int64_t)w * rp.n_part + slot + k];
-      sh[tid] = b;
-      __syncthreads();
-      for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) sh[tid] += sh[tid + o];
-        __syncthreads();
-      }
-      tot += DT::rnd(sh[0]);
+__global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParams rp) {
+  const int tid = threadIdx.x;
+  const int n_slot_blocks = (rp.n_part + kRedSlots - 1) / kRedSlots;
+  if ((int)blockIdx.x < n_slot_blocks) {
+    // thread (rl, sl) sums rows rl, rl + 16, ... of slot sl; the 16 row sums
+    // are then added in row order
+    __shared__ float sh[kRedRows][kRedSlots + 1];
+    const int sl = tid % kRedSlots, rl = tid / kRedSlots;
+    const int slot = (int)blockIdx.x * kRedSlots + sl;
+    const bool regular = slot < rp.n_part && !(slot >= rp.part_extra && slot < rp.part_extra + rp.n_extra);
+    float a = 0.f;
+    if (regular) {
+#pragma unroll 8
+      for (int w = rl; w < rp.n_groups; w += kRedRows) a += rp.partials[(int64_t)w * rp.n_part + slot];
     }
-    if (tid == 0 && rp.dextra) rp.dextra[0] = tot;
+    sh[rl][sl] = a;
+    __syncthreads();
+    if (rl == 0 && regular) {
+      float t = 0.f;
+      for (int r = 0; r < kRedRows; ++r) t += sh[r][sl];
+      if (slot >= rp.part_q && slot < rp.part_q + rp.n_q) {
+        if (rp.dquery) DT::store1((typename DT::S*)rp.dquery + (slot - rp.part_q), t);
+      } else if (slot >= rp.part_gate && slot < rp.part_gate + rp.n_gate) {
+        if (rp.dgate) DT::store1((typename DT::S*)rp.dgate + (slot - rp.part_gate), t);
+      } else if (slot >= rp.part_bias && slot < rp.part_bias + rp.n_bias) {
+        if (rp.dbias) rp.dbias[slot - rp.part_bias] = t;
+      }
+    }
     return;
   }
-  if (tid == 0) {
-    const float t = sh[0];
-    if (slot >= rp.part_q && slot < rp.part_q + rp.n_q) {
-      if (rp.dquery) DT::store1((typename DT::S*)rp.dquery + (slot - rp.part_q), t);
-    } else if (slot >= rp.part_gate && slot < rp.part_gate + rp.n_gate) {
-      if (rp.dgate) DT::store1((typename DT::S*)rp.dgate + (slot - rp.part_gate), t);
-    } else if (slot >= rp.part_bias && slot < rp.part_bias + rp.n_bias) {
-      if (rp.dbias) rp.dbias[slot - rp.part_bias] = t;
+  // the last workgroup: extra slots are the summands of one fp32 gradient,
+  // each summed over the rows and rounded to the dtype on its own (separate
+  // autograd edges reduced in the dtype), then added in slot order
+  __shared__ float tree[1024];
+  float tot = 0.f;
+  for (int k = 0; k < rp.n_extra; ++k) {
+    float b = 0.f;
+    for (int w = tid; w < rp.n_groups; w += 1024) b += rp.partials[(int64_t)w * rp.n_part + rp.part_extra + k];
+    tree[tid] = b;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+      if (tid < o) tree[tid] += tree[tid + o];
+      __syncthreads();
     }
+    tot += DT::rnd(tree[0]);
+    __syncthreads();
   }
+  if (tid == 0 && rp.dextra) rp.dextra[0] = tot;
 }
 
 // ============================================================== launchers
@@ -764,7 +774,8 @@ hipError_t launch_average_backward(int dtype, const ReadBwdParams& p, const Laun
 
 template <class DT>
 static hipError_t reduce_dt(const ReduceParams& rp, hipStream_t st) {
-  hipLaunchKernelGGL((reduce_partials_kernel<DT>), dim3(rp.n_part), dim3(256), 0, st, rp);
+  const int blocks = (rp.n_part + kRedSlots - 1) / kRedSlots + (rp.n_extra > 0 ? 1 : 0);
+  hipLaunchKernelGGL((reduce_partials_kernel<DT>), dim3(blocks), dim3(1024), 0, st, rp);
   return hipGetLastError();
 }
 hipError_t launch_reduce_partials(int dtype, const ReduceParams& rp, hipStream_t st) {

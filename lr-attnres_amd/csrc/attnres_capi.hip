@@ -671,7 +671,7 @@ extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, v
   L.vec = pl.vec;
   L.wpt = pl.wpt;
   L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
-  L.lds = (2 * (size_t)d->n_q * d->n_src + 8 * (size_t)pl.wpt) * sizeof(float);
+  L.lds = ((size_t)pl.wpt * d->n_q * d->n_src + 8 * (size_t)pl.wpt) * sizeof(float);
   if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "phase-1 forward needs %zu bytes of LDS", L.lds);
   hipError_t err = launch_phase1_forward(d->dtype, p, L, (hipStream_t)stream);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 forward launch failed: %s", hipGetErrorString(err));

@@ -241,6 +241,13 @@ __device__ __forceinline__ S* global_ptr(uint64_t a) {
   return (S*)(__attribute__((address_space(1))) S*)(a);
 }
 
+// orders one wave's LDS writes before its later LDS reads by other lanes
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // a wave-uniform 64-bit value, moved to scalar registers
 __device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);

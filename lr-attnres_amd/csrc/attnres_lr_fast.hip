@@ -32,12 +32,6 @@
 
 namespace attnres {
 
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 constexpr int kFastWaves = 4;  // waves per workgroup (independent token streams)
 
 // per-source tables in LDS

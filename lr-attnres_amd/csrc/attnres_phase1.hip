@@ -13,9 +13,12 @@
 // dv[s] = rnd(sum_q rnd(w[q, s]) * g[q]).
 //
 // One workgroup of wpt waves owns one token at a time; each lane owns CB
-// vectors of E elements of the D-wide rows.  Wave 0 computes the token's
-// softmax rows in a (site, source) lane layout while the other waves' value
-// loads are in flight; the weights reach the mix through LDS (double-buffered
+// vectors of E elements of the D-wide rows.  Forward: every wave computes the
+// token's softmax rows itself in a (site, source) lane layout and reads its
+// weights back from its own LDS region (no workgroup barrier unless the output
+// is normed), and the next token's value rows are loaded before this token's
+// stores.  Backward: wave 0 computes the softmax rows while the other waves'
+// loads are in flight; the per-wave partial dots meet in LDS (double-buffered
 // by token parity, so one barrier per token suffices).
 #include "attnres_block.h"
 #include "attnres_device.h"
@@ -69,17 +72,17 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
   const int N = p.n_src, Q = p.n_q, D = p.D;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int wpt = blockDim.x / kWave;
-  float* s_w = smem;                // [2][Q * N]
-  float* s_red = smem + 2 * Q * N;  // [wpt * kP1QC]
+  float* w = smem + wave * Q * N;    // this wave's weights [Q * N]
+  float* s_red = smem + wpt * Q * N;  // [wpt * kP1QC]
   const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
 
-  int par = 0;
-  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x, par ^= 1) {
-    float* w = s_w + par * Q * N;
-    Raw<DT, E> r[kP1SC][CB];
-    phase1_load_rows<DT, E, CB>(p, tok, 0, r, cl);
-    if (wave == 0) phase1_softmax(p, tok, lane, w, true);
-    __syncthreads();
+  Raw<DT, E> r[kP1SC][CB];
+  if ((int64_t)blockIdx.x < p.n_tok) phase1_load_rows<DT, E, CB>(p, blockIdx.x, 0, r, cl);
+  for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    // every wave computes the token's softmax rows itself: no workgroup
+    // barrier (the first batch of value rows is already in flight)
+    phase1_softmax(p, tok, lane, w, wave == 0);
+    wave_sync();
 
     for (int q0 = 0; q0 < Q; q0 += kP1QC) {
       float acc[kP1QC][CB][E];
@@ -110,6 +113,9 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
           }
         }
       }
+      // the next token's first batch of value rows goes out before this
+      // token's stores
+      if (q0 + kP1QC >= Q && tok + gridDim.x < p.n_tok) phase1_load_rows<DT, E, CB>(p, tok + gridDim.x, 0, r, cl);
       float ss[kP1QC];
 #pragma unroll
       for (int qq = 0; qq < kP1QC; ++qq) {
@@ -156,6 +162,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
         }
       }
     }
+    wave_sync();  // this token's weights are read before the next token writes them
   }
 }
 
@@ -173,6 +180,8 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
   float* s_red = s_dw + 2 * wpt * QN;  // [wpt * QMAX]
   const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
 
+  Raw<DT, E> r[kP1SC][CB];
+  if ((int64_t)blockIdx.x < p.n_tok) phase1_load_rows<DT, E, CB>(p, blockIdx.x, 0, r, cl);
   int par = 0;
   for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x, par ^= 1) {
     float* w = s_w + par * QN;
@@ -187,8 +196,6 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
           if (cl.ok[c]) load_raw<DT, E>(gp + cl.eoff[c], gr[q][c]);
       }
     }
-    Raw<DT, E> r[kP1SC][CB];
-    phase1_load_rows<DT, E, CB>(p, tok, 0, r, cl);
     if (wave == 0) phase1_softmax(p, tok, lane, w, false);
 
     if (p.norm_out) {
@@ -269,6 +276,9 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
         }
       }
     }
+    // the next token's first batch of value rows is in flight during the
+    // logits and value gradients of this one
+    if (tok + gridDim.x < p.n_tok) phase1_load_rows<DT, E, CB>(p, tok + gridDim.x, 0, r, cl);
     __syncthreads();
 
     if (wave == 0) {

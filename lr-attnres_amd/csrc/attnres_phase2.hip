@@ -44,19 +44,54 @@ struct P2State {
   float sg, prob;    // sigmoid and its dtype-rounded value
 };
 
+// One token's inputs as loaded (packed), so the next token's loads can be
+// issued before the current token is processed.
+template <class DT, int E, int CB>
+struct P2Raw {
+  Raw<DT, E> pv[CB], it[CB], g[CB];
+  float kr[kP2KPT];
+  float lse, logit;
+};
+
 template <class DT, int E, int CB, bool LR>
-__device__ __forceinline__ void p2_token(const Phase2Params& p, int64_t tok, const float (&qv)[CB][E],
-                                         const float (&qk)[kP2KPT], float vs, float bias, const Cols<CB, E>& cl,
-                                         float* s_red, int tid, int lane, int wave, int wpt, P2State<CB, E>& st) {
+__device__ __forceinline__ void p2_load(const Phase2Params& p, int64_t tok, const Cols<CB, E>& cl, int tid,
+                                        bool with_grad, P2Raw<DT, E, CB>& r) {
   using S = typename DT::S;
-  const int D = p.D, bd = blockDim.x;
+  const int bd = blockDim.x;
   const S* pvp = (const S*)p.pv + tok * p.pv_stride;
   const S* itp = (const S*)p.inter + tok * p.inter_stride;
+  const S* gp = with_grad ? (const S*)p.gout + tok * (int64_t)p.D : nullptr;
 #pragma unroll
   for (int c = 0; c < CB; ++c) {
     if (cl.ok[c]) {
-      load_vec<DT, E>(pvp + cl.eoff[c], st.pr[c]);
-      load_vec<DT, E>(itp + cl.eoff[c], st.it[c]);
+      load_raw<DT, E>(pvp + cl.eoff[c], r.pv[c]);
+      load_raw<DT, E>(itp + cl.eoff[c], r.it[c]);
+      if (with_grad) load_raw<DT, E>(gp + cl.eoff[c], r.g[c]);
+    }
+  }
+  if (LR) {
+    const S* kp = (const S*)p.pk + tok * p.pk_stride;
+#pragma unroll
+    for (int j = 0; j < kP2KPT; ++j) {
+      const int r_ = tid + j * bd;
+      r.kr[j] = r_ < p.R ? DT::load1(kp + r_) : 0.f;
+    }
+  }
+  r.lse = p.lse[tok];
+  r.logit = p.logit_given ? load_any(p.plogit, tok, p.pl_dt) : 0.f;
+}
+
+template <class DT, int E, int CB, bool LR>
+__device__ __forceinline__ void p2_token(const Phase2Params& p, const P2Raw<DT, E, CB>& raw,
+                                         const float (&qv)[CB][E], const float (&qk)[kP2KPT], float vs, float bias,
+                                         const Cols<CB, E>& cl, float* s_red, int lane, int wave, int wpt,
+                                         P2State<CB, E>& st) {
+  const int D = p.D;
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    if (cl.ok[c]) {
+      unpack<DT, E>(raw.pv[c], st.pr[c]);
+      unpack<DT, E>(raw.it[c], st.it[c]);
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) st.pr[c][e] = st.it[c][e] = 0.f;
@@ -64,19 +99,13 @@ __device__ __forceinline__ void p2_token(const Phase2Params& p, int64_t tok, con
 #pragma unroll
     for (int e = 0; e < E; ++e) st.p[c][e] = DT::rnd(st.pr[c][e] * vs);
   }
-  if (LR) {
-    const S* kp = (const S*)p.pk + tok * p.pk_stride;
 #pragma unroll
-    for (int j = 0; j < kP2KPT; ++j) {
-      const int r = tid + j * bd;
-      st.kr[j] = (!p.logit_given && r < p.R) ? DT::load1(kp + r) : 0.f;
-    }
-  }
-  const float lse = p.lse[tok];
+  for (int j = 0; j < kP2KPT; ++j) st.kr[j] = raw.kr[j];
+  const float lse = raw.lse;
 
   float logit;
   if (p.logit_given) {
-    logit = load_any(p.plogit, tok, p.pl_dt);
+    logit = raw.logit;
   } else if (LR) {
 #pragma unroll
     for (int j = 0; j < kP2KPT; ++j) st.kv[j] = p.scale_key ? DT::rnd(st.kr[j] * vs) : st.kr[j];
@@ -162,9 +191,13 @@ __global__ void __launch_bounds__(512) phase2_fwd_kernel(const Phase2Params p) {
     qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
   }
 
+  P2Raw<DT, E, CB> nxt;
+  if ((int64_t)blockIdx.x < p.n_tok) p2_load<DT, E, CB, LR>(p, blockIdx.x, cl, tid, false, nxt);
   for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    const P2Raw<DT, E, CB> cur = nxt;
+    if (tok + gridDim.x < p.n_tok) p2_load<DT, E, CB, LR>(p, tok + gridDim.x, cl, tid, false, nxt);
     P2State<CB, E> st;
-    p2_token<DT, E, CB, LR>(p, tok, qv, qk, vs, bias, cl, s_red, tid, lane, wave, wpt, st);
+    p2_token<DT, E, CB, LR>(p, cur, qv, qk, vs, bias, cl, s_red, lane, wave, wpt, st);
     float o[CB][E];
     p2_merge<DT, E, CB>(p, st, o);
     if (p.norm_out) {
@@ -221,14 +254,17 @@ __global__ void __launch_bounds__(512) phase2_bwd_kernel(const Phase2Params p) {
   for (int j = 0; j < kP2KPT; ++j) dq_l[j] = 0.f;
   float acc_bias = 0.f, acc_sv = 0.f, acc_sk = 0.f;  // bias, value-scale and key-scale gradient sums
 
+  P2Raw<DT, E, CB> nxt;
+  if ((int64_t)blockIdx.x < p.n_tok) p2_load<DT, E, CB, LR>(p, blockIdx.x, cl, tid, true, nxt);
   for (int64_t tok = blockIdx.x; tok < p.n_tok; tok += gridDim.x) {
+    const P2Raw<DT, E, CB> cur = nxt;
+    if (tok + gridDim.x < p.n_tok) p2_load<DT, E, CB, LR>(p, tok + gridDim.x, cl, tid, true, nxt);
     P2State<CB, E> st;
-    p2_token<DT, E, CB, LR>(p, tok, qv, qk, vs, bias, cl, s_red, tid, lane, wave, wpt, st);
+    p2_token<DT, E, CB, LR>(p, cur, qv, qk, vs, bias, cl, s_red, lane, wave, wpt, st);
     float G[CB][E];
-    const S* gp = (const S*)p.gout + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-      if (cl.ok[c]) load_vec<DT, E>(gp + cl.eoff[c], G[c]);
+      if (cl.ok[c]) unpack<DT, E>(cur.g[c], G[c]);
       else
 #pragma unroll
         for (int e = 0; e < E; ++e) G[c][e] = 0.f;
