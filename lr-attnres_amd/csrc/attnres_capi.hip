@@ -240,8 +240,13 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   const int N = d->n_src;
   if (N > (f->cb == 2 ? 16 : 32)) return false;
   f->nb = N <= 8 ? 8 : N <= 16 ? 16 : 32;
-  f->np = 1;
+  f->np = 2;  // at least two lanes per head: the packed mix reads source pairs
   while (f->np < N) f->np <<= 1;
+  // 32-bit token index and byte strides in the fast kernels' address math
+  if (d->n_tok > INT32_MAX) return false;
+  for (int s = 0; s < N; ++s)
+    if ((uint64_t)d->value_row_stride[s] * es > UINT32_MAX || (uint64_t)d->key_row_stride[s] * es > UINT32_MAX)
+      return false;
   if (f->np * f->nh > 64 || f->nh * rh > 64) return false;
   if ((rh * es) % 16) return false;
   f->kch = rh * es / 16;

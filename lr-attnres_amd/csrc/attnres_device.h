@@ -212,23 +212,51 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int code, float x)
 }
 
 // ---------------------------------------------------------------- reductions
-// Butterfly all-reduce over the 64 lanes of a wave (every lane gets the sum;
-// the association order is fixed, so results are deterministic).
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
-  return x;
-}
 
-// Butterfly all-reduce inside aligned groups of `width` lanes (power of two).
+
+// Cross-lane moves inside rows of 16 lanes through the DPP modifiers of
+// ordinary VALU instructions (no LDS round trip): lane i reads lane i ^ 1,
+// i ^ 2 (quad permutes), 7 - i within its half row and 15 - i within its row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+
+// All-reduce inside aligned groups of `width` lanes (power of two <= 64).
+// Within 16 lanes the partners are a quad butterfly and two mirrors (each
+// lane's partner holds the sum of the complementary part, so every lane ends
+// with the same value); wider groups continue with lane shuffles.  The order
+// is fixed, so results are deterministic.
 __device__ __forceinline__ float group_sum(float x, int width) {
-  for (int o = 1; o < width; o <<= 1) x += __shfl_xor(x, o, kWave);
+  if (width > 1) x += dpp_f32<kDppXor1>(x);
+  if (width > 2) x += dpp_f32<kDppXor2>(x);
+  if (width > 4) x += dpp_f32<kDppHalfMirror>(x);
+  if (width > 8) x += dpp_f32<kDppMirror>(x);
+  for (int o = 16; o < width; o <<= 1) x += __shfl_xor(x, o, kWave);
   return x;
 }
 
-// Butterfly max inside aligned groups of `width` lanes (power of two).
+// All-reduce over the 64 lanes of a wave (every lane gets the sum; the
+// association order is fixed, so results are deterministic).
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp_f32<kDppXor1>(x);
+  x += dpp_f32<kDppXor2>(x);
+  x += dpp_f32<kDppHalfMirror>(x);
+  x += dpp_f32<kDppMirror>(x);
+  x += __shfl_xor(x, 16, kWave);
+  x += __shfl_xor(x, 32, kWave);
+  return x;
+}
 __device__ __forceinline__ float group_max(float x, int width) {
-  for (int o = 1; o < width; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
+  if (width > 1) x = fmaxf(x, dpp_f32<kDppXor1>(x));
+  if (width > 2) x = fmaxf(x, dpp_f32<kDppXor2>(x));
+  if (width > 4) x = fmaxf(x, dpp_f32<kDppHalfMirror>(x));
+  if (width > 8) x = fmaxf(x, dpp_f32<kDppMirror>(x));
+  for (int o = 16; o < width; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
   return x;
 }
 

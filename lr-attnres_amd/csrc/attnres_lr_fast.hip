@@ -40,8 +40,8 @@ struct SrcTab {
   uint64_t kptr[kMaxSources];
   uint64_t dvptr[kMaxSources];
   uint64_t dkptr[kMaxSources];
-  int32_t vstr[kMaxSources];
-  int32_t kstr[kMaxSources];
+  uint32_t vstrb[kMaxSources];  // row strides in bytes (< 2^32, checked on the host)
+  uint32_t kstrb[kMaxSources];
 };
 constexpr int kSrcTabFloats = (int)(sizeof(SrcTab) / sizeof(float));
 
@@ -51,26 +51,40 @@ struct KeySlice {
   Raw<DT, KV> r[RHC];
 };
 
-// query element j of the pair's head: static part from LDS, per-token part
-// (optionally gated) from registers, composed and rounded like the reference
-template <class DT, int RHC>
-__device__ __forceinline__ float fast_q(const float* s_qh, const KeySlice<DT, RHC>& qd, bool dyn, float gf,
-                                        bool has_static, int j) {
-  constexpr int KV = KeySlice<DT, RHC>::KV;
-  float q = has_static ? s_qh[j] : 0.f;
-  if (dyn) {
-    float t[KV];
-    unpack<DT, KV>(qd.r[j / KV], t);
-    q = DT::rnd(q + gf * t[j % KV]);
-  }
-  return q;
+// byte address of a row: base + tok * stride, one 32 x 32 -> 64-bit
+// multiply-add (tok and the byte stride fit 32 bits on this path)
+__device__ __forceinline__ uint64_t row_addr(uint64_t base, int64_t tok, uint32_t strideb) {
+  return base + (uint64_t)(uint32_t)tok * strideb;
 }
 
 // byte address of source s's row for token tok (the table has kMaxSources
 // slots, so reading a slot past n_src is harmless; its value is never used)
-template <class S>
 __device__ __forceinline__ uint64_t row_base(const SrcTab* tab, int s, int64_t tok) {
-  return tab->vptr[s] + (uint64_t)(tok * (int64_t)tab->vstr[s]) * sizeof(S);
+  return row_addr(tab->vptr[s], tok, tab->vstrb[s]);
+}
+
+// Packed mix of two sources: (a[i], b[i]) element pairs against the pair of
+// dtype-rounded weights (w_a, w_b) with one v_dot2 per element (the products
+// of two 16-bit floats are exact in fp32).
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+
+template <class DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT::kCode == 1)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a), __builtin_bit_cast(bf16x2v, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v, a), __builtin_bit_cast(f16x2v, b), c, false);
+}
+
+// 16-bit storage bits of a dtype-rounded value
+template <class DT>
+__device__ __forceinline__ uint32_t bits16(float x) {
+  if constexpr (DT::kCode == 1) return __float_as_uint(x) >> 16;
+  else return f32_to_f16_bits(x);
 }
 
 template <class DT, int RHC>
@@ -89,6 +103,93 @@ __device__ __forceinline__ float key_inv_rms(const KeySlice<DT, RHC>& kr, int kc
   return 1.0f / sqrtf(ss / (float)rh + eps);
 }
 
+// The pair lane's query slice for one token, in registers: static part
+// (dtype-exact, token-invariant) plus, with a per-token query, the gated
+// dynamic part composed and rounded like the reference: rnd(q_s + g * q_d).
+// 16-bit types keep the (exact) values packed two per word.
+template <class DT, int RHC>
+struct QSlice {
+  static constexpr int KV = KeySlice<DT, RHC>::KV;
+  static constexpr bool kPacked = sizeof(typename DT::S) == 2;
+  static constexpr int kWords = kPacked ? RHC * KV / 2 : RHC * KV;
+  uint32_t w[kWords];
+  __device__ __forceinline__ float get(int j) const {
+    if constexpr (kPacked) {
+      const uint32_t x = w[j >> 1];
+      if constexpr (DT::kCode == 1) return __uint_as_float((j & 1) ? (x & 0xffff0000u) : (x << 16));
+      else return f16_bits_to_f32((j & 1) ? (x >> 16) : x);
+    } else {
+      return __uint_as_float(w[j]);
+    }
+  }
+  __device__ __forceinline__ void set2(int j, float a, float b) {  // elements j, j + 1 (j even), dtype-exact
+    if constexpr (kPacked) {
+      w[j >> 1] = bits16<DT>(a) | (bits16<DT>(b) << 16);
+    } else {
+      w[j] = __float_as_uint(a);
+      w[j + 1] = __float_as_uint(b);
+    }
+  }
+};
+
+template <class DT, int RHC>
+__device__ __forceinline__ void static_query(const float* s_qh, bool has_static, int kch, QSlice<DT, RHC>& qs) {
+  constexpr int KV = QSlice<DT, RHC>::KV;
+#pragma unroll
+  for (int j = 0; j < RHC * KV; j += 2) {
+    const bool in = has_static && j < kch * KV;
+    qs.set2(j, in ? s_qh[j] : 0.f, in ? s_qh[j + 1] : 0.f);
+  }
+}
+
+template <class DT, int RHC>
+__device__ __forceinline__ void token_query(const QSlice<DT, RHC>& qs, const KeySlice<DT, RHC>& qr, bool dyn, float gf,
+                                            QSlice<DT, RHC>& q) {
+  constexpr int KV = QSlice<DT, RHC>::KV;
+  if (dyn) {
+#pragma unroll
+    for (int j = 0; j < RHC; ++j) {
+      float t[KV];
+      unpack<DT, KV>(qr.r[j], t);
+#pragma unroll
+      for (int i = 0; i < KV; i += 2)
+        q.set2(j * KV + i, DT::rnd(qs.get(j * KV + i) + gf * t[i]), DT::rnd(qs.get(j * KV + i + 1) + gf * t[i + 1]));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < QSlice<DT, RHC>::kWords; ++j) q.w[j] = qs.w[j];
+  }
+}
+
+// <khat, q> of a pair lane, khat = rnd(k * inv) (key_norm) or k.  16-bit
+// types: one v_dot2 per element pair on the (exact) 16-bit values.
+template <class DT, int RHC>
+__device__ __forceinline__ float key_query_dot(const KeySlice<DT, RHC>& kr, const QSlice<DT, RHC>& q, bool key_norm,
+                                               float inv, int kch) {
+  constexpr int KV = QSlice<DT, RHC>::KV;
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < RHC; ++j) {
+    if (j < kch) {
+      float k[KV];
+      unpack<DT, KV>(kr.r[j], k);
+#pragma unroll
+      for (int i = 0; i < KV; ++i) k[i] = key_norm ? DT::rnd(k[i] * inv) : k[i];
+      if constexpr (QSlice<DT, RHC>::kPacked) {
+#pragma unroll
+        for (int i = 0; i < KV / 2; ++i) {
+          const uint32_t kk = bits16<DT>(k[2 * i]) | (bits16<DT>(k[2 * i + 1]) << 16);
+          dot = dot2<DT>(kk, q.w[(j * KV) / 2 + i], dot);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < KV; ++i) dot += k[i] * q.get(j * KV + i);
+      }
+    }
+  }
+  return dot;
+}
+
 // ============================================================== forward
 template <class DT, int VB, int CB, int NB, int RHC>
 __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
@@ -105,11 +206,14 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
   float* s_w = s_q + R + wslot * 64;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
-    tab->vptr[i] = (uint64_t)p.val[i];
-    tab->vstr[i] = p.vstride[i];
-    tab->kptr[i] = (uint64_t)p.key[i];
-    tab->kstr[i] = p.kstride[i];
+  // slots past n_src repeat the last source, so the unrolled loads over NB
+  // slots read the table at constant offsets (their values are never used)
+  for (int i = threadIdx.x; i < kMaxSources; i += blockDim.x) {
+    const int j = min(i, N - 1);
+    tab->vptr[i] = (uint64_t)p.val[j];
+    tab->vstrb[i] = (uint32_t)p.vstride[j] * (uint32_t)sizeof(S);
+    tab->kptr[i] = (uint64_t)p.key[j];
+    tab->kstrb[i] = (uint32_t)p.kstride[j] * (uint32_t)sizeof(S);
   }
   if (p.q_static)
     for (int i = threadIdx.x; i < R; i += blockDim.x) s_q[i] = DT::load1((const S*)p.q_static + i);
@@ -131,8 +235,8 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   const int kch = p.kch;
   const bool dyn = p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
-  const S* kbase = global_ptr<const S>(tab->kptr[ps]) + ph * rh;
-  const int64_t kstr = tab->kstr[ps];
+  const uint64_t kbase = tab->kptr[ps] + (uint64_t)(ph * rh) * sizeof(S);
+  const uint32_t kstrb = tab->kstrb[ps];
 
   // lanes past the row end load from the row start (valid memory) and store nothing
   int eoff[CB], hd[CB];
@@ -145,56 +249,48 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     hd[c] = ok[c] ? e / dh - h0 : 0;
   }
 
-  for (int64_t tok = t0; tok < p.n_tok; tok += p.streams) {
-    // ---- issue every load of the token: keys (and per-token query), values
-    // (no branches here: every lane loads valid addresses -- lanes without a
-    // pair read pair 0's slice, slots past kch / N re-read the last chunk /
-    // row -- so the loads issue back to back)
-    KeySlice<DT, RHC> kr, qr;
-    S graw = 0;
+  // ---- every load a token needs: keys (and per-token query), values.  No
+  // branches: every lane loads valid addresses -- lanes without a pair read
+  // pair 0's slice, slots past kch / N re-read the last chunk / row -- so the
+  // loads issue back to back.
+  QSlice<DT, RHC> qstat;
+  static_query<DT, RHC>(s_q + ph * rh, has_static, kch, qstat);
+  KeySlice<DT, RHC> kr, qr;
+  S graw = 0;
+  Raw<DT, E> vr[NB][CB];
+  auto issue_loads = [&](int64_t t) {
     {
-      const S* kp = kbase + tok * kstr;
+      const S* kp = global_ptr<const S>(row_addr(kbase, t, kstrb));
 #pragma unroll
       for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(kp + min(j, kch - 1) * KV, kr.r[j]);
     }
     if (dyn) {
-      const S* qp = global_ptr<const S>((uint64_t)p.q_dyn) + tok * p.q_dyn_stride + ph * rh;
+      const S* qp = global_ptr<const S>((uint64_t)p.q_dyn) + t * p.q_dyn_stride + ph * rh;
 #pragma unroll
       for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(qp + min(j, kch - 1) * KV, qr.r[j]);
-      if (p.gate) graw = *(global_ptr<const S>((uint64_t)p.gate) + (p.gate_per_token ? tok * H : 0) + ph);
+      if (p.gate) graw = *(global_ptr<const S>((uint64_t)p.gate) + (p.gate_per_token ? t * H : 0) + ph);
     }
-    Raw<DT, E> vr[NB][CB];
-    {
-      uint64_t base[NB];
+    uint64_t base[NB];
 #pragma unroll
-      for (int s = 0; s < NB; ++s) base[s] = row_base<S>(tab, min(s, N - 1), tok);
+    for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, t);
 #pragma unroll
-      for (int s = 0; s < NB; ++s) {
-        const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+    for (int s = 0; s < NB; ++s) {
+      const S* vp = global_ptr<const S>(uniform_u64(base[s]));
 #pragma unroll
-        for (int c = 0; c < CB; ++c) load_raw<DT, E>(vp + eoff[c], vr[s][c]);
-      }
+      for (int c = 0; c < CB; ++c) load_raw<DT, E>(vp + eoff[c], vr[s][c]);
     }
+  };
 
+  for (int64_t tok = t0; tok < p.n_tok; tok += p.streams) {
+    issue_loads(tok);
     // ---- logits of this wave's (head, source) pairs
     float logit = -INFINITY;
     if (has_pair) {
       const float gf = (dyn && p.gate) ? gate_value(DT::load1(&graw), p.gate_act) : 1.f;
       const float inv = p.key_norm ? key_inv_rms<DT, RHC>(kr, kch, rh, p.eps) : 1.f;
-      const float* s_qh = s_q + ph * rh;
-      float dot = 0.f;
-#pragma unroll
-      for (int j = 0; j < RHC; ++j) {
-        if (j < kch) {
-          float k[KV];
-          unpack<DT, KV>(kr.r[j], k);
-#pragma unroll
-          for (int i = 0; i < KV; ++i) {
-            const float kh = p.key_norm ? DT::rnd(k[i] * inv) : k[i];
-            dot += kh * fast_q<DT, RHC>(s_qh, qr, dyn, gf, has_static, j * KV + i);
-          }
-        }
-      }
+      QSlice<DT, RHC> q;
+      token_query<DT, RHC>(qstat, qr, dyn, gf, q);
+      const float dot = key_query_dot<DT, RHC>(kr, q, p.key_norm, inv, kch);
       logit = DT::rnd(DT::rnd(dot) * p.scale);
       if (p.bias) logit += p.bias[ps];
     }
@@ -202,7 +298,13 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     const float lmax = group_max(logit, np);
     const float ex = has_pair ? expf(logit - lmax) : 0.f;
     const float pw = ex / group_sum(ex, np);
-    if (has_pair) s_w[lane] = DT::rnd(pw);
+    if constexpr (sizeof(S) == 2) {
+      // 16-bit weights, zero for lanes without a pair (so an odd source count
+      // pairs its last source with a zero weight)
+      ((uint16_t*)s_w)[lane] = (uint16_t)(has_pair ? bits16<DT>(DT::rnd(pw)) : 0u);
+    } else {
+      if (has_pair) s_w[lane] = pw;
+    }
     wave_sync();
 
     // ---- mix
@@ -211,16 +313,34 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     for (int c = 0; c < CB; ++c)
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[c][e] = 0.f;
+    if constexpr (sizeof(S) == 2) {
+      const uint32_t* s_wp = (const uint32_t*)s_w;
 #pragma unroll
-    for (int s = 0; s < NB; ++s) {
-      if (s < N) {
+      for (int s = 0; s < NB; s += 2) {
+        if (s < N) {
 #pragma unroll
-        for (int c = 0; c < CB; ++c) {
-          float v[E];
-          unpack<DT, E>(vr[s][c], v);
-          const float w = s_w[hd[c] * np + s];
+          for (int c = 0; c < CB; ++c) {
+            const uint32_t wp = s_wp[(hd[c] * np + s) >> 1];
 #pragma unroll
-          for (int e = 0; e < E; ++e) acc[c][e] += w * v[e];
+            for (int i = 0; i < E / 2; ++i) {
+              acc[c][2 * i] = dot2<DT>(lo_pair(vr[s][c].w[i], vr[s + 1][c].w[i]), wp, acc[c][2 * i]);
+              acc[c][2 * i + 1] = dot2<DT>(hi_pair(vr[s][c].w[i], vr[s + 1][c].w[i]), wp, acc[c][2 * i + 1]);
+            }
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        if (s < N) {
+#pragma unroll
+          for (int c = 0; c < CB; ++c) {
+            float v[E];
+            unpack<DT, E>(vr[s][c], v);
+            const float w = s_w[hd[c] * np + s];
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[c][e] += w * v[e];
+          }
         }
       }
     }
@@ -279,13 +399,14 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   float* s_dl = s_dw + 64;
   float* s_c = s_dl + 64;  // [npairs][rh] = ge * khat
   float* s_fold = s_q + R + nwaves * wave_floats;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
-    tab->vptr[i] = (uint64_t)p.val[i];
-    tab->vstr[i] = p.vstride[i];
-    tab->kptr[i] = (uint64_t)p.key[i];
-    tab->kstr[i] = p.kstride[i];
-    tab->dvptr[i] = (uint64_t)bp.dval[i];
-    tab->dkptr[i] = (uint64_t)bp.dkey[i];
+  for (int i = threadIdx.x; i < kMaxSources; i += blockDim.x) {
+    const int j = min(i, N - 1);
+    tab->vptr[i] = (uint64_t)p.val[j];
+    tab->vstrb[i] = (uint32_t)p.vstride[j] * (uint32_t)sizeof(S);
+    tab->kptr[i] = (uint64_t)p.key[j];
+    tab->kstrb[i] = (uint32_t)p.kstride[j] * (uint32_t)sizeof(S);
+    tab->dvptr[i] = (uint64_t)bp.dval[j];
+    tab->dkptr[i] = (uint64_t)bp.dkey[j];
   }
   if (p.q_static)
     for (int i = threadIdx.x; i < R; i += blockDim.x) s_q[i] = DT::load1((const S*)p.q_static + i);
@@ -310,9 +431,10 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   const int qh = lane / rh, qj = lane - (lane / rh) * rh;
   // dW lane groups: lanes of one head inside a column
   const int gl = CB == 2 ? kWave : (dh / E < kWave ? dh / E : kWave);
-  const S* kbase = global_ptr<const S>(tab->kptr[ps]) + ph * rh;
+  const uint64_t kbase = tab->kptr[ps] + (uint64_t)(ph * rh) * sizeof(S);
   S* dkbase = global_ptr<S>(tab->dkptr[ps]) + ph * rh;
-  const int64_t kstr = tab->kstr[ps];
+  const uint32_t kstrb = tab->kstrb[ps];
+  const uint32_t rowb = (uint32_t)D * (uint32_t)sizeof(S);  // dense gradient rows
 
   int eoff[CB], hd[CB];
   bool ok[CB];
@@ -333,7 +455,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     KeySlice<DT, RHC> kr, qr;
     float pr = bp.saved_w[(tok * H + ph) * N + ps];
     {
-      const S* kp = kbase + tok * kstr;
+      const S* kp = global_ptr<const S>(row_addr(kbase, tok, kstrb));
 #pragma unroll
       for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(kp + min(j, kch - 1) * KV, kr.r[j]);
     }
@@ -356,7 +478,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     {
       uint64_t base[NB];
 #pragma unroll
-      for (int s = 0; s < NB; ++s) base[s] = row_base<S>(tab, min(s, N - 1), tok);
+      for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, tok);
 #pragma unroll
       for (int s = 0; s < NB; ++s) {
         const S* vp = global_ptr<const S>(uniform_u64(base[s]));
@@ -396,17 +518,31 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     if (has_pair) s_p[lane] = pr;
 
     // ---- dW = <g, v> per (head, source), reduced over the head's lanes
+    // (16-bit types: packed g against the packed value words, one v_dot2 per
+    // element pair; g is dtype-exact, so packing it loses nothing)
+    uint32_t gpk[CB][E / 2 > 0 ? E / 2 : 1];
+    if constexpr (sizeof(S) == 2) {
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) gpk[c][i] = bits16<DT>(g[c][2 * i]) | (bits16<DT>(g[c][2 * i + 1]) << 16);
+    }
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
       if (s < N) {
         float part[CB];
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-          float v[E];
-          unpack<DT, E>(vr[s][c], v);
           part[c] = 0.f;
+          if constexpr (sizeof(S) == 2) {
 #pragma unroll
-          for (int e = 0; e < E; ++e) part[c] += g[c][e] * v[e];
+            for (int i = 0; i < E / 2; ++i) part[c] = dot2<DT>(gpk[c][i], vr[s][c].w[i], part[c]);
+          } else {
+            float v[E];
+            unpack<DT, E>(vr[s][c], v);
+#pragma unroll
+            for (int e = 0; e < E; ++e) part[c] += g[c][e] * v[e];
+          }
         }
         if (CB == 2) {
           const float t = wave_sum(part[0] + part[1]);  // one head spans both columns
@@ -424,12 +560,17 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     // softmax backward: dl = p (dW - sum_s p dW), the sum a butterfly over the head's group
     const float dwr = has_pair ? DT::rnd(s_dw[lane]) : 0.f;
     const float pdot = group_sum(has_pair ? pr * dwr : 0.f, np);
+    QSlice<DT, RHC> q;
+    {
+      QSlice<DT, RHC> qs;  // read per token: keeps the slice out of the loop-carried registers
+      static_query<DT, RHC>(s_q + ph * rh, has_static, kch, qs);
+      token_query<DT, RHC>(qs, qr, dyn, 1.f, q);
+    }
     if (has_pair) {
       const float dl = pr * (dwr - pdot);
       s_dl[lane] = dl;
       ge = DT::rnd(DT::rnd(dl) * p.scale);
       if (p.key_norm) kinv = key_inv_rms<DT, RHC>(kr, kch, rh, p.eps);
-      const float* s_qh = s_q + ph * rh;
       float m = 0.f;
 #pragma unroll
       for (int j = 0; j < RHC; ++j) {
@@ -442,7 +583,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
             const float kh = p.key_norm ? DT::rnd(k[i] * kinv) : k[i];
             s_c[lane * rh + jj] = ge * kh;
             if (p.key_norm) {
-              const float dkh = DT::rnd(ge * fast_q<DT, RHC>(s_qh, qr, dyn, 1.f, has_static, jj));
+              const float dkh = DT::rnd(ge * q.get(jj));
               m += dkh * (k[i] * kinv);
             }
           }
@@ -469,7 +610,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
       if (s < N) {
-        S* dvp = global_ptr<S>(uniform_u64(tab->dvptr[s])) + tok * (int64_t)D;
+        S* dvp = global_ptr<S>(uniform_u64(row_addr(tab->dvptr[s], tok, rowb)));
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
           if (ok[c]) {
@@ -484,7 +625,6 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     }
     if (has_pair) {
       // dk = inv * (dkhat - khat_f32 * <dkhat, khat_f32>/rh) (rms-norm backward), dkhat = rnd(ge * q)
-      const float* s_qh = s_q + ph * rh;
       S* dkp = dkbase + tok * (int64_t)R;
 #pragma unroll
       for (int j = 0; j < RHC; ++j) {
@@ -493,7 +633,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
           unpack<DT, KV>(kr.r[j], k);
 #pragma unroll
           for (int i = 0; i < KV; ++i) {
-            const float dkh = DT::rnd(ge * fast_q<DT, RHC>(s_qh, qr, dyn, 1.f, has_static, j * KV + i));
+            const float dkh = DT::rnd(ge * q.get(j * KV + i));
             t[i] = p.key_norm ? DT::rnd(kinv * (dkh - k[i] * kinv * mr)) : dkh;
           }
           store_vec<DT, KV>(dkp + j * KV, t);
