@@ -163,9 +163,12 @@ __global__ void __launch_bounds__(1024) base_fwd_kernel(const ReadParams p) {
 // fits one wave (every reduction is then a wave butterfly, no LDS, no
 // barrier); otherwise one team of wpt waves.  The teams' query/bias
 // accumulators are folded in team order at the end.
-template <class DT, int E, int CB, int NMAX>
-__global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) {
+template <class DT, int E, int CB, int NMAX, int MAXT>
+__global__ void __launch_bounds__(MAXT) base_bwd_kernel(const ReadBwdParams bp) {
   using S = typename DT::S;
+  // 16-bit vector path: the row dot products run on packed words (v_dot2)
+  constexpr bool kPk = sizeof(S) == 2 && E >= 2;
+  constexpr int W = Vec<DT, E>::kWords;
   const ReadParams& p = bp.f;
   extern __shared__ float smem[];
   float* s_red = smem;  // [wpt * NMAX] (only used when wpt > 1, then teams == 1)
@@ -192,14 +195,14 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
 
   const int64_t tstride = (int64_t)gridDim.x * teams;
   for (int64_t tok = (int64_t)blockIdx.x * teams + team; tok < p.n_tok; tok += tstride) {
-    float g[CB][E];
+    Raw<DT, E> gr[CB];
     const S* gp = (const S*)bp.gout + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-      if (cl.ok[c]) load_vec<DT, E>(gp + cl.eoff[c], g[c]);
+      if (cl.ok[c]) load_raw<DT, E>(gp + cl.eoff[c], gr[c]);
       else
 #pragma unroll
-        for (int e = 0; e < E; ++e) g[c][e] = 0.f;
+        for (int i = 0; i < W; ++i) gr[c].w[i] = 0u;
     }
     Raw<DT, E> r[NMAX][CB];
 #pragma unroll
@@ -207,16 +210,28 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
       if (s < N) {
         const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
 #pragma unroll
-        for (int c = 0; c < CB; ++c)
+        for (int c = 0; c < CB; ++c) {
           if (cl.ok[c]) load_raw<DT, E>(vp + cl.eoff[c], r[s][c]);
+          else
+#pragma unroll
+            for (int i = 0; i < W; ++i) r[s][c].w[i] = 0u;
+        }
       }
     }
     float pw[NMAX];
 #pragma unroll
     for (int s = 0; s < NMAX; ++s) pw[s] = s < N ? bp.saved_w[tok * N + s] : 0.f;
-    if (p.norm_out)
+    float g[CB][E];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) unpack<DT, E>(gr[c], g[c]);
+    if (p.norm_out) {
       norm_output_backward<DT, CB, E>(g, (const S*)p.out_prenorm + tok * (int64_t)D, bp.saved_inv[tok], cl, D, s_red, lane,
                                       wave, wpt);
+      if constexpr (kPk) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c) pack_raw<DT, E>(g[c], gr[c]);  // g is dtype-exact
+      }
+    }
 
     // stage 1: dW = <g, v> and (key_norm) sum of squares
     float a[NMAX], b[NMAX];
@@ -227,7 +242,13 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
       if (s < N) {
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-          if (cl.ok[c]) {
+          if constexpr (kPk) {
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+              a[s] = dot2<DT>(gr[c].w[i], r[s][c].w[i], a[s]);
+              b[s] = dot2<DT>(r[s][c].w[i], r[s][c].w[i], b[s]);
+            }
+          } else {
             float v[E];
             unpack<DT, E>(r[s][c], v);
 #pragma unroll
@@ -256,7 +277,7 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
       if (tid == s) bacc += dl;
       ge[s] = DT::rnd(dl);
     }
-    // stage 2 (key_norm): m_s = <d key_hat, y_hat> for the rms-norm backward
+    // stage 2 (key_norm): m_s = <d key_hat, v> * inv for the rms-norm backward
     float mm[NMAX];
 #pragma unroll
     for (int s = 0; s < NMAX; ++s) {
@@ -264,11 +285,18 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
       if (p.key_norm && s < N) {
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-          if (cl.ok[c]) {
+          if constexpr (kPk) {
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+              const uint32_t dk2 = bits16<DT>(DT::rnd(ge[s] * q[c][2 * i])) |
+                                   (bits16<DT>(DT::rnd(ge[s] * q[c][2 * i + 1])) << 16);
+              mm[s] = dot2<DT>(dk2, r[s][c].w[i], mm[s]);
+            }
+          } else {
             float v[E];
             unpack<DT, E>(r[s][c], v);
 #pragma unroll
-            for (int e = 0; e < E; ++e) mm[s] += DT::rnd(ge[s] * q[c][e]) * (v[e] * b[s]);
+            for (int e = 0; e < E; ++e) mm[s] += DT::rnd(ge[s] * q[c][e]) * v[e];
           }
         }
       }
@@ -279,7 +307,7 @@ __global__ void __launch_bounds__(1024) base_bwd_kernel(const ReadBwdParams bp) 
     for (int s = 0; s < NMAX; ++s) {
       if (s < N) {
         const float ws = DT::rnd(pw[s]);
-        const float mr = mm[s] / (float)D;
+        const float mr = mm[s] * b[s] / (float)D;
         S* dvp = (S*)bp.dval[s] + tok * (int64_t)D;
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
@@ -686,7 +714,12 @@ static hipError_t base_fwd_t(const ReadParams& p, const Launch& L, hipStream_t s
 }
 template <class DT, int E, int CB, int NMAX>
 static hipError_t base_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((base_bwd_kernel<DT, E, CB, NMAX>), dim3(L.grid), dim3(L.wpt * kWave * L.teams), L.lds, st, p);
+  // workgroups of at most 256 threads may use up to 256 VGPRs per lane
+  const int threads = L.wpt * kWave * L.teams;
+  if (threads <= 256)
+    hipLaunchKernelGGL((base_bwd_kernel<DT, E, CB, NMAX, 256>), dim3(L.grid), dim3(threads), L.lds, st, p);
+  else
+    hipLaunchKernelGGL((base_bwd_kernel<DT, E, CB, NMAX, 1024>), dim3(L.grid), dim3(threads), L.lds, st, p);
   return hipGetLastError();
 }
 

@@ -218,7 +218,6 @@ int fast_vector_bytes(const attnres_read_desc* d) {
 
 bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, FastPlan* f) {
   if (!pl.lr || !pl.vec || !pl.key_vec) return false;
-  if (backward && d->gate) return false;
   const int es = elem_size(d->dtype);
   f->vb = fast_vector_bytes(d);
   const int E = f->vb / es;
@@ -248,6 +247,8 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
     if ((uint64_t)d->value_row_stride[s] * es > UINT32_MAX || (uint64_t)d->key_row_stride[s] * es > UINT32_MAX)
       return false;
   if (f->np * f->nh > 64 || f->nh * rh > 64) return false;
+  // the backward sums the gate gradient over each head's rh lanes (aligned groups)
+  if (backward && d->gate && (rh & (rh - 1))) return false;
   if ((rh * es) % 16) return false;
   f->kch = rh * es / 16;
   if (f->kch > 8) return false;

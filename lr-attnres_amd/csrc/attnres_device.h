@@ -196,6 +196,31 @@ __device__ __forceinline__ void pack_raw(const float (&x)[E], Raw<DT, E>& r) {
   }
 }
 
+// Packed 16-bit arithmetic: lo_pair / hi_pair interleave the low / high
+// halves of two words (element i of two sources), and dot2 is one v_dot2
+// (a.lo * b.lo + a.hi * b.hi + c; the products of two 16-bit floats are
+// exact in fp32).
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+
+template <class DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT::kCode == 1)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a), __builtin_bit_cast(bf16x2v, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v, a), __builtin_bit_cast(f16x2v, b), c, false);
+}
+
+// 16-bit storage bits of a dtype-rounded value
+template <class DT>
+__device__ __forceinline__ uint32_t bits16(float x) {
+  if constexpr (DT::kCode == 1) return __float_as_uint(x) >> 16;
+  else return f32_to_f16_bits(x);
+}
+
 // scalar access to a buffer whose dtype is only known at run time
 __device__ __forceinline__ float load_any(const void* p, int64_t i, int code) {
   if (code == 0) return ((const float*)p)[i];

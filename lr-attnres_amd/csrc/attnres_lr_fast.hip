@@ -24,8 +24,8 @@
 // Requirements (checked on the host, else the general kernels run):
 // 16-byte vector path, N <= NB (8/16/32), N * heads_per_item <= 64 pairs,
 // key slice of a head = kch 16-byte chunks with kch <= RHC, heads_per_item *
-// (R/H) <= 64, no gate in the backward, output norm only when one item covers
-// the whole row.
+// (R/H) <= 64 (a power of two when the backward has a gate), output norm only
+// when one item covers the whole row.
 #include "attnres_device.h"
 #include "attnres_params.h"
 #include "attnres_launch.h"
@@ -63,29 +63,6 @@ __device__ __forceinline__ uint64_t row_base(const SrcTab* tab, int s, int64_t t
   return row_addr(tab->vptr[s], tok, tab->vstrb[s]);
 }
 
-// Packed mix of two sources: (a[i], b[i]) element pairs against the pair of
-// dtype-rounded weights (w_a, w_b) with one v_dot2 per element (the products
-// of two 16-bit floats are exact in fp32).
-__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
-
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
-
-template <class DT>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  if constexpr (DT::kCode == 1)
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a), __builtin_bit_cast(bf16x2v, b), c, false);
-  else
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v, a), __builtin_bit_cast(f16x2v, b), c, false);
-}
-
-// 16-bit storage bits of a dtype-rounded value
-template <class DT>
-__device__ __forceinline__ uint32_t bits16(float x) {
-  if constexpr (DT::kCode == 1) return __float_as_uint(x) >> 16;
-  else return f32_to_f16_bits(x);
-}
 
 template <class DT, int RHC>
 __device__ __forceinline__ float key_inv_rms(const KeySlice<DT, RHC>& kr, int kch, int rh, float eps) {
@@ -448,6 +425,9 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 
   float qacc = 0.f;  // static-query gradient of (h0 + qh, qj), over this wave's tokens
   float bacc = 0.f;  // bias gradient of source `lane`
+  float gacc = 0.f;  // per-site gate gradient of head h0 + qh (lanes with qj == 0)
+  const bool gated = dyn && p.gate != nullptr;
+  const int64_t gate_tok = p.gate_per_token ? H : 0;  // gate row stride over tokens
 
   for (int64_t tok = t0; tok < p.n_tok; tok += p.streams) {
     // ---- issue every load of the token
@@ -459,10 +439,19 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
       for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(kp + min(j, kch - 1) * KV, kr.r[j]);
     }
+    // gate of the pair lane's head, and for the query-gradient owner lanes the
+    // gate and per-token query element of (h0 + qh, qj)
+    S graw_p = 0, graw_o = 0, qd_o = 0;
     if (dyn) {
       const S* qp = global_ptr<const S>((uint64_t)p.q_dyn) + tok * p.q_dyn_stride + ph * rh;
 #pragma unroll
       for (int j = 0; j < RHC; ++j) load_raw<DT, KV>(qp + min(j, kch - 1) * KV, qr.r[j]);
+      if (gated) {
+        const S* gt = global_ptr<const S>((uint64_t)p.gate) + tok * gate_tok;
+        graw_p = gt[ph];
+        graw_o = gt[h0 + (q_owner ? qh : 0)];
+        qd_o = *(global_ptr<const S>((uint64_t)p.q_dyn) + tok * p.q_dyn_stride + h0 * rh + (q_owner ? lane : 0));
+      }
     }
     Raw<DT, E> gr[CB];
     const S* gp = global_ptr<const S>((uint64_t)bp.gout) + tok * (int64_t)D;
@@ -564,7 +553,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     {
       QSlice<DT, RHC> qs;  // read per token: keeps the slice out of the loop-carried registers
       static_query<DT, RHC>(s_q + ph * rh, has_static, kch, qs);
-      token_query<DT, RHC>(qs, qr, dyn, 1.f, q);
+      token_query<DT, RHC>(qs, qr, dyn, gated ? gate_value(DT::load1(&graw_p), p.gate_act) : 1.f, q);
     }
     if (has_pair) {
       const float dl = pr * (dwr - pdot);
@@ -599,6 +588,22 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
       for (int s = 0; s < N; ++s) dqt += s_c[(qh * np + s) * rh + qj];
       if (dyn) dqt = DT::rnd(dqt);
       qacc += dqt;
+    }
+    float dqd = dqt;  // per-token query gradient: rnd(act(gate) * dq) when gated
+    if (gated) {
+      // gate gradient of head h0 + qh: sum_j dq_j * q_dyn_j over the head's
+      // rh owner lanes (an aligned power-of-two group), times the sigmoid slope
+      const float gv = gate_value(DT::load1(&graw_o), p.gate_act);
+      dqd = DT::rnd(gv * dqt);
+      float c = group_sum(q_owner ? dqt * DT::load1(&qd_o) : 0.f, rh);
+      if (p.gate_act == ATTNRES_GATE_SIGMOID) c *= gv * (1.f - gv);
+      if (q_owner && qj == 0) {
+        if (p.gate_per_token) {
+          if (bp.dgate) DT::store1(global_ptr<S>((uint64_t)bp.dgate) + tok * H + h0 + qh, DT::rnd(c));
+        } else {
+          gacc += c;
+        }
+      }
     }
     if (p.bias && lane < N) {
       float b = 0.f;
@@ -641,7 +646,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
       }
     }
     if (dyn && q_owner && bp.dq_dyn)
-      DT::store1(global_ptr<S>((uint64_t)bp.dq_dyn) + tok * (int64_t)R + h0 * rh + lane, dqt);
+      DT::store1(global_ptr<S>((uint64_t)bp.dq_dyn) + tok * (int64_t)R + h0 * rh + lane, dqd);
     wave_sync();  // this token's LDS is read before the next token writes it
   }
 
@@ -652,6 +657,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   float* fold = s_fold + wslot * bp.n_part;
   if (bp.part_q >= 0 && q_owner) fold[bp.part_q + h0 * rh + lane] = qacc;
   if (bp.part_bias >= 0 && lane < N) fold[bp.part_bias + lane] = bacc;
+  if (bp.part_gate >= 0 && q_owner && qj == 0) fold[bp.part_gate + h0 + qh] = gacc;
   __syncthreads();
   for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
     float a = 0.f;

@@ -381,6 +381,41 @@ def test_config3_full_size_token_subset():
     assert float((full - summed).abs().max()) <= 2e-2 * max(1.0, float(full.abs().max()))
 
 
+def test_config4_full_size_token_subset():
+    """C4 (B4 T4096 d2048 N17 r128 H8 bf16, per-token sigmoid-gated dynamic
+    query) at full size, checked on a token subset: output, value / key /
+    dynamic-query / gate gradients (all per token)."""
+    g = gen(4)
+    B, T, D, S, R, Hh = 4, 4096, 2048, 17, 128, 8
+    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
+    keys = [torch.randn(B, T, R, generator=g).to(torch.bfloat16) for _ in range(S)]
+    qs = (torch.randn(Hh, R // Hh, generator=g) * 0.02).to(torch.bfloat16)
+    qdyn = torch.randn(B, T, R, generator=g).to(torch.bfloat16)
+    gate = torch.randn(B, T, Hh, generator=g).to(torch.bfloat16)
+    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    vd = [leaf(x) for x in vals]
+    kd = [leaf(x) for x in keys]
+    qsd, qdd, gd = leaf(qs), leaf(qdyn), leaf(gate)
+    out = ops.lrid_attention_residual_read_gated(vd, kd, qsd, qdd, gd, Hh, 0.25, True, gate_activation="sigmoid")
+    out.backward(up.to(DEV))
+    torch.cuda.synchronize()
+    sel = (slice(2, 3), slice(4000, 4040))
+    vc = [x[sel].clone().requires_grad_(True) for x in vals]
+    kc = [x[sel].clone().requires_grad_(True) for x in keys]
+    qsc = qs.clone().requires_grad_(True)
+    qdc = qdyn[sel].clone().requires_grad_(True)
+    gc = gate[sel].clone().requires_grad_(True)
+    q = O.gated_query_ref(qsc.float(), qdc.float(), gc.float(), Hh, "sigmoid")
+    ref = O.lrid_attention_residual_read_ref(vc, kc, q, Hh, 0.25, True)
+    ref.backward(up[sel])
+    assert_close(out[sel], ref, torch.bfloat16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad[sel], vc[s].grad, torch.bfloat16, f"dv{s}")
+        assert_close(kd[s].grad[sel], kc[s].grad, torch.bfloat16, f"dk{s}")
+    assert_close(qdd.grad[sel], qdc.grad, torch.bfloat16, "dq_dyn")
+    assert_close(gd.grad[sel], gc.grad, torch.bfloat16, "dgate")
+
+
 def test_bf16_rounding_ties_match_torch():
     """The kernels round to bf16 in hardware (v_cvt_pk_bf16_f32); check exact
     round-half-to-even ties against torch's rounding.  With a zero query the
