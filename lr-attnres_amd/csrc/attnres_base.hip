@@ -648,34 +648,35 @@ __global__ void __launch_bounds__(1024) avg_bwd_kernel(const ReadBwdParams bp) {
 }
 
 // ============================================================== partial-sum reduction
-// A workgroup owns 64 consecutive slots and reads the partial rows as
-// coalesced 256-byte segments; every slot is summed in a fixed order (16
-// strided row sums, added in row order), so the result is bit-reproducible
-// run to run.
-constexpr int kRedSlots = 64;  // slots per workgroup (one coalesced 256-byte row segment)
-constexpr int kRedRows = 16;   // partial rows summed in parallel per slot
-
-template <class DT>
+// A workgroup of 1024 threads owns SPB consecutive slots; thread (rl, sl) sums
+// rows rl, rl + RL, ... of slot sl (RL = 1024 / SPB row lanes, reading SPB-wide
+// coalesced row segments), and the RL row sums of each slot are added by a
+// fixed tree.  The order is fixed, so the result is bit-reproducible run to
+// run.  Few slots (the LR static query: R floats) use narrow, deep workgroups
+// so that enough of them share the rows.
+template <class DT, int SPB>
 __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParams rp) {
+  constexpr int RL = 1024 / SPB;
   const int tid = threadIdx.x;
-  const int n_slot_blocks = (rp.n_part + kRedSlots - 1) / kRedSlots;
+  const int n_slot_blocks = (rp.n_part + SPB - 1) / SPB;
   if ((int)blockIdx.x < n_slot_blocks) {
-    // thread (rl, sl) sums rows rl, rl + 16, ... of slot sl; the 16 row sums
-    // are then added in row order
-    __shared__ float sh[kRedRows][kRedSlots + 1];
-    const int sl = tid % kRedSlots, rl = tid / kRedSlots;
-    const int slot = (int)blockIdx.x * kRedSlots + sl;
+    __shared__ float sh[RL][SPB + 1];
+    const int sl = tid % SPB, rl = tid / SPB;
+    const int slot = (int)blockIdx.x * SPB + sl;
     const bool regular = slot < rp.n_part && !(slot >= rp.part_extra && slot < rp.part_extra + rp.n_extra);
     float a = 0.f;
     if (regular) {
 #pragma unroll 8
-      for (int w = rl; w < rp.n_groups; w += kRedRows) a += rp.partials[(int64_t)w * rp.n_part + slot];
+      for (int w = rl; w < rp.n_groups; w += RL) a += rp.partials[(int64_t)w * rp.n_part + slot];
     }
     sh[rl][sl] = a;
     __syncthreads();
+    for (int o = RL / 2; o > 0; o >>= 1) {
+      if (rl < o) sh[rl][sl] += sh[rl + o][sl];
+      __syncthreads();
+    }
     if (rl == 0 && regular) {
-      float t = 0.f;
-      for (int r = 0; r < kRedRows; ++r) t += sh[r][sl];
+      const float t = sh[0][sl];
       if (slot >= rp.part_q && slot < rp.part_q + rp.n_q) {
         if (rp.dquery) DT::store1((typename DT::S*)rp.dquery + (slot - rp.part_q), t);
       } else if (slot >= rp.part_gate && slot < rp.part_gate + rp.n_gate) {
@@ -807,8 +808,13 @@ hipError_t launch_average_backward(int dtype, const ReadBwdParams& p, const Laun
 
 template <class DT>
 static hipError_t reduce_dt(const ReduceParams& rp, hipStream_t st) {
-  const int blocks = (rp.n_part + kRedSlots - 1) / kRedSlots + (rp.n_extra > 0 ? 1 : 0);
-  hipLaunchKernelGGL((reduce_partials_kernel<DT>), dim3(blocks), dim3(1024), 0, st, rp);
+  const int extra = rp.n_extra > 0 ? 1 : 0;
+  if (rp.n_part <= 512)
+    hipLaunchKernelGGL((reduce_partials_kernel<DT, 8>), dim3((rp.n_part + 7) / 8 + extra), dim3(1024), 0, st, rp);
+  else if (rp.n_part <= 2048)
+    hipLaunchKernelGGL((reduce_partials_kernel<DT, 16>), dim3((rp.n_part + 15) / 16 + extra), dim3(1024), 0, st, rp);
+  else
+    hipLaunchKernelGGL((reduce_partials_kernel<DT, 64>), dim3((rp.n_part + 63) / 64 + extra), dim3(1024), 0, st, rp);
   return hipGetLastError();
 }
 hipError_t launch_reduce_partials(int dtype, const ReduceParams& rp, hipStream_t st) {
