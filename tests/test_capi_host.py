@@ -175,3 +175,95 @@ def test_reference_argument_errors_are_kept():
     assert ops.attention_residual_read(vs[:1], torch.zeros(8), True) is vs[0]
     torch.testing.assert_close(ops.attention_residual_read(vs[:1], torch.zeros(8), True, normalize_output=True),
                                torch.nn.functional.rms_norm(vs[0], (8,)))
+
+
+def _p1desc(n_src=3, n_q=2, n_tok=16, dim=64, **kw):
+    vals = (ctypes.c_void_p * n_src)(*([0x1000] * n_src))
+    vstr = (ctypes.c_int64 * n_src)(*([dim] * n_src))
+    d = H.Phase1Desc()
+    d.n_src, d.n_q, d.dtype, d.logits_dtype, d.n_tok, d.dim = n_src, n_q, 1, 0, n_tok, dim
+    d.norm_eps = H.FLT_EPSILON
+    d.values, d.value_row_stride = vals, vstr
+    d.logits = 0x2000
+    d.logit_q_stride, d.logit_s_stride = n_src * n_tok, n_tok
+    for k, v in kw.items():
+        setattr(d, k, v)
+    d._keep = (vals, vstr)
+    return d
+
+
+def _p2desc(n_tok=16, dim=64, rank=0, **kw):
+    d = H.Phase2Desc()
+    d.dtype, d.n_tok, d.dim, d.rank, d.merge, d.key_norm = 1, n_tok, dim, rank, 0, 1
+    d.norm_eps, d.value_scale = H.FLT_EPSILON, 1.0
+    d.partial_value, d.partial_value_row_stride = 0x1000, dim
+    d.interblock_output, d.interblock_row_stride = 0x2000, dim
+    d.interblock_lse = ctypes.cast(ctypes.c_void_p(0x3000), ctypes.POINTER(ctypes.c_float))
+    d.query = 0x4000
+    if rank:
+        d.partial_key, d.partial_key_row_stride = 0x5000, rank
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@needs_lib
+def test_phase_host_validation_rejects_bad_descriptions_without_launching():
+    lib = H.load()
+    out = ctypes.c_void_p(0x6000)
+    lse = ctypes.cast(ctypes.c_void_p(0x7000), ctypes.POINTER(ctypes.c_float))
+    cases1 = [
+        (dict(n_q=0), -2, b"n_q"),
+        (dict(n_q=17), -2, b"n_q"),
+        (dict(dim=5000), -2, b"dim"),
+        (dict(logits=None), -1, b"logits"),
+        (dict(logit_s_stride=8), -1, b"overlap"),
+        (dict(logits_dtype=9), -1, b"dtype"),
+    ]
+    for kw, code, msg in cases1:
+        d = _p1desc(**kw)
+        rc = lib.attnres_phase1_forward(ctypes.byref(d), out, None, lse, None, None)
+        assert rc == code, (kw, rc, lib.attnres_last_error())
+        assert msg in lib.attnres_last_error(), lib.attnres_last_error()
+    cases2 = [
+        (dict(merge=5), -1, b"merge"),
+        (dict(rank=4096), -2, b"rank"),
+        (dict(logit_given=1), -1, b"partial_logit"),
+        (dict(rank=16, partial_key=None), -1, b"partial_key"),
+        (dict(query=None), -1, b"query"),
+        (dict(partial_value_row_stride=8), -1, b"stride"),
+    ]
+    for kw, code, msg in cases2:
+        d = _p2desc(**kw)
+        rc = lib.attnres_phase2_forward(ctypes.byref(d), out, None)
+        assert rc == code, (kw, rc, lib.attnres_last_error())
+        assert msg in lib.attnres_last_error(), lib.attnres_last_error()
+
+
+@needs_lib
+def test_phase2_workspace_size_is_a_host_computation():
+    lib = H.load()
+    d = _p2desc(n_tok=16384, dim=768)
+    # 2048 workgroups x (768 query + 1 bias + 1 value-scale slots)
+    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 2048 * 770 * 4
+    d = _p2desc(n_tok=100, dim=768, rank=64, scale_key=1)
+    # LR: 64 query slots, bias, value- and key-scale slots
+    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 100 * 67 * 4
+    d = _p2desc(n_tok=0, dim=768)
+    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 0
+
+
+def test_phase_ops_fail_loudly_on_cpu_tensors():
+    vs = [torch.randn(1, 2, 8) for _ in range(3)]
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attention_residual_phase1_from_logits(vs, torch.randn(2, 3, 1, 2))
+    p = torch.randn(1, 2, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attention_residual_phase2(p, torch.randn(8), p.clone(), torch.zeros(1, 2), True)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lrid_attention_residual_phase2_torch(p, torch.randn(1, 2, 4), torch.randn(1, 4), p.clone(),
+                                                 torch.zeros(1, 2), 0.5, True)
+    with pytest.raises(RuntimeError, match=r"logits must be \[Q, 3"):
+        ops.attention_residual_phase1_from_logits(vs, torch.randn(2, 4, 1, 2))
+    with pytest.raises(NotImplementedError):
+        ops.attention_residual_phase1(vs, torch.randn(2, 8), True)
