@@ -1,0 +1,265 @@
+"""Whole-model benchmark: block LR-AttnRes decoder vs the plain pre-norm decoder (reference: bench_attnres.py).
+
+Times one training step (or forward) of the decoder in ``attnres_decoder``
+with its AttnRes reads on the HIP kernels, beside the same decoder with a
+plain residual stream, and reports what the reference's script reports
+(``bench_attnres.py:150-318``): latency per step and the overhead of AttnRes
+over the baseline, plus end-to-end tokens/s and the share of the step spent
+in this library's kernels (from ``torch.profiler``'s device-time totals).
+
+Defaults are the whole-model configuration: 12 layers, d=768, 12 heads,
+MLP 4d, vocab 100277, block LR-AttnRes with rank 64 over 6 blocks (7 sources
+at the last read), B=16, T=1024, bf16 weights and activations (the model is
+cast with ``.to(bf16)``, as ``bench_attnres.py:180-181`` does), SDPA token
+attention, LM cross-entropy loss and an SGD update, random init and uniform
+random token ids.  Eager mode: no ``torch.compile``.
+
+    python lr-attnres_amd/bench_attnres.py [--batch_sizes 16] [--phase train] [--loss lm] ...
+
+Output: a header line, one CSV row per case and one JSON summary line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import os
+import sys
+
+import torch
+from torch.nn import functional as F
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
+
+import attnres_decoder as AD  # noqa: E402
+
+# Kernels of libattnres_hip.so (matched as substrings of the profiler's kernel names).
+ATTNRES_KERNELS = ("phase1_fwd_kernel", "phase1_bwd_kernel", "phase2_fwd_kernel", "phase2_bwd_kernel",
+                   "reduce_partials_kernel", "lr_fwd_kernel", "lr_bwd_kernel", "lr_fwd_fast_kernel",
+                   "lr_bwd_fast_kernel", "base_fwd_kernel", "base_bwd_kernel", "base_fwd_stream_kernel",
+                   "base_bwd_stream_kernel", "avg_fwd_kernel", "avg_bwd_kernel")
+
+
+def _bool(value):
+    if isinstance(value, bool):
+        return value
+    v = value.lower()
+    if v in {"true", "1", "yes", "y", "on"}:
+        return True
+    if v in {"false", "0", "no", "n", "off"}:
+        return False
+    raise argparse.ArgumentTypeError("expected a boolean value")
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description="Benchmark the block LR-AttnRes decoder on the HIP read kernels.")
+    p.add_argument("--n_layer", type=int, default=12)
+    p.add_argument("--n_head", type=int, default=12)
+    p.add_argument("--n_embd", type=int, default=768)
+    p.add_argument("--mlp_hidden_dim", type=int, default=None)
+    p.add_argument("--block_size", type=int, default=1024)
+    p.add_argument("--vocab_size", type=int, default=100277)
+    p.add_argument("--attnres_num_blocks", type=int, default=6)
+    p.add_argument("--batch_sizes", type=str, default="16")
+    p.add_argument("--lrid_ranks", type=str, default="64")
+    p.add_argument("--attnres_block_average", type=_bool, default=True)
+    p.add_argument("--attnres_block_average_mode", choices=("count", "sqrt"), default="count")
+    p.add_argument("--attnres_block_count_prior", type=_bool, default=True)
+    p.add_argument("--attnres_key_norm", type=_bool, default=True)
+    p.add_argument("--attnres_training_torch_phase2", type=_bool, default=True)
+    p.add_argument("--attnres_fuse_read_norm", type=_bool, default=True)
+    p.add_argument("--fold_block_summary", type=_bool, default=True)
+    p.add_argument("--dtype", choices=("fp32", "bf16", "fp16"), default="bf16")
+    p.add_argument("--phase", choices=("forward", "train"), default="train")
+    p.add_argument("--loss", choices=("hidden_mse", "lm"), default="lm")
+    p.add_argument("--optimizer_step", type=_bool, default=True)
+    p.add_argument("--lr", type=float, default=1e-4)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--iters", type=int, default=10)
+    p.add_argument("--cases", type=str, default="baseline,lrid_fused",
+                   help="comma-separated: baseline (plain pre-norm), lrid_fused (block LR-AttnRes on HIP)")
+    p.add_argument("--nonzero_attnres_queries", type=_bool, default=True)
+    p.add_argument("--profile_iters", type=int, default=2,
+                   help="extra steps under torch.profiler for the kernel share (0 = skip)")
+    p.add_argument("--seed", type=int, default=1234)
+    return p.parse_args(argv)
+
+
+def resolve_dtype(name):
+    return {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[name]
+
+
+def make_config(args, use_attnres, rank):
+    return AD.DecoderConfig(
+        n_layer=args.n_layer, n_head=args.n_head, n_embd=args.n_embd, mlp_hidden_dim=args.mlp_hidden_dim,
+        vocab_size=args.vocab_size, block_size=args.block_size, norm_pos="before", use_attnres=use_attnres,
+        attnres_num_blocks=args.attnres_num_blocks, attnres_block_average=args.attnres_block_average,
+        attnres_block_average_mode=args.attnres_block_average_mode,
+        attnres_block_count_prior=args.attnres_block_count_prior, attnres_key_norm=args.attnres_key_norm,
+        attnres_training_torch_phase2=args.attnres_training_torch_phase2,
+        attnres_fuse_read_norm=args.attnres_fuse_read_norm, lrid_rank=rank or 64, lrid_num_heads=1,
+        lrid_use_logit_scale=True, fold_block_summary=args.fold_block_summary)
+
+
+def training_loss(args, model, idx, targets):
+    if args.loss == "hidden_mse":
+        return model(idx, return_hidden=True).float().square().mean()
+    logits = model(idx)
+    return F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.view(-1))
+
+
+def train_step(args, model, idx, targets):
+    for p in model.parameters():
+        p.grad = None
+    loss = training_loss(args, model, idx, targets)
+    loss.backward()
+    if args.optimizer_step:
+        with torch.no_grad():
+            for p in model.parameters():
+                if p.grad is not None:
+                    p.add_(p.grad, alpha=-args.lr)
+    return loss
+
+
+def _device_time_us(event):
+    for attr in ("self_device_time_total", "self_cuda_time_total"):
+        if hasattr(event, attr):
+            return float(getattr(event, attr))
+    return 0.0
+
+
+def kernel_share(step, iters):
+    """(attnres kernel µs per step, all kernels µs per step) from torch.profiler, or (None, None)."""
+    try:
+        from torch.profiler import ProfilerActivity, profile
+    except ImportError:
+        return None, None
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for _ in range(iters):
+            step()
+        torch.cuda.synchronize()
+    total = attn = 0.0
+    for ev in prof.key_averages():
+        t = _device_time_us(ev)
+        total += t
+        if any(k in ev.key for k in ATTNRES_KERNELS):
+            attn += t
+    if total == 0.0:
+        return None, None
+    return attn / iters, total / iters
+
+
+def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
+    torch.manual_seed(args.seed)
+    cfg = make_config(args, use_attnres, rank)
+    with torch.device(device):
+        model = AD.Decoder(cfg)
+    if args.nonzero_attnres_queries and use_attnres:
+        with torch.no_grad():
+            for q in model.transformer.lrid_queries:
+                q.normal_(0.0, cfg.init_std)
+    model.to(dtype=dtype)
+    model.train(args.phase == "train")
+    gen = torch.Generator(device=device).manual_seed(args.seed + 1)
+    idx = torch.randint(0, args.vocab_size, (batch, args.block_size), device=device, generator=gen)
+    targets = torch.randint(0, args.vocab_size, (batch, args.block_size), device=device, generator=gen)
+
+    if args.phase == "forward":
+        def step():
+            with torch.inference_mode():
+                model(idx, return_hidden=True)
+    else:
+        def step():
+            train_step(args, model, idx, targets)
+
+    try:
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.iters):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        latency_ms = start.elapsed_time(end) / args.iters
+        attn_us = total_us = None
+        if args.profile_iters > 0:
+            attn_us, total_us = kernel_share(step, args.profile_iters)
+        n_params = model.get_num_params()
+    finally:
+        del model, idx, targets
+        gc.collect()
+        torch.cuda.empty_cache()
+    return {
+        "label": label,
+        "batch": batch,
+        "rank": rank or "",
+        "latency_ms": latency_ms,
+        "tokens_per_s": batch * args.block_size / (latency_ms * 1e-3),
+        "attnres_kernel_ms": None if attn_us is None else attn_us / 1000.0,
+        "device_kernel_ms": None if total_us is None else total_us / 1000.0,
+        "params": n_params,
+    }
+
+
+def _fmt(x, spec):
+    return "" if x is None else format(x, spec)
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if not torch.cuda.is_available():
+        raise RuntimeError("a ROCm GPU is required for this benchmark")
+    device = torch.device("cuda")
+    dtype = resolve_dtype(args.dtype)
+    batches = [int(x) for x in args.batch_sizes.split(",") if x.strip()]
+    ranks = [int(x) for x in args.lrid_ranks.split(",") if x.strip()]
+    cases = {x.strip() for x in args.cases.split(",") if x.strip()}
+    unknown = cases - {"baseline", "lrid_fused"}
+    if unknown:
+        raise SystemExit(f"unknown cases: {sorted(unknown)}")
+
+    print(f"dtype={args.dtype} phase={args.phase} loss={args.loss} optimizer_step={args.optimizer_step} "
+          f"n_layer={args.n_layer} n_embd={args.n_embd} n_head={args.n_head} vocab={args.vocab_size} "
+          f"T={args.block_size} blocks={args.attnres_num_blocks} fold_block_summary={args.fold_block_summary} "
+          f"torch={torch.__version__} device={torch.cuda.get_device_name(0)}", flush=True)
+    print("case,batch,rank,latency_ms,overhead_vs_baseline_pct,tokens_per_s,attnres_kernel_ms,"
+          "attnres_kernel_share_pct", flush=True)
+    summary = []
+    for batch in batches:
+        rows = []
+        base = None
+        if "baseline" in cases:
+            base = measure_case(args, device, dtype, batch, "baseline_prenorm", False)
+            rows.append(base)
+        if "lrid_fused" in cases:
+            for rank in ranks:
+                rows.append(measure_case(args, device, dtype, batch, "lrid_fused", True, rank))
+        for row in rows:
+            row["overhead_vs_baseline_pct"] = (None if base is None else
+                                               100.0 * (row["latency_ms"] / base["latency_ms"] - 1.0))
+            row["attnres_kernel_share_pct"] = (None if row["attnres_kernel_ms"] is None else
+                                               100.0 * row["attnres_kernel_ms"] / row["latency_ms"])
+            print(f"{row['label']},{row['batch']},{row['rank']},{row['latency_ms']:.3f},"
+                  f"{_fmt(row['overhead_vs_baseline_pct'], '.2f')},{row['tokens_per_s']:.0f},"
+                  f"{_fmt(row['attnres_kernel_ms'], '.3f')},{_fmt(row['attnres_kernel_share_pct'], '.2f')}",
+                  flush=True)
+        summary.extend(rows)
+    print(json.dumps({
+        "metric": "whole-model step tokens/s; AttnRes share of step time",
+        "workload": "c5" if (args.n_layer, args.n_embd, args.n_head, args.vocab_size, args.block_size,
+                             args.attnres_num_blocks) == (12, 768, 12, 100277, 1024, 6) else "custom",
+        "phase": args.phase, "loss": args.loss, "optimizer_step": args.optimizer_step, "dtype": args.dtype,
+        "data": "synthetic (uniform random token ids, random init)",
+        "cases": summary,
+    }), flush=True)
+    return summary
+
+
+if __name__ == "__main__":
+    main()
