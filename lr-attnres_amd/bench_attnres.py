@@ -36,11 +36,8 @@ if HERE not in sys.path:
 
 import attnres_decoder as AD  # noqa: E402
 
-# Kernels of libattnres_hip.so (matched as substrings of the profiler's kernel names).
-ATTNRES_KERNELS = ("phase1_fwd_kernel", "phase1_bwd_kernel", "phase2_fwd_kernel", "phase2_bwd_kernel",
-                   "reduce_partials_kernel", "lr_fwd_kernel", "lr_bwd_kernel", "lr_fwd_fast_kernel",
-                   "lr_bwd_fast_kernel", "base_fwd_kernel", "base_bwd_kernel", "base_fwd_stream_kernel",
-                   "base_bwd_stream_kernel", "avg_fwd_kernel", "avg_bwd_kernel")
+# Every kernel of libattnres_hip.so lives in the C++ namespace ``attnres``.
+ATTNRES_KERNEL_PREFIX = "attnres::"
 
 
 def _bool(value):
@@ -145,7 +142,7 @@ def kernel_share(step, iters):
     for ev in prof.key_averages():
         t = _device_time_us(ev)
         total += t
-        if any(k in ev.key for k in ATTNRES_KERNELS):
+        if ATTNRES_KERNEL_PREFIX in ev.key:
             attn += t
     if total == 0.0:
         return None, None

@@ -646,6 +646,41 @@ int phase2_waves(const attnres_phase2_desc* d, const PhasePlan& pl) {
   return kw > w ? kw : w;
 }
 
+// One wave per token when a wave covers the row with at most 16 elements per
+// lane and the LR key with at most 4: fp32 rows in 16-byte vectors (1-4 per
+// lane), 16-bit rows in 16-byte vectors (1-2 per lane) or, where those would
+// leave lanes idle (D <= 256, 512 < D <= 768), in 8-byte vectors (1 or 3).
+// ATTNRES_PHASE2_LAYOUT=block (read by the host on every call) keeps the
+// workgroup-per-token kernels: the two layouts give the same per-token
+// results, which a test checks with this switch.
+constexpr int kPhase2Teams = 4;  // tokens (waves) per workgroup
+struct P2Wave {
+  int vb, cb, ncols;
+};
+bool phase2_wave_plan(const attnres_phase2_desc* d, const PhasePlan& pl, P2Wave* w) {
+  const char* env = getenv("ATTNRES_PHASE2_LAYOUT");
+  if (env && strcmp(env, "block") == 0) return false;
+  if (!pl.vec || d->rank > 4 * kWaveSize) return false;
+  const int D = d->dim;
+  if (elem_size(d->dtype) == 4) {
+    w->vb = 16;
+    w->ncols = (D + 255) / 256;
+    w->cb = w->ncols;
+    return w->ncols <= 4;
+  }
+  if (D <= 256 || (D > 512 && D <= 768)) {
+    w->vb = 8;
+    w->ncols = (D + 255) / 256;
+    w->cb = w->ncols == 1 ? 1 : 3;
+    return true;
+  }
+  if (D > 1024) return false;
+  w->vb = 16;
+  w->ncols = (D + 511) / 512;
+  w->cb = w->ncols;
+  return true;
+}
+
 }  // namespace
 
 extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, void* out_prenorm, float* lse,
@@ -755,10 +790,21 @@ extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, v
   Launch L;
   memset(&L, 0, sizeof(L));
   L.vec = pl.vec;
-  L.wpt = phase2_waves(d, pl);
   L.nmax = (d->rank > 0 && !d->logit_given) ? 1 : 0;
-  L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
-  L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
+  P2Wave wv;
+  if (phase2_wave_plan(d, pl, &wv)) {
+    p.ncols = wv.ncols;
+    L.teams = kPhase2Teams;
+    L.vb = wv.vb;
+    L.wpt = wv.cb;
+    const int64_t wgs = (d->n_tok + kPhase2Teams - 1) / kPhase2Teams;
+    L.grid = (int)(wgs < kMaxFwdGroups ? wgs : kMaxFwdGroups);
+    L.lds = 0;
+  } else {
+    L.wpt = phase2_waves(d, pl);
+    L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
+    L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
+  }
   hipError_t err = launch_phase2_forward(d->dtype, p, L, (hipStream_t)stream);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 forward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
@@ -810,10 +856,22 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
   Launch L;
   memset(&L, 0, sizeof(L));
   L.vec = pl.vec;
-  L.wpt = phase2_waves(d, pl);
   L.nmax = lr ? 1 : 0;
-  L.grid = (int)groups;
-  L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
+  P2Wave wv;
+  if (phase2_wave_plan(d, pl, &wv)) {
+    // at most bwd_groups(n_tok) workgroups, so the workspace size above holds
+    p.ncols = wv.ncols;
+    L.teams = kPhase2Teams;
+    L.vb = wv.vb;
+    L.wpt = wv.cb;
+    const int64_t wgs = (d->n_tok + kPhase2Teams - 1) / kPhase2Teams;
+    L.grid = (int)(wgs < groups ? wgs : groups);
+    L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
+  } else {
+    L.wpt = phase2_waves(d, pl);
+    L.grid = (int)groups;
+    L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
+  }
   hipError_t err = launch_phase2_backward(d->dtype, p, L, st);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 backward launch failed: %s", hipGetErrorString(err));
   if (PL.n_part > 0) {

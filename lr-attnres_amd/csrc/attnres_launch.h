@@ -14,7 +14,8 @@ struct Launch {
   int grid;     // workgroups (persistent over tokens)
   size_t lds;   // dynamic LDS bytes
   int nmax;     // base read: register-resident source slots (8/16; more = streaming)
-  int teams;    // token teams per workgroup (LR backward)
+  int teams;    // token teams per workgroup (LR backward; phase 2: waves per workgroup)
+  int vb;       // phase 2 one-wave-per-token kernels: vector bytes (16 or 8)
 };
 
 hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);

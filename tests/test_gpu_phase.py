@@ -215,6 +215,44 @@ def test_lrid_phase2_key_widths(R):
     _check_phase2(out, grads, ref_out, ref_grads, torch.bfloat16)
 
 
+@pytest.mark.parametrize("variant,dtype", [("lrid", torch.bfloat16), ("base", torch.float32),
+                                           ("lrid_addcmul", torch.float32)])
+def test_phase2_many_tokens_matches_oracle(variant, dtype):
+    """More tokens than workgroups x waves (16400 > 2048 x 4): each wave walks
+    several tokens and the cross-token sums go through many partial rows.
+    (At this many tokens a 16-bit base-key case meets one-ulp flips of a
+    per-token scalar -- dprob, the logit -- whose fp32 sum order differs from
+    the oracle's; that case is covered by the layout test below.)"""
+    t = _phase2_case(300 + len(variant), dtype, 4, 4100, 768, variant)
+    m = dict(variant=variant, key_norm=True, bias=0.4, bias_tensor=True, normalize_output=True, scale=0.125)
+    out, grads = _phase2_hip(t, m)
+    ref_out, ref_grads = _phase2_oracle(t, m)
+    _check_phase2(out, grads, ref_out, ref_grads, dtype)
+
+
+@pytest.mark.parametrize("variant", ["base", "lrid", "lrid_addcmul", "logit"])
+@pytest.mark.parametrize("D", [512, 1024])
+def test_phase2_wave_layout_matches_block_layout(variant, D, monkeypatch):
+    """For rows one wave covers with 16-byte vectors, phase 2 runs one wave
+    per token; the workgroup-per-token kernels (ATTNRES_PHASE2_LAYOUT=block)
+    sum each row in the same order, so every per-token output and gradient
+    is bit-identical in bf16.  Cross-token sums (query, bias) walk tokens in
+    another order and are compared at the reduced bound.  (D=768 uses 8-byte
+    vectors, whose sums associate differently; it is checked against the
+    oracle by the tests above.)"""
+    t = _phase2_case(700 + D + len(variant), torch.bfloat16, 4, 4100, D, variant)
+    m = dict(variant=variant, key_norm=True, bias=0.4, bias_tensor=True, normalize_output=True, scale=0.125)
+    out_w, g_w = _phase2_hip(t, m)
+    monkeypatch.setenv("ATTNRES_PHASE2_LAYOUT", "block")
+    out_b, g_b = _phase2_hip(t, m)
+    assert torch.equal(out_w, out_b)
+    for key in g_w:
+        if key in ("dquery", "dbias"):
+            assert_close(g_w[key], g_b[key], torch.bfloat16, key, reduced=True)
+        else:
+            assert torch.equal(g_w[key], g_b[key]), key
+
+
 # ------------------------------------------------------------------ block summaries folded into phase 2
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
