@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 3
+#define ATTNRES_ABI_VERSION 4
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -266,6 +266,49 @@ int attnres_phase2_backward(const attnres_phase2_desc* desc, const attnres_phase
 
 /* Workspace bytes attnres_phase2_backward needs (host-only). */
 size_t attnres_phase2_backward_workspace_size(const attnres_phase2_desc* desc);
+
+/*
+ * Key-producer epilogue: split of a sublayer's fused output projection.
+ *
+ * The reference's LR sublayers project to dim + projection_rank columns with
+ * one GEMM and take the sublayer output and its LR key from the result
+ * (LRIDFusedProjection.forward, model.py:363-388; per-head key norm
+ * _norm_lrid_key, model.py:34-37):
+ *     out = y[:, :dim].contiguous()
+ *     key = y[:, dim:dim + rank], rms-normed over each of `heads` groups of
+ *           rank/heads columns when key_norm (fp32 math, one rounding)
+ * y is [n_tok, row_stride] (row_stride >= proj_cols >= dim + rank), so the
+ * GEMM output is consumed in place.  The forward writes out (dense
+ * [n_tok, dim]), key (dense [n_tok, rank]) and, when key_norm, the fp32
+ * inverse rms of each (token, head) [n_tok, heads].
+ */
+typedef struct attnres_keyed_split_desc {
+  int32_t dtype;
+  int64_t n_tok;
+  int32_t dim;        /* sublayer output columns */
+  int32_t rank;       /* key columns (rank % heads == 0; rank <= 256) */
+  int32_t proj_cols;  /* columns of y that carry gradient (dim + projection_rank) */
+  int32_t heads;      /* depth heads of the key norm: rank/heads a power of two,
+                         or a multiple of 64 */
+  int32_t key_norm;
+  float norm_eps;     /* torch's default: FLT_EPSILON */
+  const void* projected;  /* y, device */
+  int64_t row_stride;     /* elements between rows of y */
+} attnres_keyed_split_desc;
+
+/* Replaces the slice / .contiguous() / _norm_lrid_key sequence of
+ * model.py:374-378 with one pass over y. */
+int attnres_keyed_split_forward(const attnres_keyed_split_desc* desc, void* out, void* key, float* key_inv_rms,
+                                void* stream);
+
+/* Gradient of y, dense [n_tok, proj_cols]: columns [0, dim) take grad_out,
+ * columns [dim, dim + rank) the rms-norm backward of grad_key (or grad_key
+ * itself without key_norm; key_inv_rms from the forward), the rest zero.
+ * grad_out or grad_key may be NULL (a zero gradient).  Replaces the autograd
+ * of the slices and the key norm (two zero-filled [n_tok, proj_cols] buffers,
+ * two slice copies and their sum) with one pass. */
+int attnres_keyed_split_backward(const attnres_keyed_split_desc* desc, const void* grad_out, const void* grad_key,
+                                 const float* key_inv_rms, void* grad_projected, void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_SOURCES = 64
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -153,6 +153,13 @@ def library_path() -> str:
     return LIB_PATH
 
 
+class KeyedSplitDesc(ctypes.Structure):
+    """attnres_keyed_split_desc (include/attnres_hip.h)."""
+    _fields_ = [("dtype", c_int32), ("n_tok", c_int64), ("dim", c_int32), ("rank", c_int32),
+                ("proj_cols", c_int32), ("heads", c_int32), ("key_norm", c_int32), ("norm_eps", c_float),
+                ("projected", c_void_p), ("row_stride", c_int64)]
+
+
 def load() -> ctypes.CDLL:
     """Load the HIP library once; raise with a build hint if it is missing."""
     global _lib
@@ -184,6 +191,12 @@ def load() -> ctypes.CDLL:
     lib.attnres_phase2_backward.argtypes = [POINTER(Phase2Desc), POINTER(Phase2Grads), c_void_p]
     lib.attnres_phase2_backward_workspace_size.restype = c_size_t
     lib.attnres_phase2_backward_workspace_size.argtypes = [POINTER(Phase2Desc)]
+    lib.attnres_keyed_split_forward.restype = c_int
+    lib.attnres_keyed_split_forward.argtypes = [POINTER(KeyedSplitDesc), c_void_p, c_void_p, POINTER(c_float),
+                                                c_void_p]
+    lib.attnres_keyed_split_backward.restype = c_int
+    lib.attnres_keyed_split_backward.argtypes = [POINTER(KeyedSplitDesc), c_void_p, c_void_p, POINTER(c_float),
+                                                 c_void_p, c_void_p]
     v = lib.attnres_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libattnres_hip ABI {v} != expected {ABI_VERSION}; rebuild the library")
@@ -477,3 +490,53 @@ def phase2_backward(desc: Phase2, device, dtype, grad_out, want_dquery, query_sh
     rc = lib.attnres_phase2_backward(ctypes.byref(desc.c), ctypes.byref(g), _stream(device))
     _check(rc, "phase-2 backward")
     return dp, dpk, dq, di, dl, dlg, db, ds
+
+
+def keyed_split_desc(dtype, n_tok: int, proj_cols: int, row_stride: int, ptr, dim: int, rank: int, heads: int,
+                     key_norm: bool) -> KeyedSplitDesc:
+    """Descriptor of a projection y [n_tok, proj_cols] whose rows are row_stride elements apart."""
+    if dtype not in DTYPE_CODE:
+        raise RuntimeError(f"keyed split: dtype {dtype} is not supported (fp32, bf16, fp16)")
+    d = KeyedSplitDesc()
+    d.dtype = DTYPE_CODE[dtype]
+    d.n_tok = n_tok
+    d.dim = dim
+    d.rank = rank
+    d.proj_cols = proj_cols
+    d.heads = heads
+    d.key_norm = 1 if key_norm else 0
+    d.norm_eps = FLT_EPSILON
+    d.projected = ptr
+    d.row_stride = row_stride
+    return d
+
+
+def keyed_split_forward(y2d: torch.Tensor, dim: int, rank: int, heads: int, key_norm: bool):
+    """(out [n_tok, dim], key [n_tok, rank], key_inv_rms [n_tok, heads] fp32, or [0] without key norm)."""
+    lib = load()
+    n, P = y2d.size(0), y2d.size(1)
+    d = keyed_split_desc(y2d.dtype, n, P, y2d.stride(0) if n > 1 else P, y2d.data_ptr() if n else None, dim, rank,
+                         heads, key_norm)
+    out = torch.empty((n, dim), device=y2d.device, dtype=y2d.dtype)
+    key = torch.empty((n, rank), device=y2d.device, dtype=y2d.dtype)
+    inv = torch.empty((n, heads) if key_norm else (0,), device=y2d.device, dtype=torch.float32)
+    rc = lib.attnres_keyed_split_forward(ctypes.byref(d), _ptr(out), _ptr(key), _fptr(inv) if key_norm else None,
+                                         _stream(y2d.device))
+    _check(rc, "keyed split forward")
+    return out, key, inv
+
+
+def keyed_split_backward(y2d, n: int, P: int, dim: int, rank: int, heads: int, key_norm: bool, grad_out, grad_key,
+                         inv, dtype, device):
+    """Gradient of y, dense [n, P].  y2d (the forward's projection) is read only for the key norm."""
+    lib = load()
+    if y2d is not None:
+        d = keyed_split_desc(dtype, n, P, y2d.stride(0) if n > 1 else P, y2d.data_ptr() if n else None, dim, rank,
+                             heads, key_norm)
+    else:
+        d = keyed_split_desc(dtype, n, P, P, None, dim, rank, heads, key_norm)
+    gy = torch.empty((n, P), device=device, dtype=dtype)
+    rc = lib.attnres_keyed_split_backward(ctypes.byref(d), _ptr(grad_out), _ptr(grad_key),
+                                          _fptr(inv) if key_norm else None, _ptr(gy), _stream(device))
+    _check(rc, "keyed split backward")
+    return gy

@@ -181,26 +181,22 @@ class KeyedOutputProjection(nn.Module):
 
     One GEMM produces ``D + projection_rank`` columns; the first ``rank`` of
     the extra columns are the key, rms-normed per depth head when key norm is
-    on.
+    on.  The split is ``ops.lrid_fused_projection_split`` (one HIP pass each
+    way, in place of slicing, copying and norming in separate kernels).
     """
 
-    def __init__(self, config: DecoderConfig, input_dim: int, output_dim: int):
+    def __init__(self, config: DecoderConfig, input_dim: int, output_dim: int, ops):
         super().__init__()
         self.output_dim = output_dim
         self.rank = config.lrid_rank
         self.heads = config.lrid_num_heads
         self.key_norm = config.attnres_key_norm
+        self.ops = ops
         self.proj = nn.Linear(input_dim, output_dim + config.lrid_projection_rank, bias=False)
 
-    def forward(self, x: Tensor, emit_key: bool = True):
-        if not emit_key:
-            return F.linear(x, self.proj.weight[:self.output_dim], None), None
-        projected = self.proj(x)
-        out = projected[..., :self.output_dim].contiguous()
-        key = projected[..., self.output_dim:self.output_dim + self.rank]
-        if self.key_norm:
-            key = _norm_heads(key, self.heads)
-        return out, key
+    def forward(self, x: Tensor):
+        return self.ops.lrid_fused_projection_split(self.proj(x), self.output_dim, self.rank, self.heads,
+                                                    self.key_norm)
 
 
 class SourceKeyProjection(nn.Module):
@@ -230,7 +226,7 @@ def _attend(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
 class MultiHeadAttention(nn.Module):
     """Causal self-attention with qk-norm and rotary positions (``model.py:430-569``)."""
 
-    def __init__(self, config: DecoderConfig):
+    def __init__(self, config: DecoderConfig, ops=None):
         super().__init__()
         self.n_head = config.n_head
         self.n_embd = config.n_embd
@@ -240,7 +236,7 @@ class MultiHeadAttention(nn.Module):
         self.rope = RotaryEmbedding(config)
         self.c_attn = nn.Linear(config.n_embd, 3 * config.n_embd, bias=False)
         if self.keyed:
-            self.c_proj = KeyedOutputProjection(config, config.n_embd, config.n_embd)
+            self.c_proj = KeyedOutputProjection(config, config.n_embd, config.n_embd, ops)
         else:
             self.c_proj = nn.Linear(config.n_embd, config.n_embd, bias=False)
 
@@ -264,13 +260,13 @@ class MultiHeadAttention(nn.Module):
 class MLP(nn.Module):
     """SwiGLU MLP: ``fc2(silu(gate) * up)`` with ``[up, gate] = fc1(x)`` (``model.py:572-589``)."""
 
-    def __init__(self, config: DecoderConfig):
+    def __init__(self, config: DecoderConfig, ops=None):
         super().__init__()
         hidden = config.hidden_dim
         self.keyed = config.use_attnres
         self.fc1 = nn.Linear(config.n_embd, 2 * hidden, bias=False)
         if self.keyed:
-            self.fc2 = KeyedOutputProjection(config, hidden, config.n_embd)
+            self.fc2 = KeyedOutputProjection(config, hidden, config.n_embd, ops)
         else:
             self.fc2 = nn.Linear(hidden, config.n_embd, bias=False)
 
@@ -289,11 +285,11 @@ class Block(nn.Module):
     residual stream (plain addition for the baseline, AttnRes reads otherwise).
     """
 
-    def __init__(self, config: DecoderConfig):
+    def __init__(self, config: DecoderConfig, ops=None):
         super().__init__()
         self.norm_pos = config.norm_pos
-        self.attn = MultiHeadAttention(config)
-        self.mlp = MLP(config)
+        self.attn = MultiHeadAttention(config, ops)
+        self.mlp = MLP(config, ops)
 
     def _sublayer(self, fn, x: Tensor, x_is_normalized: bool):
         if self.norm_pos in {"before", "both"} and not x_is_normalized:
@@ -325,11 +321,11 @@ class Decoder(nn.Module):
     def __init__(self, config: DecoderConfig, ops=None):
         super().__init__()
         self.config = config
-        self._ops = ops
+        self.ops = ops if ops is not None else (_default_ops() if config.use_attnres else None)
         self.block_ends = block_ends(config.n_layer, config.attnres_num_blocks) if config.use_attnres else None
         modules = dict(
             wte=nn.Embedding(config.vocab_size, config.n_embd),
-            layers=nn.ModuleList([Block(config) for _ in range(config.n_layer)]),
+            layers=nn.ModuleList([Block(config, self.ops) for _ in range(config.n_layer)]),
         )
         if config.use_attnres:
             modules["lrid_embedding_key"] = SourceKeyProjection(config)
@@ -359,12 +355,6 @@ class Decoder(nn.Module):
 
     def get_num_params(self) -> int:
         return sum(p.numel() for p in self.parameters())
-
-    @property
-    def ops(self):
-        if self._ops is None:
-            self._ops = _default_ops()
-        return self._ops
 
     # -- forward ------------------------------------------------------------
 

@@ -713,3 +713,77 @@ def lrid_attention_residual_phase2_torch(partial_value: Tensor, partial_key: Ten
     return _phase2(partial_value, partial_key, query, None, interblock_output, interblock_lse, _hip.MERGE_LERP,
                    key_norm, normalize_output, logit_scale, logit_bias, partial_scale, scale_key,
                    "lrid_attention_residual_phase2_torch")
+
+
+# ------------------------------------------------------------------ key-producer epilogue
+
+@torch.library.custom_op("attnres_hip::keyed_split", mutates_args=())
+def _keyed_split_op(y: Tensor, dim: int, rank: int, heads: int, key_norm: bool) -> tuple[Tensor, Tensor, Tensor]:
+    return _hip.keyed_split_forward(y, dim, rank, heads, key_norm)
+
+
+@_keyed_split_op.register_fake
+def _keyed_split_fake(y, dim, rank, heads, key_norm):
+    n = y.size(0)
+    return (y.new_empty((n, dim)), y.new_empty((n, rank)),
+            y.new_empty((n, heads) if key_norm else (0,), dtype=torch.float32))
+
+
+@torch.library.custom_op("attnres_hip::keyed_split_backward", mutates_args=())
+def _keyed_split_backward_op(y: Optional[Tensor], grad_out: Optional[Tensor], grad_key: Optional[Tensor],
+                             inv: Tensor, n_tok: int, proj_cols: int, dim: int, rank: int, heads: int,
+                             key_norm: bool) -> Tensor:
+    like = grad_out if grad_out is not None else grad_key
+    return _hip.keyed_split_backward(y, n_tok, proj_cols, dim, rank, heads, key_norm, grad_out, grad_key, inv,
+                                     like.dtype, like.device)
+
+
+@_keyed_split_backward_op.register_fake
+def _keyed_split_backward_fake(y, grad_out, grad_key, inv, n_tok, proj_cols, dim, rank, heads, key_norm):
+    like = grad_out if grad_out is not None else grad_key
+    return like.new_empty((n_tok, proj_cols))
+
+
+def _keyed_split_setup_context(ctx, inputs, output):
+    y, dim, rank, heads, key_norm = inputs
+    ctx.args = (y.size(0), y.size(1), dim, rank, heads, key_norm)
+    # the raw key (inside y) is read only by the key-norm backward
+    ctx.save_for_backward(y if key_norm else None, output[2])
+
+
+def _keyed_split_backward(ctx, grad_out, grad_key, grad_inv):
+    y, inv = ctx.saved_tensors
+    go = grad_out.contiguous() if grad_out is not None else None
+    gk = grad_key.contiguous() if grad_key is not None else None
+    if go is None and gk is None:
+        return None, None, None, None, None
+    return _keyed_split_backward_op(y, go, gk, inv, *ctx.args), None, None, None, None
+
+
+_keyed_split_op.register_autograd(_keyed_split_backward, setup_context=_keyed_split_setup_context)
+
+
+def lrid_fused_projection_split(projected: Tensor, output_dim: int, rank: int, num_heads: int = 1,
+                                key_norm: bool = True):
+    """Sublayer output and LR key from a fused ``[out | key | pad]`` projection.
+
+    Not in the reference's op module: the reference does this in
+    ``LRIDFusedProjection.forward`` (model.py:363-388) as
+    ``out = projected[..., :D].contiguous()``, ``key = projected[..., D:D+rank]``
+    and, with key norm, ``_norm_lrid_key(key, num_heads)`` (model.py:34-37).
+    Here one HIP pass writes both (the key rms-normed per depth head in fp32,
+    torch's default eps) and the backward writes the projection's gradient
+    ``[d_out | norm backward of d_key | 0]`` in one pass, instead of two
+    zero-filled slice gradients and their sum.  ``projected`` is ``[..., >= D +
+    rank]`` on the GPU; returns ``(out [..., D], key [..., rank])``.
+    """
+    if projected.size(-1) < output_dim + rank:
+        raise RuntimeError(f"lrid_fused_projection_split: projection has {projected.size(-1)} columns, "
+                           f"needs at least {output_dim + rank}")
+    _check_gpu([projected], "lrid_fused_projection_split")
+    lead = projected.shape[:-1]
+    y = projected.reshape(-1, projected.size(-1))
+    if y.stride(-1) != 1:
+        y = y.contiguous()
+    out, key, _ = _keyed_split_op(y, int(output_dim), int(rank), int(num_heads), bool(key_norm))
+    return out.view(*lead, output_dim), key.view(*lead, rank)

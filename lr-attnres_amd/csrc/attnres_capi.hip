@@ -895,3 +895,94 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
   }
   return ATTNRES_OK;
 }
+
+// ---------------------------------------------------------------- key-producer epilogue
+namespace {
+
+constexpr int kKeySplitTeams = 4;  // tokens (waves) per workgroup
+
+int check_keyed_split(const attnres_keyed_split_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->dtype < 0 || d->dtype > 2) return fail(ATTNRES_EINVAL, "unknown dtype %d", d->dtype);
+  if (d->n_tok < 0 || d->n_tok > INT32_MAX) return fail(ATTNRES_EINVAL, "n_tok=%lld outside [0, 2^31)", (long long)d->n_tok);
+  if (d->dim < 1 || d->rank < 1) return fail(ATTNRES_EINVAL, "dim=%d / rank=%d must be positive", d->dim, d->rank);
+  if (d->rank > 4 * kWaveSize)
+    return fail(ATTNRES_EUNSUPPORTED, "rank=%d exceeds %d", d->rank, 4 * kWaveSize);
+  if (d->heads < 1 || d->rank % d->heads != 0)
+    return fail(ATTNRES_EINVAL, "heads=%d must divide rank=%d", d->heads, d->rank);
+  const int hd = d->rank / d->heads;
+  const bool pow2 = (hd & (hd - 1)) == 0;
+  if (d->key_norm && !((hd < kWaveSize && pow2) || hd % kWaveSize == 0))
+    return fail(ATTNRES_EUNSUPPORTED, "key head width %d must be a power of two below 64 or a multiple of 64", hd);
+  if (d->proj_cols < d->dim + d->rank)
+    return fail(ATTNRES_EINVAL, "proj_cols=%d < dim + rank = %d", d->proj_cols, d->dim + d->rank);
+  if (d->row_stride < d->proj_cols)
+    return fail(ATTNRES_EINVAL, "row_stride=%lld < proj_cols=%d", (long long)d->row_stride, d->proj_cols);
+  return ATTNRES_OK;
+}
+
+void fill_keyed_split(const attnres_keyed_split_desc* d, KeySplitParams* p, Launch* L, bool vec) {
+  memset(p, 0, sizeof(*p));
+  p->y = d->projected;
+  p->n_tok = d->n_tok;
+  p->y_stride = d->row_stride;
+  p->D = d->dim;
+  p->R = d->rank;
+  p->P = d->proj_cols;
+  p->H = d->heads;
+  p->hd = d->rank / d->heads;
+  p->key_norm = d->key_norm ? 1 : 0;
+  p->eps = d->norm_eps;
+  memset(L, 0, sizeof(*L));
+  L->vec = vec ? 1 : 0;
+  L->teams = kKeySplitTeams;
+  const int64_t wgs = (d->n_tok + kKeySplitTeams - 1) / kKeySplitTeams;
+  L->grid = (int)(wgs < kMaxFwdGroups ? wgs : kMaxFwdGroups);
+}
+
+}  // namespace
+
+extern "C" int attnres_keyed_split_forward(const attnres_keyed_split_desc* d, void* out, void* key,
+                                           float* key_inv_rms, void* stream) {
+  int rc = check_keyed_split(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!d->projected || !out || !key) return fail(ATTNRES_EINVAL, "projected / out / key is NULL");
+  if (d->key_norm && !key_inv_rms) return fail(ATTNRES_EINVAL, "key_norm needs key_inv_rms");
+  const int es = elem_size(d->dtype);
+  const bool vec = (d->dim * es) % 16 == 0 && (d->row_stride * es) % 16 == 0 && aligned16(d->projected) &&
+                   aligned16(out);
+  KeySplitParams p;
+  Launch L;
+  fill_keyed_split(d, &p, &L, vec);
+  p.out = out;
+  p.key = key;
+  p.inv = key_inv_rms;
+  hipError_t err = launch_keyed_split_forward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "keyed split forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_keyed_split_backward(const attnres_keyed_split_desc* d, const void* grad_out,
+                                            const void* grad_key, const float* key_inv_rms, void* grad_projected,
+                                            void* stream) {
+  int rc = check_keyed_split(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!grad_projected) return fail(ATTNRES_EINVAL, "grad_projected is NULL");
+  if (d->key_norm && grad_key && (!key_inv_rms || !d->projected))
+    return fail(ATTNRES_EINVAL, "key_norm backward needs projected and key_inv_rms");
+  const int es = elem_size(d->dtype);
+  const bool vec = (d->dim * es) % 16 == 0 && (d->proj_cols * es) % 16 == 0 && aligned16(grad_projected) &&
+                   (!grad_out || aligned16(grad_out));
+  KeySplitParams p;
+  Launch L;
+  fill_keyed_split(d, &p, &L, vec);
+  p.gout = grad_out;
+  p.gkey = grad_key;
+  p.inv = const_cast<float*>(key_inv_rms);
+  p.gy = grad_projected;
+  hipError_t err = launch_keyed_split_backward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "keyed split backward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}

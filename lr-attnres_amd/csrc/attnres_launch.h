@@ -36,5 +36,9 @@ hipError_t launch_phase1_forward(int dtype, const Phase1Params& p, const Launch&
 hipError_t launch_phase1_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
+// key-producer epilogue: one wave per token, L.teams waves per workgroup,
+// L.vec = 16-byte vectors for the output columns
+hipError_t launch_keyed_split_forward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_keyed_split_backward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);
 
 }  // namespace attnres

@@ -120,4 +120,18 @@ struct Phase2Params {
   float scale, eps, bias, vscale;
 };
 
+// Key-producer epilogue: split of the fused [out | key | pad] projection.
+struct KeySplitParams {
+  const void* y;     // [n_tok, y_stride]: the projection (GEMM output)
+  void* out;         // forward: [n_tok, D]
+  void* key;         // forward: [n_tok, R]
+  float* inv;        // [n_tok, H]: 1/rms of each key head (key_norm)
+  const void* gout;  // backward: [n_tok, D] or null
+  const void* gkey;  // backward: [n_tok, R] or null
+  void* gy;          // backward: [n_tok, P]
+  int64_t n_tok, y_stride;
+  int32_t D, R, P, H, hd, key_norm;
+  float eps;
+};
+
 }  // namespace attnres

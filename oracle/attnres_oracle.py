@@ -38,6 +38,8 @@ lrid_attention_residual_read_ref          same + single-source identity
 attention_residual_average_read_ref       closed form (mean) and fp64
 gated_query_ref                           closed form (zero gate -> static)
 block_* helpers                           the reference tests' known answers
+lrid_fused_projection_split_ref           the reference model itself: whole-model
+                                          golden vectors (tests/golden/model_*)
 phase1_from_logits_ref / phase2_*_ref     phase1+phase2 == full read identity
                                           (tests/test_attnres_ops.py:582-610),
                                           golden fixtures with gradients,
@@ -373,6 +375,18 @@ def phase2_from_logit_ref(partial_value: Tensor, partial_logit: Tensor, interblo
     prob = torch.sigmoid(partial_logit.float() - interblock_lse.float()).to(partial_value.dtype)
     out = torch.addcmul(interblock_output, partial_value - interblock_output, prob.unsqueeze(-1))
     return norm(out) if normalize_output else out
+
+
+def lrid_fused_projection_split_ref(projected: Tensor, output_dim: int, rank: int, num_heads: int = 1,
+                                    key_norm: bool = True):
+    """Sublayer output and LR key of a fused projection, ``model.py:374-378``
+    with the per-head key norm ``_norm_lrid_key`` (``model.py:34-37``)."""
+    out = projected[..., :output_dim].contiguous()
+    key = projected[..., output_dim:output_dim + rank]
+    if key_norm:
+        shape = key.shape
+        key = norm(key.reshape(*shape[:-1], num_heads, shape[-1] // num_heads)).reshape(shape)
+    return out, key
 
 
 def softmax_weights_ref(values_or_keys, query: Tensor, num_heads: int, logit_scale: float, key_norm: bool,

@@ -38,6 +38,10 @@ class OracleOps:
                        scale_key, "lerp")
 
     @staticmethod
+    def lrid_fused_projection_split(projected, output_dim, rank, num_heads=1, key_norm=True):
+        return O.lrid_fused_projection_split_ref(projected, output_dim, rank, num_heads, key_norm)
+
+    @staticmethod
     def lrid_attention_residual_phase2(pv, pk, q, inter, lse, scale, key_norm, force_triton=False,
                                        normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False):
         return _phase2(pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias, partial_scale,

@@ -35,7 +35,8 @@ def test_library_exports_every_declared_symbol():
     assert names == sorted(["attnres_abi_version", "attnres_last_error", "attnres_read_backward",
                             "attnres_read_backward_workspace_size", "attnres_read_forward",
                             "attnres_phase1_forward", "attnres_phase1_backward", "attnres_phase2_forward",
-                            "attnres_phase2_backward", "attnres_phase2_backward_workspace_size"])
+                            "attnres_phase2_backward", "attnres_phase2_backward_workspace_size",
+                            "attnres_keyed_split_forward", "attnres_keyed_split_backward"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -46,18 +47,20 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 3
+    assert lib.attnres_abi_version() == 4
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()
     assert lib.attnres_phase1_forward(None, None, None, None, None, None) == -1
     assert lib.attnres_phase2_forward(None, None, None) == -1
     assert b"desc is NULL" in lib.attnres_last_error()
+    assert lib.attnres_keyed_split_forward(None, None, None, None, None) == -1
+    assert lib.attnres_keyed_split_backward(None, None, None, None, None, None) == -1
 
 
 STRUCTS = ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads"),
            (H.Phase1Desc, "attnres_phase1_desc"), (H.Phase2Desc, "attnres_phase2_desc"),
-           (H.Phase2Grads, "attnres_phase2_grads"))
+           (H.Phase2Grads, "attnres_phase2_grads"), (H.KeyedSplitDesc, "attnres_keyed_split_desc"))
 
 
 def _c_layout():
@@ -267,3 +270,47 @@ def test_phase_ops_fail_loudly_on_cpu_tensors():
         ops.attention_residual_phase1_from_logits(vs, torch.randn(2, 4, 1, 2))
     with pytest.raises(NotImplementedError):
         ops.attention_residual_phase1(vs, torch.randn(2, 8), True)
+
+
+def _ksdesc(**kw):
+    d = H.keyed_split_desc(torch.bfloat16, 16, 832, 832, 0x1000, 768, 64, 1, True)
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@needs_lib
+def test_keyed_split_host_validation_rejects_bad_descriptions_without_launching():
+    lib = H.load()
+    out, key = ctypes.c_void_p(0x6000), ctypes.c_void_p(0x7000)
+    inv = ctypes.cast(ctypes.c_void_p(0x8000), ctypes.POINTER(ctypes.c_float))
+    cases = [
+        (dict(rank=512, proj_cols=1280, row_stride=1280), -2, b"rank"),
+        (dict(heads=3), -1, b"heads"),
+        (dict(heads=0), -1, b"heads"),
+        (dict(heads=2, rank=96, proj_cols=864, row_stride=864), -2, b"head width"),
+        (dict(proj_cols=800), -1, b"proj_cols"),
+        (dict(row_stride=800), -1, b"row_stride"),
+        (dict(projected=None), -1, b"projected"),
+        (dict(dtype=7), -1, b"dtype"),
+    ]
+    for kw, code, msg in cases:
+        d = _ksdesc(**kw)
+        rc = lib.attnres_keyed_split_forward(ctypes.byref(d), out, key, inv, None)
+        assert rc == code, (kw, rc, lib.attnres_last_error())
+        assert msg in lib.attnres_last_error(), lib.attnres_last_error()
+    d = _ksdesc()
+    assert lib.attnres_keyed_split_forward(ctypes.byref(d), out, key, None, None) == -1
+    assert b"key_inv_rms" in lib.attnres_last_error()
+    assert lib.attnres_keyed_split_backward(ctypes.byref(d), None, key, None, None, None) == -1
+    assert b"grad_projected" in lib.attnres_last_error()
+    d = _ksdesc(n_tok=0)
+    assert lib.attnres_keyed_split_forward(ctypes.byref(d), None, None, None, None) == 0
+
+
+def test_keyed_split_fails_loudly_on_cpu_tensors():
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lrid_fused_projection_split(torch.randn(2, 3, 80), 64, 16)
+    with pytest.raises(RuntimeError, match="columns"):
+        ops.lrid_fused_projection_split(torch.randn(2, 3, 70), 64, 16)
+

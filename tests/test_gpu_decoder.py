@@ -76,6 +76,14 @@ class CheckingOps:
         self.calls.append(("phase1", len(values), logits.size(0)))
         return out, lse
 
+    def lrid_fused_projection_split(self, projected, output_dim, rank, num_heads=1, key_norm=True):
+        out, key = ops.lrid_fused_projection_split(projected, output_dim, rank, num_heads, key_norm)
+        e_out, e_key = O.lrid_fused_projection_split_ref(projected.cpu(), output_dim, rank, num_heads, key_norm)
+        assert torch.equal(out.cpu(), e_out)
+        assert_close(key, e_key, projected.dtype, "key")
+        self.calls.append(("split",))
+        return out, key
+
     def _phase2(self, fn, merge, pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias,
                 partial_scale, scale_key):
         out = fn(pv, pk, q, inter, lse, scale, key_norm, normalize_output=normalize_output, logit_bias=logit_bias,

@@ -74,6 +74,7 @@ def test_phase1_golden(name):
     (20, 3, 2048, torch.float32, False),
     (6, 2, 100, torch.float32, False),    # unaligned rows: scalar path
     (4, 8, 4096, torch.float32, False),
+    (4, 3, 1280, torch.bfloat16, True),   # 16-bit rows: five waves of 8-byte vectors
 ])
 def test_phase1_matches_oracle(dtype, S, Q, D, ldt, norm):
     g = gen(1000 + S * 31 + Q * 7 + D)
