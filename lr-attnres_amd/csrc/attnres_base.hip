@@ -27,7 +27,7 @@ __device__ __forceinline__ void store_prenorm(const ReadParams& p, int64_t tok, 
   typename DT::S* xp = (typename DT::S*)p.out_prenorm + tok * (int64_t)p.D;
 #pragma unroll
   for (int c = 0; c < CB; ++c)
-    if (cl.ok[c]) store_vec<DT, E>(xp + cl.eoff[c], acc[c]);
+    if (cl.ok[c]) store_vec<DT, E, true>(xp + cl.eoff[c], acc[c]);
 }
 
 // ============================================================== base forward
@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(1024) base_fwd_kernel(const ReadParams p) {
         const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
 #pragma unroll
         for (int c = 0; c < CB; ++c)
-          if (cl.ok[c]) load_raw<DT, E>(vp + cl.eoff[c], r[s][c]);
+          if (cl.ok[c]) load_raw<DT, E, true>(vp + cl.eoff[c], r[s][c]);
       }
     }
     // stage 1: sum of squares (key_norm) or the raw logit
@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(1024) base_fwd_kernel(const ReadParams p) {
     S* op = (S*)p.out + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], acc[c]);
+      if (cl.ok[c]) store_vec<DT, E, true>(op + cl.eoff[c], acc[c]);
   }
 }
 
@@ -199,7 +199,7 @@ __global__ void __launch_bounds__(MAXT) base_bwd_kernel(const ReadBwdParams bp) 
     const S* gp = (const S*)bp.gout + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-      if (cl.ok[c]) load_raw<DT, E>(gp + cl.eoff[c], gr[c]);
+      if (cl.ok[c]) load_raw<DT, E, true>(gp + cl.eoff[c], gr[c]);
       else
 #pragma unroll
         for (int i = 0; i < W; ++i) gr[c].w[i] = 0u;
@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(MAXT) base_bwd_kernel(const ReadBwdParams bp) 
         const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-          if (cl.ok[c]) load_raw<DT, E>(vp + cl.eoff[c], r[s][c]);
+          if (cl.ok[c]) load_raw<DT, E, true>(vp + cl.eoff[c], r[s][c]);
           else
 #pragma unroll
             for (int i = 0; i < W; ++i) r[s][c].w[i] = 0u;
@@ -322,7 +322,7 @@ __global__ void __launch_bounds__(MAXT) base_bwd_kernel(const ReadBwdParams bp) 
               const float dvk = p.key_norm ? DT::rnd(b[s] * (dkh - v[e] * b[s] * mr)) : dkh;
               dv[e] = DT::rnd(DT::rnd(ws * g[c][e]) + dvk);
             }
-            store_vec<DT, E>(dvp + cl.eoff[c], dv);
+            store_vec<DT, E, true>(dvp + cl.eoff[c], dv);
           }
         }
       }
@@ -447,7 +447,7 @@ __global__ void __launch_bounds__(1024) base_fwd_stream_kernel(const ReadParams 
     S* op = (S*)p.out + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], acc[c]);
+      if (cl.ok[c]) store_vec<DT, E, true>(op + cl.eoff[c], acc[c]);
     __syncthreads();
   }
 }
@@ -548,7 +548,7 @@ __global__ void __launch_bounds__(1024) base_bwd_stream_kernel(const ReadBwdPara
             const float dvk = p.key_norm ? DT::rnd(inv * (dkh - v[c][e] * inv * mr)) : dkh;
             dv[e] = DT::rnd(DT::rnd(ws * g[c][e]) + dvk);
           }
-          store_vec<DT, E>(dvp + cl.eoff[c], dv);
+          store_vec<DT, E, true>(dvp + cl.eoff[c], dv);
         }
       }
     }
@@ -589,7 +589,7 @@ __global__ void __launch_bounds__(1024) avg_fwd_kernel(const ReadParams p) {
       for (int c = 0; c < CB; ++c) {
         if (cl.ok[c]) {
           float v[E];
-          load_vec<DT, E>(vp + cl.eoff[c], v);
+          load_vec<DT, E, true>(vp + cl.eoff[c], v);
 #pragma unroll
           for (int e = 0; e < E; ++e) acc[c][e] += v[e];
         }
@@ -607,7 +607,7 @@ __global__ void __launch_bounds__(1024) avg_fwd_kernel(const ReadParams p) {
     S* op = (S*)p.out + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], acc[c]);
+      if (cl.ok[c]) store_vec<DT, E, true>(op + cl.eoff[c], acc[c]);
   }
 }
 
@@ -626,7 +626,7 @@ __global__ void __launch_bounds__(1024) avg_bwd_kernel(const ReadBwdParams bp) {
     const S* gp = (const S*)bp.gout + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-      if (cl.ok[c]) load_vec<DT, E>(gp + cl.eoff[c], g[c]);
+      if (cl.ok[c]) load_vec<DT, E, true>(gp + cl.eoff[c], g[c]);
       else
 #pragma unroll
         for (int e = 0; e < E; ++e) g[c][e] = 0.f;
@@ -642,7 +642,7 @@ __global__ void __launch_bounds__(1024) avg_bwd_kernel(const ReadBwdParams bp) {
       S* dvp = (S*)bp.dval[s] + tok * (int64_t)D;
 #pragma unroll
       for (int c = 0; c < CB; ++c)
-        if (cl.ok[c]) store_vec<DT, E>(dvp + cl.eoff[c], g[c]);
+        if (cl.ok[c]) store_vec<DT, E, true>(dvp + cl.eoff[c], g[c]);
     }
   }
 }

@@ -81,19 +81,36 @@ struct Raw {  // raw bits of one vector, kept packed in VGPRs until used
   uint32_t w[Vec<DT, E>::kWords];
 };
 
-template <class DT, int E>
+// Streaming accesses.  Rows that a kernel touches exactly once (source values,
+// upstream gradients, outputs and value gradients: hundreds of MB per launch,
+// far beyond L2 and the MALL) go through the non-temporal cache policy
+// (NT = true): they then neither displace lines other waves still use nor sit
+// dirty in the caches until a later kernel's traffic forces their write-back.
+// Small rows that are re-read (keys, queries, tables) keep the default policy.
+template <class T, bool NT>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <class T, bool NT>
+__device__ __forceinline__ void st(T* p, T v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+template <class DT, int E, bool NT = false>
 __device__ __forceinline__ void load_raw(const typename DT::S* __restrict__ p, Raw<DT, E>& r) {
   constexpr int B = Vec<DT, E>::kBytes;
   if constexpr (B == 16) {
-    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    u32x4 v = ld<u32x4, NT>(reinterpret_cast<const u32x4*>(p));
     r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
   } else if constexpr (B == 8) {
-    u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    u32x2 v = ld<u32x2, NT>(reinterpret_cast<const u32x2*>(p));
     r.w[0] = v.x; r.w[1] = v.y;
   } else if constexpr (B == 4) {
-    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+    r.w[0] = ld<uint32_t, NT>(reinterpret_cast<const uint32_t*>(p));
   } else {
-    r.w[0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(p));
+    r.w[0] = (uint32_t)ld<uint16_t, NT>(reinterpret_cast<const uint16_t*>(p));
   }
 }
 
@@ -119,58 +136,38 @@ __device__ __forceinline__ void unpack(const Raw<DT, E>& r, float (&o)[E]) {
   }
 }
 
-template <class DT, int E>
+template <class DT, int E, bool NT = false>
 __device__ __forceinline__ void load_vec(const typename DT::S* __restrict__ p, float (&o)[E]) {
   Raw<DT, E> r;
-  load_raw<DT, E>(p, r);
+  load_raw<DT, E, NT>(p, r);
   unpack<DT, E>(r, o);
 }
 
 // store E fp32 values (already rounded where the caller wants) as DT
-template <class DT, int E>
+template <class DT, int E, bool NT = false>
 __device__ __forceinline__ void store_vec(typename DT::S* __restrict__ p, const float (&x)[E]) {
   if constexpr (sizeof(typename DT::S) == 4) {
     if constexpr (E == 4) {
       u32x4 v = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
-      *reinterpret_cast<u32x4*>(p) = v;
+      st<u32x4, NT>(reinterpret_cast<u32x4*>(p), v);
     } else if constexpr (E == 2) {
       u32x2 v = {__float_as_uint(x[0]), __float_as_uint(x[1])};
-      *reinterpret_cast<u32x2*>(p) = v;
+      st<u32x2, NT>(reinterpret_cast<u32x2*>(p), v);
     } else {
 #pragma unroll
-      for (int i = 0; i < E; ++i) p[i] = x[i];
+      for (int i = 0; i < E; ++i) st<float, NT>(p + i, x[i]);
     }
   } else {
+    auto pack2 = [](float lo, float hi) -> uint32_t {
+      if constexpr (DT::kCode == 1) return pack_bf16x2(lo, hi);
+      else return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+    };
     if constexpr (E == 8) {
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t lo, hi;
-        if constexpr (DT::kCode == 1) {
-          w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-        } else {
-          lo = f32_to_f16_bits(x[2 * i]);
-          hi = f32_to_f16_bits(x[2 * i + 1]);
-          w[i] = lo | (hi << 16);
-        }
-      }
-      u32x4 v = {w[0], w[1], w[2], w[3]};
-      *reinterpret_cast<u32x4*>(p) = v;
+      u32x4 v = {pack2(x[0], x[1]), pack2(x[2], x[3]), pack2(x[4], x[5]), pack2(x[6], x[7])};
+      st<u32x4, NT>(reinterpret_cast<u32x4*>(p), v);
     } else if constexpr (E == 4) {
-      uint32_t w[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        uint32_t lo, hi;
-        if constexpr (DT::kCode == 1) {
-          w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-        } else {
-          lo = f32_to_f16_bits(x[2 * i]);
-          hi = f32_to_f16_bits(x[2 * i + 1]);
-          w[i] = lo | (hi << 16);
-        }
-      }
-      u32x2 v = {w[0], w[1]};
-      *reinterpret_cast<u32x2*>(p) = v;
+      u32x2 v = {pack2(x[0], x[1]), pack2(x[2], x[3])};
+      st<u32x2, NT>(reinterpret_cast<u32x2*>(p), v);
     } else {
 #pragma unroll
       for (int i = 0; i < E; ++i) DT::store1(p + i, x[i]);

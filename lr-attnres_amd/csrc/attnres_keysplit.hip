@@ -60,10 +60,10 @@ __global__ void __launch_bounds__(256) keyed_split_fwd_kernel(const KeySplitPara
     S* orow = (S*)p.out + tok * (int64_t)p.D;
     for (int v = lane; v < nv; v += kWave) {
       Raw<DT, E> t;
-      load_raw<DT, E>(yr + v * E, t);
+      load_raw<DT, E, true>(yr + v * E, t);
       float f[E];
       unpack<DT, E>(t, f);
-      store_vec<DT, E>(orow + v * E, f);
+      store_vec<DT, E, true>(orow + v * E, f);
     }
     S* krow = (S*)p.key + tok * (int64_t)p.R;
     if (p.key_norm) {
@@ -104,13 +104,13 @@ __global__ void __launch_bounds__(256) keyed_split_bwd_kernel(const KeySplitPara
       float f[E];
       if (gor) {
         Raw<DT, E> t;
-        load_raw<DT, E>(gor + v * E, t);
+        load_raw<DT, E, true>(gor + v * E, t);
         unpack<DT, E>(t, f);
       } else {
 #pragma unroll
         for (int e = 0; e < E; ++e) f[e] = 0.f;
       }
-      store_vec<DT, E>(gyr + v * E, f);
+      store_vec<DT, E, true>(gyr + v * E, f);
     }
     // key columns
     float g[kKsJ];

@@ -169,7 +169,7 @@ __global__ void __launch_bounds__(1024) lr_fwd_kernel(const ReadParams p) {
           const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
 #pragma unroll
           for (int c = 0; c < CB; ++c)
-            if (ok[c]) load_raw<DT, E>(vp + eoff[c], r[i][c]);
+            if (ok[c]) load_raw<DT, E, true>(vp + eoff[c], r[i][c]);
         }
       }
 #pragma unroll
@@ -203,7 +203,7 @@ __global__ void __launch_bounds__(1024) lr_fwd_kernel(const ReadParams p) {
         S* xp = (S*)p.out_prenorm + tok * (int64_t)p.D;
 #pragma unroll
         for (int c = 0; c < CB; ++c)
-          if (ok[c]) store_vec<DT, E>(xp + eoff[c], acc[c]);
+          if (ok[c]) store_vec<DT, E, true>(xp + eoff[c], acc[c]);
       }
       ss = wave_sum(ss);
       if (wpt > 1) {
@@ -222,7 +222,7 @@ __global__ void __launch_bounds__(1024) lr_fwd_kernel(const ReadParams p) {
     S* op = (S*)p.out + tok * (int64_t)p.D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (ok[c]) store_vec<DT, E>(op + eoff[c], acc[c]);
+      if (ok[c]) store_vec<DT, E, true>(op + eoff[c], acc[c]);
     __syncthreads();
   }
 }
@@ -302,7 +302,7 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
     const S* gp = (const S*)bp.gout + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-      if (ok[c]) load_vec<DT, E>(gp + eoff[c], g[c]);
+      if (ok[c]) load_vec<DT, E, true>(gp + eoff[c], g[c]);
       else
 #pragma unroll
         for (int e = 0; e < E; ++e) g[c][e] = 0.f;
@@ -314,7 +314,7 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
       float dot = 0.f;
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
-        if (ok[c]) load_vec<DT, E>(xp + eoff[c], x[c]);
+        if (ok[c]) load_vec<DT, E, true>(xp + eoff[c], x[c]);
         else
 #pragma unroll
           for (int e = 0; e < E; ++e) x[c][e] = 0.f;
@@ -347,7 +347,7 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
           const S* vp = (const S*)p.val[s] + tok * (int64_t)p.vstride[s];
 #pragma unroll
           for (int c = 0; c < CB; ++c)
-            if (ok[c]) load_raw<DT, E>(vp + eoff[c], r[i][c]);
+            if (ok[c]) load_raw<DT, E, true>(vp + eoff[c], r[i][c]);
         }
       }
 #pragma unroll
@@ -367,7 +367,7 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
                 part += g[c][e] * v[e];
                 dv[e] = DT::rnd(w * g[c][e]);
               }
-              store_vec<DT, E>(dvp + eoff[c], dv);
+              store_vec<DT, E, true>(dvp + eoff[c], dv);
             }
             part = group_sum(part, gl);
             const int col = wave + c * wpt;

@@ -254,7 +254,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     for (int s = 0; s < NB; ++s) {
       const S* vp = global_ptr<const S>(uniform_u64(base[s]));
 #pragma unroll
-      for (int c = 0; c < CB; ++c) load_raw<DT, E>(vp + eoff[c], vr[s][c]);
+      for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + eoff[c], vr[s][c]);
     }
   };
 
@@ -336,7 +336,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
         S* xp = global_ptr<S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
         for (int c = 0; c < CB; ++c)
-          if (ok[c]) store_vec<DT, E>(xp + eoff[c], acc[c]);
+          if (ok[c]) store_vec<DT, E, true>(xp + eoff[c], acc[c]);
       }
       const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + p.eps);
 #pragma unroll
@@ -348,7 +348,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     S* op = global_ptr<S>((uint64_t)p.out) + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (ok[c]) store_vec<DT, E>(op + eoff[c], acc[c]);
+      if (ok[c]) store_vec<DT, E, true>(op + eoff[c], acc[c]);
     if (has_pair && p.weights) p.weights[(tok * H + ph) * N + ps] = pw;
   }
 }
@@ -456,12 +456,12 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     Raw<DT, E> gr[CB];
     const S* gp = global_ptr<const S>((uint64_t)bp.gout) + tok * (int64_t)D;
 #pragma unroll
-    for (int c = 0; c < CB; ++c) load_raw<DT, E>(gp + eoff[c], gr[c]);
+    for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gp + eoff[c], gr[c]);
     Raw<DT, E> xr[CB];
     if (p.norm_out) {
       const S* xp = global_ptr<const S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
-      for (int c = 0; c < CB; ++c) load_raw<DT, E>(xp + eoff[c], xr[c]);
+      for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(xp + eoff[c], xr[c]);
     }
     Raw<DT, E> vr[NB][CB];
     {
@@ -472,7 +472,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
       for (int s = 0; s < NB; ++s) {
         const S* vp = global_ptr<const S>(uniform_u64(base[s]));
 #pragma unroll
-        for (int c = 0; c < CB; ++c) load_raw<DT, E>(vp + eoff[c], vr[s][c]);
+        for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + eoff[c], vr[s][c]);
       }
     }
     float g[CB][E];
@@ -623,7 +623,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
             float dv[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) dv[e] = DT::rnd(w * g[c][e]);
-            store_vec<DT, E>(dvp + eoff[c], dv);
+            store_vec<DT, E, true>(dvp + eoff[c], dv);
           }
         }
       }

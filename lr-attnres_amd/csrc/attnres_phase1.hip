@@ -59,7 +59,7 @@ __device__ __forceinline__ void phase1_load_rows(const Phase1Params& p, int64_t 
       const S* vp = (const S*)p.val[s0 + j] + tok * (int64_t)p.vstride[s0 + j];
 #pragma unroll
       for (int c = 0; c < CB; ++c)
-        if (cl.ok[c]) load_raw<DT, E>(vp + cl.eoff[c], r[j][c]);
+        if (cl.ok[c]) load_raw<DT, E, true>(vp + cl.eoff[c], r[j][c]);
     }
   }
 }
@@ -136,7 +136,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
             S* xp = (S*)p.out_prenorm + ((int64_t)(q0 + qq) * p.n_tok + tok) * D;
 #pragma unroll
             for (int c = 0; c < CB; ++c)
-              if (cl.ok[c]) store_vec<DT, E>(xp + cl.eoff[c], acc[qq][c]);
+              if (cl.ok[c]) store_vec<DT, E, true>(xp + cl.eoff[c], acc[qq][c]);
           }
         }
         block_allreduce<kP1QC>(ss, nq, s_red, lane, wave, wpt);
@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
           S* op = (S*)p.out + ((int64_t)(q0 + qq) * p.n_tok + tok) * D;
 #pragma unroll
           for (int c = 0; c < CB; ++c)
-            if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], acc[qq][c]);
+            if (cl.ok[c]) store_vec<DT, E, true>(op + cl.eoff[c], acc[qq][c]);
         }
       }
     }
@@ -193,7 +193,7 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
         const S* gp = (const S*)p.gout + ((int64_t)q * p.n_tok + tok) * D;
 #pragma unroll
         for (int c = 0; c < CB; ++c)
-          if (cl.ok[c]) load_raw<DT, E>(gp + cl.eoff[c], gr[q][c]);
+          if (cl.ok[c]) load_raw<DT, E, true>(gp + cl.eoff[c], gr[q][c]);
       }
     }
     if (wave == 0) phase1_softmax(p, tok, lane, w, false);
@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
 #pragma unroll
           for (int c = 0; c < CB; ++c) {
             if (cl.ok[c]) {
-              load_raw<DT, E>(xp + cl.eoff[c], xr[q][c]);
+              load_raw<DT, E, true>(xp + cl.eoff[c], xr[q][c]);
               float g[E], x[E];
               unpack<DT, E>(gr[q][c], g);
               unpack<DT, E>(xr[q][c], x);
@@ -332,7 +332,7 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
         if (cl.ok[c]) {
 #pragma unroll
           for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e]);
-          store_vec<DT, E>(dp + cl.eoff[c], acc[c]);
+          store_vec<DT, E, true>(dp + cl.eoff[c], acc[c]);
         }
       }
     }

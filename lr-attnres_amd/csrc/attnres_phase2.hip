@@ -64,9 +64,9 @@ __device__ __forceinline__ void p2_load(const Phase2Params& p, int64_t tok, cons
 #pragma unroll
   for (int c = 0; c < CB; ++c) {
     if (cl.ok[c]) {
-      load_raw<DT, E>(pvp + cl.eoff[c], r.pv[c]);
-      load_raw<DT, E>(itp + cl.eoff[c], r.it[c]);
-      if (with_grad) load_raw<DT, E>(gp + cl.eoff[c], r.g[c]);
+      load_raw<DT, E, true>(pvp + cl.eoff[c], r.pv[c]);
+      load_raw<DT, E, true>(itp + cl.eoff[c], r.it[c]);
+      if (with_grad) load_raw<DT, E, true>(gp + cl.eoff[c], r.g[c]);
     }
   }
   if (LR) {
@@ -216,7 +216,7 @@ __global__ void __launch_bounds__(512) phase2_fwd_kernel(const Phase2Params p) {
     S* op = (S*)p.out + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], o[c]);
+      if (cl.ok[c]) store_vec<DT, E, true>(op + cl.eoff[c], o[c]);
   }
 }
 
@@ -391,8 +391,8 @@ __global__ void __launch_bounds__(512) phase2_bwd_kernel(const Phase2Params p) {
         dp[e] = DT::rnd(g * vs);
       }
       if (cl.ok[c]) {
-        store_vec<DT, E>(dpvp + cl.eoff[c], dp);
-        store_vec<DT, E>(dip + cl.eoff[c], dint[c]);
+        store_vec<DT, E, true>(dpvp + cl.eoff[c], dp);
+        store_vec<DT, E, true>(dip + cl.eoff[c], dint[c]);
       }
     }
   }
@@ -471,8 +471,8 @@ __device__ __forceinline__ void p2w_token(const Phase2Params& p, int64_t tok, co
 #pragma unroll
   for (int c = 0; c < CB; ++c)
     if (cl.ok[c]) {
-      load_raw<DT, E>(pvp + cl.eoff[c], st.pv[c]);
-      load_raw<DT, E>(itp + cl.eoff[c], itr[c]);
+      load_raw<DT, E, true>(pvp + cl.eoff[c], st.pv[c]);
+      load_raw<DT, E, true>(itp + cl.eoff[c], itr[c]);
     }
   if (LR) {
     const S* kp = (const S*)p.pk + tok * p.pk_stride;
@@ -606,7 +606,7 @@ __global__ void __launch_bounds__(256) phase2_wave_fwd_kernel(const Phase2Params
     S* op = (S*)p.out + tok * (int64_t)p.D;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
-      if (cl.ok[c]) store_vec<DT, E>(op + cl.eoff[c], o[c]);
+      if (cl.ok[c]) store_vec<DT, E, true>(op + cl.eoff[c], o[c]);
   }
 }
 
@@ -676,9 +676,9 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
         if (cl.ok[c]) {
-          load_raw<DT, E>(gp + cl.eoff[c], gr[c]);
-          load_raw<DT, E>(pvp + cl.eoff[c], pvr[c]);
-          load_raw<DT, E>(itp + cl.eoff[c], itr[c]);
+          load_raw<DT, E, true>(gp + cl.eoff[c], gr[c]);
+          load_raw<DT, E, true>(pvp + cl.eoff[c], pvr[c]);
+          load_raw<DT, E, true>(itp + cl.eoff[c], itr[c]);
         } else {
 #pragma unroll
           for (int i = 0; i < Vec<DT, E>::kWords; ++i) gr[c].w[i] = pvr[c].w[i] = itr[c].w[i] = 0u;
@@ -822,7 +822,7 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
         }
         dpr[c] += DT::rnd(g[e] * diff);
       }
-      if (cl.ok[c]) store_vec<DT, E>(dip + cl.eoff[c], dint);
+      if (cl.ok[c]) store_vec<DT, E, true>(dip + cl.eoff[c], dint);
       if (direct) {
         float pr[E], dp[E];
         unpack<DT, E>(pvr[c], pr);
@@ -831,7 +831,7 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
           if (want_sv && cl.ok[c]) acc_sv += DT::rnd(dpm[e] * pr[e]);
           dp[e] = DT::rnd(dpm[e] * vs);
         }
-        if (cl.ok[c]) store_vec<DT, E>(dpvp + cl.eoff[c], dp);
+        if (cl.ok[c]) store_vec<DT, E, true>(dpvp + cl.eoff[c], dp);
       } else {
         pack_raw<DT, E>(dpm, gr[c]);
       }
@@ -919,7 +919,7 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
           if (want_sv && cl.ok[c]) acc_sv += DT::rnd(g * pr[e]);
           dp[e] = DT::rnd(g * vs);
         }
-        if (cl.ok[c]) store_vec<DT, E>(dpvp + cl.eoff[c], dp);
+        if (cl.ok[c]) store_vec<DT, E, true>(dpvp + cl.eoff[c], dp);
       }
     }
   }
