@@ -309,13 +309,26 @@ def forward(desc: Desc, device, dtype, need_weights: bool, normalize_output: boo
     return out, w, inv, pre
 
 
+def _row_blocks(count: int, n_tok: int, width: int, device, dtype, batched: bool):
+    """``count`` dense [n_tok, width] gradient buffers: separate allocations, or
+    (``batched``) views of one allocation."""
+    if not batched:
+        return [torch.empty((n_tok, width), device=device, dtype=dtype) for _ in range(count)]
+    return list(torch.empty((count, n_tok, width), device=device, dtype=dtype).unbind(0))
+
+
 def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, want_dquery: bool,
-             want_dgate: bool, want_dbias: bool, query_shape, gate_shape, lr: bool, has_query_dyn: bool):
-    """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias)."""
+             want_dgate: bool, want_dbias: bool, query_shape, gate_shape, lr: bool, has_query_dyn: bool,
+             batched: bool = False):
+    """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias).
+
+    With ``batched`` the per-source gradients are views of one allocation per
+    kind (fewer allocator calls); otherwise each is its own tensor (the
+    library op's outputs may not alias one another)."""
     lib = load()
     n = desc.n_src
-    dvals = [torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype) for _ in range(n)]
-    dkeys = [torch.empty((desc.n_tok, desc.R), device=device, dtype=dtype) for _ in range(n)] if lr else []
+    dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, batched)
+    dkeys = _row_blocks(n, desc.n_tok, desc.R, device, dtype, batched) if lr else []
     dq = torch.empty(query_shape, device=device, dtype=dtype) if want_dquery else None
     dqd = torch.empty((desc.n_tok, desc.R), device=device, dtype=dtype) if has_query_dyn else None
     dg = torch.empty(gate_shape, device=device, dtype=dtype) if want_dgate else None
@@ -393,11 +406,12 @@ def phase1_forward(desc: Phase1, device, dtype, for_backward: bool):
     return out, lse, pre, inv
 
 
-def phase1_backward(desc: Phase1, device, dtype, logits_dtype, grad_out, grad_lse, prenorm, inv_rms):
+def phase1_backward(desc: Phase1, device, dtype, logits_dtype, grad_out, grad_lse, prenorm, inv_rms,
+                    batched: bool = False):
     """Returns (dvalues list of [n_tok, D], dlogits [Q, S, n_tok])."""
     lib = load()
     n = desc.n_src
-    dvals = [torch.empty((desc.n_tok, desc.D), device=device, dtype=dtype) for _ in range(n)]
+    dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, batched)
     dlog = torch.empty((desc.n_q, n, desc.n_tok), device=device, dtype=logits_dtype)
     dv_arr = (c_void_p * n)(*[t.data_ptr() for t in dvals])
     keep = prenorm is not None and prenorm.numel() > 0

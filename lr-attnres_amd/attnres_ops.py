@@ -21,7 +21,9 @@ deterministically.
 
 from __future__ import annotations
 
+import contextlib
 import math
+from collections import OrderedDict
 from typing import Optional, Sequence
 
 import torch
@@ -57,6 +59,29 @@ def is_fused_attnres_available() -> bool:
 
 # ---------------------------------------------------------------- argument handling
 
+# Logit biases given as host numbers (python floats or lists) become small
+# device tensors.  They are cached by value, so repeated calls (every step of a
+# training loop) neither copy host data to the device again nor launch kernels
+# to build them, and a call inside HIP-graph capture (after an eager warm-up
+# call with the same numbers) records no host-to-device copy.  The cached
+# tensors are never written.
+_HOST_BIAS_CACHE: "OrderedDict[tuple, Tensor]" = OrderedDict()
+_HOST_BIAS_CACHE_SIZE = 256
+
+
+def _host_bias(key, device, make) -> Tensor:
+    k = (str(device), key)
+    t = _HOST_BIAS_CACHE.get(k)
+    if t is None:
+        t = make().to(device=device, dtype=torch.float32).contiguous()
+        _HOST_BIAS_CACHE[k] = t
+        if len(_HOST_BIAS_CACHE) > _HOST_BIAS_CACHE_SIZE:
+            _HOST_BIAS_CACHE.popitem(last=False)
+    else:
+        _HOST_BIAS_CACHE.move_to_end(k)
+    return t
+
+
 def _source_logit_bias(source_counts, source_logit_biases, n_sources: int, device) -> Optional[Tensor]:
     """fp32 [N] logit bias with the reference's rules and errors (attnres_ops.py:65-105)."""
     if source_counts is not None and source_logit_biases is not None:
@@ -66,25 +91,31 @@ def _source_logit_bias(source_counts, source_logit_biases, n_sources: int, devic
             return None
         if isinstance(source_counts, Tensor):
             counts = source_counts.reshape(-1).to(device=device, dtype=torch.float32)
-        elif isinstance(source_counts, (int, float)):
-            counts = torch.full((n_sources,), float(source_counts), device=device, dtype=torch.float32)
+            if counts.numel() != n_sources:
+                raise RuntimeError("source_counts length must match the number of sources")
+            return counts.log()
+        if isinstance(source_counts, (int, float)):
+            vals = (float(source_counts),) * n_sources  # (the reference checks only list entries)
         else:
             if len(source_counts) != n_sources:
                 raise RuntimeError("source_counts length must match the number of sources")
-            vals = [float(c) for c in source_counts]
+            vals = tuple(float(c) for c in source_counts)
             if any(c <= 0.0 for c in vals):
                 raise RuntimeError("source_counts must be positive")
-            counts = torch.tensor(vals, device=device, dtype=torch.float32)
-        if counts.numel() != n_sources:
-            raise RuntimeError("source_counts length must match the number of sources")
-        return counts.log()
+        # log on the device, as the reference computes it
+        return _host_bias(("log_counts", vals), device,
+                          lambda: torch.tensor(vals, dtype=torch.float32).to(device).log())
     if isinstance(source_logit_biases, Tensor):
         biases = source_logit_biases.reshape(-1).to(device=device, dtype=torch.float32)
     elif isinstance(source_logit_biases, (int, float)):
-        biases = torch.full((n_sources,), float(source_logit_biases), device=device, dtype=torch.float32)
+        vals = (float(source_logit_biases),) * n_sources
+        biases = _host_bias(("bias", vals), device, lambda: torch.tensor(vals, dtype=torch.float32))
     else:
         if len(source_logit_biases) != n_sources:
             raise RuntimeError("source_logit_biases length must match the number of sources")
+        if not any(isinstance(b, Tensor) for b in source_logit_biases):
+            vals = tuple(float(b) for b in source_logit_biases)
+            return _host_bias(("bias", vals), device, lambda: torch.tensor(vals, dtype=torch.float32))
         items = [b.to(device=device, dtype=torch.float32).reshape(()) if isinstance(b, Tensor)
                  else torch.tensor(float(b), device=device, dtype=torch.float32) for b in source_logit_biases]
         biases = torch.stack(items)
@@ -243,13 +274,95 @@ def _read_backward(ctx, grad_out, grad_w, grad_inv, grad_pre):
 _read_op.register_autograd(_read_backward, setup_context=_read_setup_context)
 
 
+# ---------------------------------------------------------------- eager autograd path
+#
+# Eager calls (no torch.compile tracing) go through torch.autograd.Function
+# classes instead of the torch.library ops above: the same C ABI calls on the
+# same kernels, without the custom-op layer's per-call cost (schema defaults,
+# pytree flattening of the source lists, a second op for the backward).  The
+# forward's C descriptor is reused by the backward, and the per-source
+# gradients are views of one allocation.  While torch.compile traces, the
+# library ops are used, so the compiled graph holds attnres_hip:: ops with
+# their fake implementations.
+
+def _compiling() -> bool:
+    return torch.compiler.is_compiling()
+
+
+def _device_ctx(dev):
+    """Device guard, skipped when ``dev`` is already the current device."""
+    return contextlib.nullcontext() if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+
+
+def _unflatten_opt(has, tensors):
+    """Optional tensors back from a flat tuple: ``has`` marks which are present."""
+    it = iter(tensors)
+    return [next(it) if h else None for h in has]
+
+
+class _ReadFn(torch.autograd.Function):
+    """Eager autograd of the read: inputs are (meta, *values, *keys, *optional)."""
+
+    @staticmethod
+    def forward(ctx, meta, *flat):
+        n_v, n_k, has, heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token, save = meta
+        values = flat[:n_v]
+        keys = flat[n_v:n_v + n_k]
+        query, query_dyn, gate, bias = _unflatten_opt(has, flat[n_v + n_k:])
+        v0 = values[0]
+        B, T, D = v0.shape
+        desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
+                         mode, gate_act, gate_per_token)
+        with _device_ctx(v0.device):
+            out, w, inv, pre = _hip.forward(desc, v0.device, v0.dtype, save and mode == _hip.MODE_SOFTMAX,
+                                            normalize_output, save)
+        if save:
+            ctx.desc = desc
+            ctx.meta = meta
+            ctx.shape = (B, T, D)
+            ctx.save_for_backward(*flat, pre, w, inv)
+        return out.view(B, T, D)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out):
+        n_v, n_k, has, heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token, _ = ctx.meta
+        saved = ctx.saved_tensors  # (checks that no input was modified in place)
+        query, query_dyn, gate, bias = _unflatten_opt(has, saved[n_v + n_k:-3])
+        pre, w, inv = saved[-3:]
+        B, T, D = ctx.shape
+        dev = saved[0].device
+        want = ctx.needs_input_grad
+        with _device_ctx(dev):
+            dvals, dkeys, dq, dqd, dg, db = _hip.backward(
+                ctx.desc, dev, saved[0].dtype, grad_out.contiguous(), pre, inv, w,
+                want_dquery=query is not None and mode == _hip.MODE_SOFTMAX,
+                want_dgate=gate is not None, want_dbias=bias is not None,
+                query_shape=tuple(query.shape) if query is not None else (0,),
+                gate_shape=tuple(gate.shape) if gate is not None else (0,), lr=n_k > 0,
+                has_query_dyn=query_dyn is not None, batched=True)
+        grads = [None]
+        grads += [t.view(B, T, D) for t in dvals]
+        grads += [t.view(B, T, ctx.desc.R) for t in dkeys]
+        for present, g in zip(has, (dq, dqd.view(query_dyn.shape) if dqd is not None else None, dg, db)):
+            if present:
+                grads.append(g)
+        # inputs that do not need a gradient get None (the kernels write all of them in one pass)
+        return tuple(g if (g is None or want[i]) else None for i, g in enumerate(grads))
+
+
 def _run(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode,
          gate_act=_hip.GATE_NONE, gate_per_token=False):
-    save = torch.is_grad_enabled() and any(
-        t is not None and t.requires_grad for t in [*values, *keys, query, query_dyn, gate, bias])
-    out, _, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, int(heads), float(logit_scale), bool(key_norm),
-                         bool(normalize_output), int(mode), int(gate_act), bool(gate_per_token), bool(save))
-    return out
+    opt = (query, query_dyn, gate, bias)
+    save = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (*values, *keys, *opt))
+    if _compiling():
+        out, _, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, int(heads), float(logit_scale),
+                                bool(key_norm), bool(normalize_output), int(mode), int(gate_act),
+                                bool(gate_per_token), bool(save))
+        return out
+    meta = (len(values), len(keys), tuple(t is not None for t in opt), int(heads), float(logit_scale),
+            bool(key_norm), bool(normalize_output), int(mode), int(gate_act), bool(gate_per_token), bool(save))
+    return _ReadFn.apply(meta, *values, *keys, *[t for t in opt if t is not None])
 
 
 # ---------------------------------------------------------------- public API: base read
@@ -479,6 +592,40 @@ def _phase1_backward(ctx, grad_out, grad_lse, grad_pre, grad_inv):
 _phase1_op.register_autograd(_phase1_backward, setup_context=_phase1_setup_context)
 
 
+class _Phase1Fn(torch.autograd.Function):
+    """Eager autograd of phase 1: inputs (meta, logits [Q,S,n], *value rows)."""
+
+    @staticmethod
+    def forward(ctx, meta, logits, *values):
+        normalize_output, save = meta
+        ctx.set_materialize_grads(False)
+        v0 = values[0]
+        desc = _hip.Phase1(values, logits, normalize_output)
+        with _device_ctx(v0.device):
+            out, lse, pre, inv = _hip.phase1_forward(desc, v0.device, v0.dtype, save)
+        if save:
+            ctx.desc = desc
+            ctx.save_for_backward(logits, *values, pre, inv)
+        return out, lse
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out, grad_lse):
+        saved = ctx.saved_tensors
+        logits, values, (pre, inv) = saved[0], saved[1:-2], saved[-2:]
+        v0 = values[0]
+        if grad_out is None and grad_lse is None:
+            return (None, None, *([None] * len(values)))
+        if grad_out is None:
+            grad_out = v0.new_zeros((logits.size(0), v0.size(0), v0.size(1)))
+        grad_lse = grad_lse.float().contiguous() if grad_lse is not None else None
+        with _device_ctx(v0.device):
+            dvals, dlog = _hip.phase1_backward(ctx.desc, v0.device, v0.dtype, logits.dtype, grad_out.contiguous(),
+                                               grad_lse, pre, inv, batched=True)
+        want = ctx.needs_input_grad
+        return (None, dlog if want[1] else None, *[d if want[2 + i] else None for i, d in enumerate(dvals)])
+
+
 def attention_residual_phase1_from_logits(values, logits: Tensor, force_triton: bool = False,
                                           normalize_output: bool = False):
     """Cached-logit read of completed sources for Q read sites (reference: attnres_ops.py:3910-3961).
@@ -507,7 +654,10 @@ def attention_residual_phase1_from_logits(values, logits: Tensor, force_triton: 
     rows = [_rows2d(t) for t in srcs]
     lg = logits.contiguous().view(Q, S, B * T)
     save = torch.is_grad_enabled() and (logits.requires_grad or any(t.requires_grad for t in srcs))
-    out, lse, _, _ = _phase1_op(rows, lg, bool(normalize_output), bool(save))
+    if _compiling():
+        out, lse, _, _ = _phase1_op(rows, lg, bool(normalize_output), bool(save))
+    else:
+        out, lse = _Phase1Fn.apply((bool(normalize_output), bool(save)), lg, *rows)
     return out.view(Q, B, T, D), lse.view(Q, B, T)
 
 
@@ -605,6 +755,60 @@ def _phase2_backward(ctx, grad_out):
 _phase2_op.register_autograd(_phase2_backward, setup_context=_phase2_setup_context)
 
 
+class _Phase2Fn(torch.autograd.Function):
+    """Eager autograd of the phase-2 merge: inputs (meta, partial rows, inter rows, lse, *optional)."""
+
+    @staticmethod
+    def forward(ctx, meta, partial_value, inter, lse, *opt_flat):
+        has, merge, key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key = meta
+        partial_key, query, partial_logit, bias_t, scale_t = _unflatten_opt(has, opt_flat)
+        desc = _hip.Phase2(partial_value, partial_key, query, partial_logit, inter, lse, merge, key_norm,
+                           normalize_output, logit_scale, bias_value, bias_t, scale_value, scale_t, scale_key)
+        dev = partial_value.device
+        with _device_ctx(dev):
+            out = _hip.phase2_forward(desc, dev, partial_value.dtype)
+        ctx.desc = desc
+        ctx.meta = meta
+        ctx.save_for_backward(partial_value, inter, lse, *opt_flat)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out):
+        has = ctx.meta[0]
+        saved = ctx.saved_tensors
+        partial_value = saved[0]
+        partial_key, query, partial_logit, bias_t, scale_t = _unflatten_opt(has, saved[3:])
+        want = ctx.needs_input_grad
+        # needs_input_grad index of each present optional input (after meta, partial, inter, lse)
+        pos = {}
+        k = 4
+        for name, h in zip(("pk", "q", "pl", "b", "s"), has):
+            if h:
+                pos[name] = k
+                k += 1
+        want_dbias = bias_t is not None and want[pos["b"]]
+        want_dscale = scale_t is not None and want[pos["s"]]
+        dev = partial_value.device
+        with _device_ctx(dev):
+            dp, dpk, dq, di, dl, dlg, db, ds = _hip.phase2_backward(
+                ctx.desc, dev, partial_value.dtype, grad_out.contiguous(),
+                want_dquery=query is not None and partial_logit is None,
+                query_shape=tuple(query.shape) if query is not None else (0,),
+                logit_dtype=partial_logit.dtype if partial_logit is not None else None,
+                want_dbias=want_dbias, want_dscale=want_dscale)
+        grads = [None, dp if want[1] else None, di if want[2] else None, dl if want[3] else None]
+        for name, g in (("pk", dpk), ("q", dq), ("pl", dlg), ("b", db), ("s", ds)):
+            if name in pos:
+                t = pos[name]
+                if name == "b" and g is not None:
+                    g = g.reshape(bias_t.shape)
+                if name == "s" and g is not None:
+                    g = g.reshape(scale_t.shape)
+                grads.append(g if want[t] else None)
+        return tuple(grads)
+
+
 def _scalar_arg(x, device, what):
     """(float value, fp32 [1] tensor or None) for a float-or-tensor argument."""
     if x is None:
@@ -653,8 +857,14 @@ def _phase2(partial_value, partial_key, query, partial_logit, interblock_output,
         q = query.reshape(-1).to(dtype).contiguous()
         if q.numel() != D:
             raise RuntimeError(f"{what}: query must have {D} elements, got {q.numel()}")
-    out = _phase2_op(pv, pk, q, pl, it, lse, bias_t, scale_t, int(merge), bool(key_norm), bool(normalize_output),
-                     float(logit_scale), bias_value, scale_value, bool(scale_key))
+    if _compiling():
+        out = _phase2_op(pv, pk, q, pl, it, lse, bias_t, scale_t, int(merge), bool(key_norm), bool(normalize_output),
+                         float(logit_scale), bias_value, scale_value, bool(scale_key))
+    else:
+        opt = (pk, q, pl, bias_t, scale_t)
+        meta = (tuple(t is not None for t in opt), int(merge), bool(key_norm), bool(normalize_output),
+                float(logit_scale), bias_value, scale_value, bool(scale_key))
+        out = _Phase2Fn.apply(meta, pv, it, lse, *[t for t in opt if t is not None])
     return out.view(B, T, D)
 
 
@@ -763,6 +973,34 @@ def _keyed_split_backward(ctx, grad_out, grad_key, grad_inv):
 _keyed_split_op.register_autograd(_keyed_split_backward, setup_context=_keyed_split_setup_context)
 
 
+class _KeySplitFn(torch.autograd.Function):
+    """Eager autograd of the key-producer epilogue: inputs (meta, y [n, P])."""
+
+    @staticmethod
+    def forward(ctx, meta, y):
+        dim, rank, heads, key_norm = meta
+        ctx.set_materialize_grads(False)
+        with _device_ctx(y.device):
+            out, key, inv = _hip.keyed_split_forward(y, dim, rank, heads, key_norm)
+        ctx.args = (y.size(0), y.size(1), dim, rank, heads, key_norm)
+        # the raw key (inside y) is read only by the key-norm backward
+        ctx.save_for_backward(y if key_norm else None, inv)
+        return out, key
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out, grad_key):
+        y, inv = ctx.saved_tensors
+        if grad_out is None and grad_key is None:
+            return None, None
+        go = grad_out.contiguous() if grad_out is not None else None
+        gk = grad_key.contiguous() if grad_key is not None else None
+        like = go if go is not None else gk
+        with _device_ctx(like.device):
+            gy = _hip.keyed_split_backward(y, *ctx.args, go, gk, inv, like.dtype, like.device)
+        return None, gy
+
+
 def lrid_fused_projection_split(projected: Tensor, output_dim: int, rank: int, num_heads: int = 1,
                                 key_norm: bool = True):
     """Sublayer output and LR key from a fused ``[out | key | pad]`` projection.
@@ -785,5 +1023,8 @@ def lrid_fused_projection_split(projected: Tensor, output_dim: int, rank: int, n
     y = projected.reshape(-1, projected.size(-1))
     if y.stride(-1) != 1:
         y = y.contiguous()
-    out, key, _ = _keyed_split_op(y, int(output_dim), int(rank), int(num_heads), bool(key_norm))
+    if _compiling():
+        out, key, _ = _keyed_split_op(y, int(output_dim), int(rank), int(num_heads), bool(key_norm))
+    else:
+        out, key = _KeySplitFn.apply((int(output_dim), int(rank), int(num_heads), bool(key_norm)), y)
     return out.view(*lead, output_dim), key.view(*lead, rank)

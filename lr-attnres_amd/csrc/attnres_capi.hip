@@ -199,6 +199,17 @@ PartLayout part_layout(const attnres_read_desc* d, bool want_q, bool want_gate, 
   return L;
 }
 
+// Zeroes `bytes` bytes with a kernel on the caller's stream.  A memset node
+// would do the same, but callers may capture these calls in a HIP graph, where
+// a kernel node is the safer form.  Used only for the gradients of empty inputs
+// (a few KB at most).
+__global__ void zero_bytes_kernel(unsigned char* p, size_t bytes) {
+  for (size_t i = threadIdx.x; i < bytes; i += blockDim.x) p[i] = 0;
+}
+void zero_async(void* p, size_t bytes, hipStream_t st) {
+  if (p && bytes) hipLaunchKernelGGL(zero_bytes_kernel, dim3(1), dim3(256), 0, st, (unsigned char*)p, bytes);
+}
+
 int64_t bwd_groups(int64_t n_tok) { return n_tok < kMaxBwdGroups ? n_tok : kMaxBwdGroups; }
 
 // LR fast path: one wave per (token, head-aligned column group).  Returns false
@@ -368,10 +379,9 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     // gradients of the cross-token quantities are zero
     hipStream_t st = (hipStream_t)stream;
     const int es = elem_size(d->dtype);
-    if (softmax && g->dquery && d->query)
-      (void)hipMemsetAsync(g->dquery, 0, (size_t)(lr ? d->rank : d->dim) * es, st);
-    if (softmax && g->dgate && d->gate && !d->gate_per_token) (void)hipMemsetAsync(g->dgate, 0, (size_t)d->heads * es, st);
-    if (softmax && g->dbias && d->logit_bias) (void)hipMemsetAsync(g->dbias, 0, (size_t)d->n_src * 4, st);
+    if (softmax && g->dquery && d->query) zero_async(g->dquery, (size_t)(lr ? d->rank : d->dim) * es, st);
+    if (softmax && g->dgate && d->gate && !d->gate_per_token) zero_async(g->dgate, (size_t)d->heads * es, st);
+    if (softmax && g->dbias && d->logit_bias) zero_async(g->dbias, (size_t)d->n_src * 4, st);
     return ATTNRES_OK;
   }
   Plan pl;
@@ -817,10 +827,9 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
   const bool lr = d->rank > 0 && !d->logit_given;
   hipStream_t st = (hipStream_t)stream;
   if (d->n_tok == 0) {
-    if (g->dquery && !d->logit_given)
-      (void)hipMemsetAsync(g->dquery, 0, (size_t)(lr ? d->rank : d->dim) * elem_size(d->dtype), st);
-    if (g->dlogit_bias) (void)hipMemsetAsync(g->dlogit_bias, 0, sizeof(float), st);
-    if (g->dvalue_scale) (void)hipMemsetAsync(g->dvalue_scale, 0, sizeof(float), st);
+    if (g->dquery && !d->logit_given) zero_async(g->dquery, (size_t)(lr ? d->rank : d->dim) * elem_size(d->dtype), st);
+    if (g->dlogit_bias) zero_async(g->dlogit_bias, sizeof(float), st);
+    if (g->dvalue_scale) zero_async(g->dvalue_scale, sizeof(float), st);
     return ATTNRES_OK;
   }
   if (!g->grad_out || !g->dpartial_value || !g->dinterblock_output || !g->dinterblock_lse)
