@@ -218,19 +218,10 @@ struct FastPlan {
   int vb, cb, nb, rhc, n_items, nh, kch, np;
 };
 
-// value vector bytes of the fast kernels: 8-byte lane vectors make one-head
-// work items for heads of 64*4 bf16 elements (half the registers of 16-byte
-// vectors, so more waves in flight)
-int fast_vector_bytes(const attnres_read_desc* d) {
-  const char* env = getenv("ATTNRES_FAST_VB");
-  if (env && (atoi(env) == 8 || atoi(env) == 16)) return atoi(env);
-  return 16;
-}
-
 bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, FastPlan* f) {
   if (!pl.lr || !pl.vec || !pl.key_vec) return false;
   const int es = elem_size(d->dtype);
-  f->vb = fast_vector_bytes(d);
+  f->vb = 16;  // 16-byte lane vectors
   const int E = f->vb / es;
   const int colw = kWaveSize * E;
   const int dh = d->dim / d->heads, rh = d->rank / d->heads;
@@ -249,7 +240,6 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   if (d->normalize_output && f->n_items != 1) return false;
   const int N = d->n_src;
   if (N > (f->cb == 2 ? 16 : 32)) return false;
-  f->nb = N <= 8 ? 8 : N <= 16 ? 16 : 32;
   f->np = 2;  // at least two lanes per head: the packed mix reads source pairs
   while (f->np < N) f->np <<= 1;
   // 32-bit token index and byte strides in the fast kernels' address math
@@ -264,7 +254,21 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   f->kch = rh * es / 16;
   if (f->kch > 8) return false;
   f->rhc = f->kch <= 2 ? 2 : 8;
+  // value slots: the kernels load NB rows per token whatever N is (branch-free
+  // unrolled loads; slots past N re-read a real row), so each slot past N is a
+  // wasted load instruction.  The common shape (one column per wave, short key
+  // slices) is instantiated for slot counts close together.
+  f->nb = N <= 8 ? 8 : N <= 16 ? 16 : 32;
+  if (f->cb == 1 && f->rhc == 2) {
+    static const int kFineSlots[] = {8, 12, 14, 16, 20, 24, 32};
+    for (int nb : kFineSlots)
+      if (N <= nb) {
+        f->nb = nb;
+        break;
+      }
+  }
   if (f->cb == 2 && f->rhc == 8 && f->nb == 16) return false;  // no register room
+  if (f->cb == 1 && f->rhc == 8 && f->vb == 16 && f->nb == 32) return false;  // not instantiated
   return true;
 }
 

@@ -22,7 +22,8 @@
 // not pin dozens of SGPRs for the whole kernel.
 //
 // Requirements (checked on the host, else the general kernels run):
-// 16-byte vector path, N <= NB (8/16/32), N * heads_per_item <= 64 pairs,
+// 16-byte vector path, N <= NB (8/16/32, or 12/14/20/24 for one column
+// and two key chunks), N * heads_per_item <= 64 pairs,
 // key slice of a head = kch 16-byte chunks with kch <= RHC, heads_per_item *
 // (R/H) <= 64 (a power of two when the backward has a gate), output norm only
 // when one item covers the whole row.
@@ -680,24 +681,23 @@ static hipError_t fast_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_
   return hipGetLastError();
 }
 
-// L.vec = value vector bytes (16 / 8), L.wpt = columns per item (1/2),
-// L.nmax = source slots (8/16/32), L.teams = key chunks per head slot (2/8)
+// L.vec = value vector bytes (16), L.wpt = columns per item (1/2),
+// L.nmax = source slots (8/16/32; also 12/14/20/24 for one column and two key
+// chunks), L.teams = key chunks per head slot (2/8)
 #define ATTNRES_FAST_SWITCH(fn, P)                        \
   switch (L.vec * 10000 + L.wpt * 1000 + L.nmax * 10 + L.teams) { \
     case 161082: return fn<DT, 16, 1, 8, 2>(P, L, st);    \
+    case 161122: return fn<DT, 16, 1, 12, 2>(P, L, st);   \
+    case 161142: return fn<DT, 16, 1, 14, 2>(P, L, st);   \
     case 161162: return fn<DT, 16, 1, 16, 2>(P, L, st);   \
+    case 161202: return fn<DT, 16, 1, 20, 2>(P, L, st);   \
+    case 161242: return fn<DT, 16, 1, 24, 2>(P, L, st);   \
     case 161322: return fn<DT, 16, 1, 32, 2>(P, L, st);   \
     case 161088: return fn<DT, 16, 1, 8, 8>(P, L, st);    \
     case 161168: return fn<DT, 16, 1, 16, 8>(P, L, st);   \
     case 162082: return fn<DT, 16, 2, 8, 2>(P, L, st);    \
     case 162162: return fn<DT, 16, 2, 16, 2>(P, L, st);   \
     case 162088: return fn<DT, 16, 2, 8, 8>(P, L, st);    \
-    case 81082: return fn<DT, 8, 1, 8, 2>(P, L, st);      \
-    case 81162: return fn<DT, 8, 1, 16, 2>(P, L, st);     \
-    case 81322: return fn<DT, 8, 1, 32, 2>(P, L, st);     \
-    case 81088: return fn<DT, 8, 1, 8, 8>(P, L, st);      \
-    case 81168: return fn<DT, 8, 1, 16, 8>(P, L, st);     \
-    case 81328: return fn<DT, 8, 1, 32, 8>(P, L, st);     \
     default: return hipErrorInvalidValue;                 \
   }
 

@@ -139,7 +139,7 @@ def test_lr_options_dynamic_bias_norm(dtype):
     _lr_case(205, dtype, 2, 5, 256, 5, 64, 4, 0.125, True, normalize_output=True, bias=[0.1, 0.2, 0.3, 0.4, 0.5])
 
 
-@pytest.mark.parametrize("S", [2, 9, 16, 17, 33, 64])
+@pytest.mark.parametrize("S", [2, 9, 13, 16, 17, 21, 24, 33, 64])
 def test_lr_source_counts(S):
     _lr_case(300 + S, torch.bfloat16, 1, 5, 128, S, 32, 2, 0.25, True)
 
