@@ -31,8 +31,8 @@ __device__ __forceinline__ void store_prenorm(const ReadParams& p, int64_t tok, 
 }
 
 // ============================================================== base forward
-template <class DT, int E, int CB, int NMAX>
-__global__ void __launch_bounds__(1024) base_fwd_kernel(const ReadParams p) {
+template <class DT, int E, int CB, int NMAX, int MAXT>
+__global__ void __launch_bounds__(MAXT) base_fwd_kernel(const ReadParams p) {
   using S = typename DT::S;
   extern __shared__ float smem[];
   float* s_red = smem;  // [wpt * NMAX]
@@ -710,7 +710,12 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
 // ============================================================== launchers
 template <class DT, int E, int CB, int NMAX>
 static hipError_t base_fwd_t(const ReadParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((base_fwd_kernel<DT, E, CB, NMAX>), dim3(L.grid), dim3(L.wpt * kWave), L.lds, st, p);
+  // workgroups of at most 256 threads may use up to 256 VGPRs per lane (the
+  // rows of 16 sources stay resident without spilling)
+  if (L.wpt * kWave <= 256)
+    hipLaunchKernelGGL((base_fwd_kernel<DT, E, CB, NMAX, 256>), dim3(L.grid), dim3(L.wpt * kWave), L.lds, st, p);
+  else
+    hipLaunchKernelGGL((base_fwd_kernel<DT, E, CB, NMAX, 1024>), dim3(L.grid), dim3(L.wpt * kWave), L.lds, st, p);
   return hipGetLastError();
 }
 template <class DT, int E, int CB, int NMAX>
@@ -726,9 +731,19 @@ static hipError_t base_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_
 
 // Resident path (N <= 16): vector path keeps two columns per lane.  More
 // sources take the streaming kernels, which read each value row twice.
+// 16-bit rows of 256 or 768 elements use 8-byte vectors in one or three
+// columns, so that every lane of the wave holds part of the row (16-byte
+// vectors would leave half of the last column's lanes idle).
 template <class DT>
 static hipError_t base_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st) {
   constexpr int EV = 16 / sizeof(typename DT::S);
+  if constexpr (sizeof(typename DT::S) == 2) {
+    if (L.vec && L.vb == 8) {
+      if (L.wpt == 1 && p.ncols == 1)
+        return L.nmax == 8 ? base_fwd_t<DT, EV / 2, 1, 8>(p, L, st) : base_fwd_t<DT, EV / 2, 1, 16>(p, L, st);
+      return L.nmax == 8 ? base_fwd_t<DT, EV / 2, 3, 8>(p, L, st) : base_fwd_t<DT, EV / 2, 3, 16>(p, L, st);
+    }
+  }
   if (L.vec) {
     switch (L.nmax) {
       case 8: return base_fwd_t<DT, EV, 2, 8>(p, L, st);
@@ -749,6 +764,13 @@ static hipError_t base_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t 
 template <class DT>
 static hipError_t base_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
   constexpr int EV = 16 / sizeof(typename DT::S);
+  if constexpr (sizeof(typename DT::S) == 2) {
+    if (L.vec && L.vb == 8) {
+      if (L.wpt == 1 && p.f.ncols == 1)
+        return L.nmax == 8 ? base_bwd_t<DT, EV / 2, 1, 8>(p, L, st) : base_bwd_t<DT, EV / 2, 1, 16>(p, L, st);
+      return L.nmax == 8 ? base_bwd_t<DT, EV / 2, 3, 8>(p, L, st) : base_bwd_t<DT, EV / 2, 3, 16>(p, L, st);
+    }
+  }
   if (L.vec) {
     switch (L.nmax) {
       case 8: return base_bwd_t<DT, EV, 2, 8>(p, L, st);

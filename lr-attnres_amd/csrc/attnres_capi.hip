@@ -49,6 +49,7 @@ struct Plan {
   int wpt;
   int nmax;
   int key_vec;
+  int vb;         // vector bytes of the vector path (16, or 8 for 16-bit base rows of 256 / 768)
 };
 
 int check_desc(const attnres_read_desc* d) {
@@ -113,12 +114,22 @@ int make_plan(const attnres_read_desc* d, const void* const* extra, int n_extra,
   if (vec && d->mode == ATTNRES_MODE_SOFTMAX && d->rank == 0) vec = aligned16(d->query);
   pl->vec = vec ? 1 : 0;
   pl->E = vec ? EV : 1;
+  pl->vb = 16;
   pl->ncols = (d->dim + kWaveSize * pl->E - 1) / (kWaveSize * pl->E);
   pl->nmax = 0;
   if (d->mode == ATTNRES_MODE_SOFTMAX && d->rank == 0) {
     // register-resident kernels for up to 16 sources, streaming beyond
     pl->nmax = d->n_src <= 8 ? 8 : d->n_src <= 16 ? 16 : 64;
     pl->cb = vec ? 2 : 4;
+    // 16-bit rows of 256 or 768 elements: 8-byte vectors fill one or three
+    // whole columns of a wave (16-byte ones leave half a column idle)
+    const int col8 = kWaveSize * (EV / 2);
+    if (vec && es == 2 && pl->nmax <= 16 && (d->dim == col8 || d->dim == 3 * col8)) {
+      pl->E = EV / 2;
+      pl->vb = 8;
+      pl->ncols = d->dim / col8;
+      pl->cb = pl->ncols;
+    }
   } else {
     pl->cb = vec ? 2 : 4;
   }
@@ -318,7 +329,9 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
   p.out_inv_rms = out_inv_rms;
 
   Launch L;
+  memset(&L, 0, sizeof(L));
   L.vec = pl.vec;
+  L.vb = pl.vb;
   L.wpt = pl.wpt;
   L.nmax = pl.nmax;
   L.teams = 1;
@@ -422,7 +435,9 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   bp.part_bias = PL.part_bias;
 
   Launch L;
+  memset(&L, 0, sizeof(L));
   L.vec = pl.vec;
+  L.vb = pl.vb;
   L.wpt = pl.wpt;
   L.nmax = pl.nmax;
   L.teams = 1;

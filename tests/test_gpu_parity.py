@@ -229,9 +229,47 @@ def test_base_matches_oracle(dtype, key_norm):
     _base_case(600 + int(key_norm), dtype, 2, 6, 256, 5, key_norm)
 
 
-@pytest.mark.parametrize("S,D", [(2, 64), (7, 768), (12, 1024), (16, 2048), (17, 256), (40, 128), (5, 40)])
+@pytest.mark.parametrize("S,D", [(2, 64), (7, 768), (13, 768), (9, 256), (12, 1024), (16, 2048), (17, 256),
+                                 (40, 128), (5, 40)])
 def test_base_shapes(S, D):
     _base_case(700 + S, torch.bfloat16, 1, 5, D, S, True)
+
+
+def test_base_row768_fp16_norm_counts():
+    """768-element 16-bit rows (three 8-byte columns per wave) with output norm and counts."""
+    _base_case(805, torch.float16, 2, 4, 768, 7, True, normalize_output=True, counts=[1, 2, 2, 2, 2, 2, 2])
+
+
+def test_config2_full_size_token_subset():
+    """C2 (B8 T1024 d768 N7 bf16, rms-norm keys) at full size, checked on a
+    token subset; the query gradient over all tokens by linearity."""
+    g = gen(2)
+    B, T, D, S = 8, 1024, 768, 7
+    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
+    q = torch.randn(D, generator=g) * 0.02
+    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    vd = [leaf(x) for x in vals]
+    qd = leaf(q)
+    out = ops.attention_residual_read(vd, qd, True)
+    out.backward(up.to(DEV))
+    torch.cuda.synchronize()
+    sel = (slice(5, 6), slice(200, 264))
+    vc = [x[sel].clone().requires_grad_(True) for x in vals]
+    qc = q.clone().requires_grad_(True)
+    ref = O.attention_residual_read_ref(vc, qc, True)
+    ref.backward(up[sel])
+    assert_close(out[sel], ref, torch.bfloat16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad[sel], vc[s].grad, torch.bfloat16, f"dv{s}")
+    halves = []
+    for part in (slice(0, 4), slice(4, 8)):
+        qh = leaf(q)
+        o = ops.attention_residual_read([x.detach()[part] for x in vd], qh, True)
+        o.backward(up[part].to(DEV))
+        halves.append(qh.grad)
+    full = qd.grad.float().cpu()
+    summed = (halves[0].float() + halves[1].float()).cpu()
+    assert float((full - summed).abs().max()) <= 2e-2 * max(1.0, float(full.abs().max()))
 
 
 def test_base_options():
