@@ -522,21 +522,34 @@ namespace {
 
 struct PhasePlan {
   int vec, E, cb, ncols, wpt;
+  int vb;  // vector bytes of the vector path
 };
 
 // Row geometry of the phase kernels: one 16-byte vector per column when every
 // row is aligned (fp32: two columns per lane), else eight single-element
-// columns per lane; at most 8 waves per token.
-int phase_plan(int dtype, int dim, const void* const* rows, const int64_t* strides, int n_rows, PhasePlan* pl) {
+// columns per lane; at most 8 waves per token.  With `rows8`, 16-bit rows of
+// 256 or 768 elements take one wave of 8-byte vectors (one or three columns
+// per lane, every lane busy) instead of one or two waves of 16-byte vectors
+// with idle lanes; `rows8` is the largest column count allowed (0: off).
+int phase_plan(int dtype, int dim, const void* const* rows, const int64_t* strides, int n_rows, PhasePlan* pl,
+               int rows8 = 0) {
   const int es = elem_size(dtype);
   const int EV = 16 / es;
   bool vec = dim % EV == 0;
   for (int i = 0; vec && i < n_rows; ++i)
     vec = (!rows[i] || aligned16(rows[i])) && ((strides[i] * es) % 16 == 0);
   pl->vec = vec ? 1 : 0;
+  pl->vb = 16;
   pl->E = vec ? EV : 1;
   pl->cb = vec ? (es == 4 ? 2 : 1) : 8;
   pl->ncols = (dim + kWaveSize * pl->E - 1) / (kWaveSize * pl->E);
+  const int col8 = kWaveSize * (EV / 2);
+  if (vec && es == 2 && ((dim == col8 && rows8 >= 1) || (dim == 3 * col8 && rows8 >= 3))) {
+    pl->vb = 8;
+    pl->E = EV / 2;
+    pl->ncols = dim / col8;
+    pl->cb = pl->ncols;
+  }
   pl->wpt = (pl->ncols + pl->cb - 1) / pl->cb;
   if (pl->wpt > 8) return fail(ATTNRES_EUNSUPPORTED, "dim=%d exceeds the phase kernels' row width", dim);
   return ATTNRES_OK;
@@ -728,7 +741,7 @@ extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, v
   rows[d->n_src] = out;
   rows[d->n_src + 1] = d->normalize_output ? out_prenorm : nullptr;
   strides[d->n_src] = strides[d->n_src + 1] = d->dim;
-  rc = phase_plan(d->dtype, d->dim, rows, strides, d->n_src + 2, &pl);
+  rc = phase_plan(d->dtype, d->dim, rows, strides, d->n_src + 2, &pl, 3);
   if (rc) return rc;
   Phase1Params p;
   fill_phase1(d, pl, &p);
@@ -739,6 +752,7 @@ extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, v
   Launch L;
   memset(&L, 0, sizeof(L));
   L.vec = pl.vec;
+  L.vb = pl.vb;
   L.wpt = pl.wpt;
   L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
   L.lds = ((size_t)pl.wpt * d->n_q * d->n_src + 8 * (size_t)pl.wpt) * sizeof(float);
@@ -772,7 +786,8 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   strides[n++] = d->dim;
   rows[n] = d->normalize_output ? out_prenorm : nullptr;
   strides[n++] = d->dim;
-  rc = phase_plan(d->dtype, d->dim, rows, strides, n, &pl);
+  // three 8-byte columns hold the upstream rows of at most 4 sites in registers
+  rc = phase_plan(d->dtype, d->dim, rows, strides, n, &pl, d->n_q <= 4 ? 3 : 1);
   if (rc) return rc;
   Phase1Params p;
   fill_phase1(d, pl, &p);
@@ -785,6 +800,7 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   Launch L;
   memset(&L, 0, sizeof(L));
   L.vec = pl.vec;
+  L.vb = pl.vb;
   L.wpt = pl.wpt;
   L.nmax = d->n_q <= 4 ? 4 : d->n_q <= 8 ? 8 : ATTNRES_PHASE1_MAX_QUERIES;
   L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);

@@ -65,7 +65,9 @@ __device__ __forceinline__ void phase1_load_rows(const Phase1Params& p, int64_t 
 }
 
 // ============================================================== forward
-template <class DT, int E, int CB>
+// QC read sites accumulate per pass over the source rows (kP1QC; 4 when a
+// lane holds three columns, to stay within the register budget)
+template <class DT, int E, int CB, int QC = kP1QC>
 __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
   using S = typename DT::S;
   extern __shared__ float smem[];
@@ -73,7 +75,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int wpt = blockDim.x / kWave;
   float* w = smem + wave * Q * N;    // this wave's weights [Q * N]
-  float* s_red = smem + wpt * Q * N;  // [wpt * kP1QC]
+  float* s_red = smem + wpt * Q * N;  // [wpt * QC]
   const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
 
   Raw<DT, E> r[kP1SC][CB];
@@ -84,10 +86,10 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
     phase1_softmax(p, tok, lane, w, wave == 0);
     wave_sync();
 
-    for (int q0 = 0; q0 < Q; q0 += kP1QC) {
-      float acc[kP1QC][CB][E];
+    for (int q0 = 0; q0 < Q; q0 += QC) {
+      float acc[QC][CB][E];
 #pragma unroll
-      for (int qq = 0; qq < kP1QC; ++qq)
+      for (int qq = 0; qq < QC; ++qq)
 #pragma unroll
         for (int c = 0; c < CB; ++c)
 #pragma unroll
@@ -101,7 +103,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
 #pragma unroll
             for (int c = 0; c < CB; ++c) unpack<DT, E>(r[j][c], v[c]);
 #pragma unroll
-            for (int qq = 0; qq < kP1QC; ++qq) {
+            for (int qq = 0; qq < QC; ++qq) {
               if (q0 + qq < Q) {
                 const float wq = DT::rnd(w[(q0 + qq) * N + s0 + j]);
 #pragma unroll
@@ -115,10 +117,10 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
       }
       // the next token's first batch of value rows goes out before this
       // token's stores
-      if (q0 + kP1QC >= Q && tok + gridDim.x < p.n_tok) phase1_load_rows<DT, E, CB>(p, tok + gridDim.x, 0, r, cl);
-      float ss[kP1QC];
+      if (q0 + QC >= Q && tok + gridDim.x < p.n_tok) phase1_load_rows<DT, E, CB>(p, tok + gridDim.x, 0, r, cl);
+      float ss[QC];
 #pragma unroll
-      for (int qq = 0; qq < kP1QC; ++qq) {
+      for (int qq = 0; qq < QC; ++qq) {
         ss[qq] = 0.f;
 #pragma unroll
         for (int c = 0; c < CB; ++c)
@@ -128,10 +130,10 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
             if (cl.ok[c]) ss[qq] += acc[qq][c][e] * acc[qq][c][e];
           }
       }
-      const int nq = Q - q0 < kP1QC ? Q - q0 : kP1QC;
+      const int nq = Q - q0 < QC ? Q - q0 : QC;
       if (p.norm_out) {
 #pragma unroll
-        for (int qq = 0; qq < kP1QC; ++qq) {
+        for (int qq = 0; qq < QC; ++qq) {
           if (qq < nq && p.out_prenorm) {
             S* xp = (S*)p.out_prenorm + ((int64_t)(q0 + qq) * p.n_tok + tok) * D;
 #pragma unroll
@@ -139,9 +141,9 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
               if (cl.ok[c]) store_vec<DT, E, true>(xp + cl.eoff[c], acc[qq][c]);
           }
         }
-        block_allreduce<kP1QC>(ss, nq, s_red, lane, wave, wpt);
+        block_allreduce<QC>(ss, nq, s_red, lane, wave, wpt);
 #pragma unroll
-        for (int qq = 0; qq < kP1QC; ++qq) {
+        for (int qq = 0; qq < QC; ++qq) {
           if (qq < nq) {
             const float inv = 1.0f / sqrtf(ss[qq] / (float)D + p.eps);
 #pragma unroll
@@ -153,7 +155,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_kernel(const Phase1Params p) {
         }
       }
 #pragma unroll
-      for (int qq = 0; qq < kP1QC; ++qq) {
+      for (int qq = 0; qq < QC; ++qq) {
         if (qq < nq) {
           S* op = (S*)p.out + ((int64_t)(q0 + qq) * p.n_tok + tok) * D;
 #pragma unroll
@@ -342,10 +344,21 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
 // ============================================================== launchers
 // Vector path: one 16-byte vector per column (fp32: two columns per lane);
 // unaligned rows: eight single-element columns per lane.
+// 16-bit rows of 256 / 768 elements: one wave of 8-byte vectors, one or three
+// columns per lane.
 template <class DT>
 static hipError_t phase1_fwd_dt(const Phase1Params& p, const Launch& L, hipStream_t st) {
   constexpr int EV = 16 / sizeof(typename DT::S);
   constexpr int CBV = sizeof(typename DT::S) == 4 ? 2 : 1;
+  if constexpr (sizeof(typename DT::S) == 2) {
+    if (L.vec && L.vb == 8) {
+      if (p.ncols == 1)
+        hipLaunchKernelGGL((phase1_fwd_kernel<DT, EV / 2, 1>), dim3(L.grid), dim3(kWave), L.lds, st, p);
+      else
+        hipLaunchKernelGGL((phase1_fwd_kernel<DT, EV / 2, 3, 4>), dim3(L.grid), dim3(kWave), L.lds, st, p);
+      return hipGetLastError();
+    }
+  }
   if (L.vec)
     hipLaunchKernelGGL((phase1_fwd_kernel<DT, EV, CBV>), dim3(L.grid), dim3(L.wpt * kWave), L.lds, st, p);
   else
@@ -358,6 +371,20 @@ static hipError_t phase1_bwd_dt(const Phase1Params& p, const Launch& L, hipStrea
   constexpr int EV = 16 / sizeof(typename DT::S);
   constexpr int CBV = sizeof(typename DT::S) == 4 ? 2 : 1;
   const dim3 g(L.grid), b(L.wpt * kWave);
+  if constexpr (sizeof(typename DT::S) == 2) {
+    if (L.vec && L.vb == 8) {
+      if (p.ncols == 1) {
+        if (L.nmax <= 4) hipLaunchKernelGGL((phase1_bwd_kernel<DT, EV / 2, 1, 4>), g, b, L.lds, st, p);
+        else if (L.nmax <= 8) hipLaunchKernelGGL((phase1_bwd_kernel<DT, EV / 2, 1, 8>), g, b, L.lds, st, p);
+        else hipLaunchKernelGGL((phase1_bwd_kernel<DT, EV / 2, 1, kPhase1MaxQ>), g, b, L.lds, st, p);
+      } else {
+        // three columns: the host picks this layout for at most 4 sites
+        if (L.nmax > 4) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((phase1_bwd_kernel<DT, EV / 2, 3, 4>), g, b, L.lds, st, p);
+      }
+      return hipGetLastError();
+    }
+  }
   if (L.vec) {
     if (L.nmax <= 4) hipLaunchKernelGGL((phase1_bwd_kernel<DT, EV, CBV, 4>), g, b, L.lds, st, p);
     else if (L.nmax <= 8) hipLaunchKernelGGL((phase1_bwd_kernel<DT, EV, CBV, 8>), g, b, L.lds, st, p);
