@@ -283,6 +283,12 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   return true;
 }
 
+// The fast LR kernels have LEAN instantiations without the per-token query /
+// gate and output-norm code, for reads that use neither.
+bool lr_fast_lean(const attnres_read_desc* d) {
+  return !d->query_dyn && !d->gate && !d->normalize_output;
+}
+
 // token teams per LR-backward workgroup: four independent one-wave teams when a
 // token fits one wave, else one team of wpt waves
 int lr_bwd_teams(const Plan& pl) { return pl.wpt == 1 ? 4 : 1; }
@@ -354,6 +360,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       L.wpt = f.cb;
       L.nmax = f.nb;
       L.teams = f.rhc;
+      L.lean = lr_fast_lean(d);
       L.grid = (int)((f.n_items * (int64_t)p.streams + 3) / 4);
       L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float);
       err = launch_lr_fast_forward(d->dtype, p, L, st);
@@ -441,16 +448,18 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   L.wpt = pl.wpt;
   L.nmax = pl.nmax;
   L.teams = 1;
-  L.grid = (int)groups;
+  const int64_t full_groups = groups < kFullBwdGroups ? groups : kFullBwdGroups;
+  L.grid = (int)full_groups;
   if (lr) L.teams = lr_bwd_teams(pl);
   else if (softmax && pl.nmax <= 16 && pl.wpt == 1) L.teams = 4;  // resident base read, one wave per token
   if (L.teams > 1) {
     // workgroups carry `teams` tokens at a time; the workspace is sized for
     // `groups` partials and the grid never exceeds it
     const int64_t need = (d->n_tok + L.teams - 1) / L.teams;
-    L.grid = (int)(need < groups ? need : groups);
+    L.grid = (int)(need < full_groups ? need : full_groups);
   }
   hipStream_t st = (hipStream_t)stream;
+  bool fast = false;  // fast LR backward: partials are slot-major
   hipError_t err;
   if (d->mode == ATTNRES_MODE_AVERAGE) {
     L.lds = 32 * sizeof(float);
@@ -458,12 +467,17 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   } else if (lr) {
     FastPlan f;
     int64_t streams = 0;
+    const bool lean = lr_fast_lean(d);
     if (lr_fast_plan(d, pl, true, &f)) {
-      // at most `groups` workgroups of four waves (the workspace rows)
-      streams = 4 * groups / f.n_items;
+      // at most `groups` workgroups of four waves (the workspace rows); the
+      // full kernels (3 waves per SIMD) stream best with 2048 workgroups, the
+      // lean ones (4 per SIMD) with twice as many (measured at C3 and C4)
+      const int64_t cap = lean ? groups : (groups < kFullBwdGroups ? groups : kFullBwdGroups);
+      streams = 4 * cap / f.n_items;
       if (streams > d->n_tok) streams = d->n_tok;
     }
     if (streams > 0) {
+      fast = true;
       bp.f.n_items = f.n_items;
       bp.f.nh = f.nh;
       bp.f.kch = f.kch;
@@ -473,6 +487,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       L.wpt = f.cb;
       L.nmax = f.nb;
       L.teams = f.rhc;
+      L.lean = lean;
       L.grid = (int)((f.n_items * streams + 3) / 4);
       L.lds = lr_fast_table_bytes() +
               ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *
@@ -496,9 +511,11 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
 
   if (PL.n_part > 0) {
     ReduceParams rp;
+    memset(&rp, 0, sizeof(rp));
     rp.partials = bp.partials;
     rp.n_groups = L.grid;
     rp.n_part = PL.n_part;
+    rp.slot_major = fast ? 1 : 0;
     rp.part_q = PL.part_q;
     rp.n_q = PL.n_q;
     rp.part_gate = PL.part_gate;
@@ -909,11 +926,12 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     L.vb = wv.vb;
     L.wpt = wv.cb;
     const int64_t wgs = (d->n_tok + kPhase2Teams - 1) / kPhase2Teams;
-    L.grid = (int)(wgs < groups ? wgs : groups);
+    const int64_t cap = groups < kFullBwdGroups ? groups : kFullBwdGroups;
+    L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
   } else {
     L.wpt = phase2_waves(d, pl);
-    L.grid = (int)groups;
+    L.grid = (int)(groups < kFullBwdGroups ? groups : kFullBwdGroups);
     L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
   }
   hipError_t err = launch_phase2_backward(d->dtype, p, L, st);

@@ -15,7 +15,8 @@ struct Launch {
   size_t lds;   // dynamic LDS bytes
   int nmax;     // base read: register-resident source slots (8/16; more = streaming)
   int teams;    // token teams per workgroup (LR backward; phase 2: waves per workgroup)
-  int vb;       // phase 2 one-wave-per-token kernels: vector bytes (16 or 8)
+  int vb;       // vector bytes (16 or 8) where a kernel family has both layouts
+  int lean;     // LR fast path: no per-token query / gate and no output norm
 };
 
 hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
@@ -40,5 +41,13 @@ hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch
 // L.vec = 16-byte vectors for the output columns
 hipError_t launch_keyed_split_forward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_keyed_split_backward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);
+
+// dtype switch of the launchers
+#define ATTNRES_DISPATCH(dtype, fn, ...)                          \
+  switch (dtype) {                                                \
+    case ATTNRES_DTYPE_F32: return fn<F32>(__VA_ARGS__);          \
+    case ATTNRES_DTYPE_BF16: return fn<BF16>(__VA_ARGS__);        \
+    default: return fn<F16>(__VA_ARGS__);                         \
+  }
 
 }  // namespace attnres

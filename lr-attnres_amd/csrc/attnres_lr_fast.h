@@ -27,6 +27,8 @@
 // key slice of a head = kch 16-byte chunks with kch <= RHC, heads_per_item *
 // (R/H) <= 64 (a power of two when the backward has a gate), output norm only
 // when one item covers the whole row.
+#pragma once
+
 #include "attnres_device.h"
 #include "attnres_params.h"
 #include "attnres_launch.h"
@@ -34,6 +36,10 @@
 namespace attnres {
 
 constexpr int kFastWaves = 4;  // waves per workgroup (independent token streams)
+
+// LEAN instantiations drop the per-token query / gate and output-norm code at
+// compile time (the host picks them when a read has neither): the static-query
+// backward then fits 4 waves per SIMD instead of 3.
 
 // per-source tables in LDS
 struct SrcTab {
@@ -169,7 +175,7 @@ __device__ __forceinline__ float key_query_dot(const KeySlice<DT, RHC>& kr, cons
 }
 
 // ============================================================== forward
-template <class DT, int VB, int CB, int NB, int RHC>
+template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
 __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   using S = typename DT::S;
   constexpr int E = VB / (int)sizeof(S);        // value elements per lane vector
@@ -211,7 +217,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   const int ph = h0 + (lh < nh ? lh : 0);
   const int ps = has_pair ? lsrc : 0;
   const int kch = p.kch;
-  const bool dyn = p.q_dyn != nullptr;
+  const bool dyn = !LEAN && p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
   const uint64_t kbase = tab->kptr[ps] + (uint64_t)(ph * rh) * sizeof(S);
   const uint32_t kstrb = tab->kstrb[ps];
@@ -332,7 +338,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
       }
 
     // ---- stores
-    if (p.norm_out) {  // one item covers the whole row here
+    if (!LEAN && p.norm_out) {  // one item covers the whole row here
       if (p.out_prenorm) {
         S* xp = global_ptr<S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
@@ -355,7 +361,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
 }
 
 // ============================================================== backward
-template <class DT, int VB, int CB, int NB, int RHC>
+template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
 __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp) {
   using S = typename DT::S;
   constexpr int E = VB / (int)sizeof(S);
@@ -401,7 +407,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   const int ph = h0 + (lh < nh ? lh : 0);
   const int ps = has_pair ? lsrc : 0;
   const int kch = p.kch;
-  const bool dyn = p.q_dyn != nullptr;
+  const bool dyn = !LEAN && p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
   // query-gradient owner lanes: (head h0 + lane / rh, element lane % rh)
   const int nq = nh * rh;
@@ -459,7 +465,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
     for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gp + eoff[c], gr[c]);
     Raw<DT, E> xr[CB];
-    if (p.norm_out) {
+    if (!LEAN && p.norm_out) {
       const S* xp = global_ptr<const S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(xp + eoff[c], xr[c]);
@@ -485,7 +491,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     }
 
     // ---- upstream gradient through the output norm (item = whole row)
-    if (p.norm_out) {
+    if (!LEAN && p.norm_out) {
       float dot = 0.f;
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
@@ -663,68 +669,29 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
     float a = 0.f;
     for (int w = 0; w < nwaves; ++w) a += s_fold[w * bp.n_part + i];
-    bp.partials[(int64_t)blockIdx.x * bp.n_part + i] = a;
+    bp.partials[(int64_t)i * gridDim.x + blockIdx.x] = a;  // slot-major: each slot's rows contiguous
   }
 }
 
-// ============================================================== launchers
-template <class DT, int VB, int CB, int NB, int RHC>
-static hipError_t fast_fwd_t(const ReadParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, VB, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st,
-                     p);
-  return hipGetLastError();
-}
-template <class DT, int VB, int CB, int NB, int RHC>
-static hipError_t fast_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((lr_bwd_fast_kernel<DT, VB, CB, NB, RHC>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds, st,
-                     p);
-  return hipGetLastError();
-}
-
-// L.vec = value vector bytes (16), L.wpt = columns per item (1/2),
-// L.nmax = source slots (8/16/32; also 12/14/20/24 for one column and two key
-// chunks), L.teams = key chunks per head slot (2/8)
-#define ATTNRES_FAST_SWITCH(fn, P)                        \
-  switch (L.vec * 10000 + L.wpt * 1000 + L.nmax * 10 + L.teams) { \
-    case 161082: return fn<DT, 16, 1, 8, 2>(P, L, st);    \
-    case 161122: return fn<DT, 16, 1, 12, 2>(P, L, st);   \
-    case 161142: return fn<DT, 16, 1, 14, 2>(P, L, st);   \
-    case 161162: return fn<DT, 16, 1, 16, 2>(P, L, st);   \
-    case 161202: return fn<DT, 16, 1, 20, 2>(P, L, st);   \
-    case 161242: return fn<DT, 16, 1, 24, 2>(P, L, st);   \
-    case 161322: return fn<DT, 16, 1, 32, 2>(P, L, st);   \
-    case 161088: return fn<DT, 16, 1, 8, 8>(P, L, st);    \
-    case 161168: return fn<DT, 16, 1, 16, 8>(P, L, st);   \
-    case 162082: return fn<DT, 16, 2, 8, 2>(P, L, st);    \
-    case 162162: return fn<DT, 16, 2, 16, 2>(P, L, st);   \
-    case 162088: return fn<DT, 16, 2, 8, 8>(P, L, st);    \
-    default: return hipErrorInvalidValue;                 \
+// Launch switch shared by the forward and backward translation units:
+// L.vec = value vector bytes (16), L.wpt = columns per item (1/2), L.nmax =
+// source slots (8/16/32; also 12/14/20/24 for one column and two key chunks),
+// L.teams = key chunks per head slot (2/8); LEANV is the LEAN flag.
+#define ATTNRES_FAST_SWITCH(fn, P, LEANV)                            \
+  switch (L.vec * 10000 + L.wpt * 1000 + L.nmax * 10 + L.teams) {     \
+    case 161082: return fn<DT, 16, 1, 8, 2, LEANV>(P, L, st);        \
+    case 161122: return fn<DT, 16, 1, 12, 2, LEANV>(P, L, st);       \
+    case 161142: return fn<DT, 16, 1, 14, 2, LEANV>(P, L, st);       \
+    case 161162: return fn<DT, 16, 1, 16, 2, LEANV>(P, L, st);       \
+    case 161202: return fn<DT, 16, 1, 20, 2, LEANV>(P, L, st);       \
+    case 161242: return fn<DT, 16, 1, 24, 2, LEANV>(P, L, st);       \
+    case 161322: return fn<DT, 16, 1, 32, 2, LEANV>(P, L, st);       \
+    case 161088: return fn<DT, 16, 1, 8, 8, LEANV>(P, L, st);        \
+    case 161168: return fn<DT, 16, 1, 16, 8, LEANV>(P, L, st);       \
+    case 162082: return fn<DT, 16, 2, 8, 2, LEANV>(P, L, st);        \
+    case 162162: return fn<DT, 16, 2, 16, 2, LEANV>(P, L, st);       \
+    case 162088: return fn<DT, 16, 2, 8, 8, LEANV>(P, L, st);        \
+    default: return hipErrorInvalidValue;                            \
   }
-
-template <class DT>
-static hipError_t fast_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st) {
-  ATTNRES_FAST_SWITCH(fast_fwd_t, p)
-}
-template <class DT>
-static hipError_t fast_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  ATTNRES_FAST_SWITCH(fast_bwd_t, p)
-}
-
-size_t lr_fast_table_bytes() { return sizeof(SrcTab); }
-
-hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {
-  switch (dtype) {
-    case ATTNRES_DTYPE_F32: return fast_fwd_dt<F32>(p, L, st);
-    case ATTNRES_DTYPE_BF16: return fast_fwd_dt<BF16>(p, L, st);
-    default: return fast_fwd_dt<F16>(p, L, st);
-  }
-}
-hipError_t launch_lr_fast_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  switch (dtype) {
-    case ATTNRES_DTYPE_F32: return fast_bwd_dt<F32>(p, L, st);
-    case ATTNRES_DTYPE_BF16: return fast_bwd_dt<BF16>(p, L, st);
-    default: return fast_bwd_dt<F16>(p, L, st);
-  }
-}
 
 }  // namespace attnres

@@ -1,0 +1,29 @@
+// LR AttnRes read, fast path: forward launches (kernels in attnres_lr_fast.h).
+#include "attnres_lr_fast.h"
+
+namespace attnres {
+
+template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
+static hipError_t fast_fwd_t(const ReadParams& p, const Launch& L, hipStream_t st) {
+  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, VB, CB, NB, RHC, LEAN>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds,
+                     st, p);
+  return hipGetLastError();
+}
+
+template <class DT>
+static hipError_t fast_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st) {
+  if (L.lean) {
+    ATTNRES_FAST_SWITCH(fast_fwd_t, p, true)
+  }
+  ATTNRES_FAST_SWITCH(fast_fwd_t, p, false)
+}
+
+hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {
+  switch (dtype) {
+    case ATTNRES_DTYPE_F32: return fast_fwd_dt<F32>(p, L, st);
+    case ATTNRES_DTYPE_BF16: return fast_fwd_dt<BF16>(p, L, st);
+    default: return fast_fwd_dt<F16>(p, L, st);
+  }
+}
+
+}  // namespace attnres

@@ -12,8 +12,11 @@ namespace attnres {
 constexpr int kMaxSources = ATTNRES_MAX_SOURCES;
 constexpr int kWaveSize = 64;  // CDNA wavefront
 // Backward grids are capped so the per-workgroup partial sums stay small and
-// the cross-token reduction order does not depend on the device.
-constexpr int kMaxBwdGroups = 2048;
+// the cross-token reduction order does not depend on the device.  The
+// workspace holds kMaxBwdGroups rows; most backward kernels use at most
+// kFullBwdGroups workgroups, the lean fast LR backward all of them.
+constexpr int kMaxBwdGroups = 4096;
+constexpr int kFullBwdGroups = 2048;
 constexpr int kMaxFwdGroups = 65536;
 
 struct ReadParams {
@@ -54,14 +57,15 @@ struct ReadBwdParams {
   void* dkey[kMaxSources];   // [n_tok, R]
   void* dq_dyn;              // [n_tok, R]
   void* dgate;               // per-token gate gradient [n_tok, H]
-  float* partials;           // [gridDim.x, n_part]
+  float* partials;           // [gridDim.x, n_part] ([n_part, gridDim.x] from the fast LR backward)
   int32_t n_part;            // slots per workgroup: q (R or D) | gate (H) | bias (N)
   int32_t part_q, part_gate, part_bias;  // slot offsets (-1 = unused)
 };
 
 struct ReduceParams {
-  const float* partials;
+  const float* partials;      // [n_groups][n_part], or [n_part][n_groups] when slot_major
   int32_t n_groups, n_part;
+  int32_t slot_major;
   int32_t part_q, n_q;        // static query slots
   int32_t part_gate, n_gate;  // per-site gate slots
   int32_t part_bias, n_bias;

@@ -139,11 +139,11 @@ def test_host_validation_rejects_bad_descriptions_without_launching():
 def test_workspace_size_is_a_host_computation():
     lib = H.load()
     d = _desc(n_src=13, n_tok=16384, dim=1024, rank=64, heads=4)
-    # 2048 workgroups x (64 query slots) floats; no bias
-    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 2048 * 64 * 4
+    # 4096 workgroups x (64 query slots) floats; no bias
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 4096 * 64 * 4
     bias = (ctypes.c_float * 13)()
     d.logit_bias = ctypes.cast(bias, ctypes.POINTER(ctypes.c_float))
-    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 2048 * (64 + 13) * 4
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 4096 * (64 + 13) * 4
     d.n_tok = 5
     assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 5 * (64 + 13) * 4
     d.n_tok = 0
@@ -247,8 +247,8 @@ def test_phase_host_validation_rejects_bad_descriptions_without_launching():
 def test_phase2_workspace_size_is_a_host_computation():
     lib = H.load()
     d = _p2desc(n_tok=16384, dim=768)
-    # 2048 workgroups x (768 query + 1 bias + 1 value-scale slots)
-    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 2048 * 770 * 4
+    # 4096 workgroups x (768 query + 1 bias + 1 value-scale slots)
+    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 4096 * 770 * 4
     d = _p2desc(n_tok=100, dim=768, rank=64, scale_key=1)
     # LR: 64 query slots, bias, value- and key-scale slots
     assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 100 * 67 * 4
