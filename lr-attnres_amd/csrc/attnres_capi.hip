@@ -283,10 +283,12 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   return true;
 }
 
-// The fast LR kernels have LEAN instantiations without the per-token query /
-// gate and output-norm code, for reads that use neither.
-bool lr_fast_lean(const attnres_read_desc* d) {
-  return !d->query_dyn && !d->gate && !d->normalize_output;
+// Optional code the fast LR kernels must carry for a read: 0 (static query,
+// no output norm), 1 (per-token query / gate) or 3 (everything); these are
+// the instantiated sets (the kFeat* bits of attnres_lr_fast.h).
+int lr_fast_features(const attnres_read_desc* d) {
+  if (d->normalize_output) return 3;
+  return (d->query_dyn || d->gate) ? 1 : 0;
 }
 
 // token teams per LR-backward workgroup: four independent one-wave teams when a
@@ -360,7 +362,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       L.wpt = f.cb;
       L.nmax = f.nb;
       L.teams = f.rhc;
-      L.lean = lr_fast_lean(d);
+      L.feat = lr_fast_features(d);
       L.grid = (int)((f.n_items * (int64_t)p.streams + 3) / 4);
       L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float);
       err = launch_lr_fast_forward(d->dtype, p, L, st);
@@ -467,12 +469,13 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   } else if (lr) {
     FastPlan f;
     int64_t streams = 0;
-    const bool lean = lr_fast_lean(d);
+    const int feat = lr_fast_features(d);
     if (lr_fast_plan(d, pl, true, &f)) {
       // at most `groups` workgroups of four waves (the workspace rows); the
-      // full kernels (3 waves per SIMD) stream best with 2048 workgroups, the
-      // lean ones (4 per SIMD) with twice as many (measured at C3 and C4)
-      const int64_t cap = lean ? groups : (groups < kFullBwdGroups ? groups : kFullBwdGroups);
+      // instantiations with all optional code (fewer waves per SIMD) stream
+      // best with 2048 workgroups, the leaner ones with twice as many
+      // (measured at C3 and C4)
+      const int64_t cap = feat != 3 ? groups : (groups < kFullBwdGroups ? groups : kFullBwdGroups);
       streams = 4 * cap / f.n_items;
       if (streams > d->n_tok) streams = d->n_tok;
     }
@@ -487,7 +490,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       L.wpt = f.cb;
       L.nmax = f.nb;
       L.teams = f.rhc;
-      L.lean = lean;
+      L.feat = feat;
       L.grid = (int)((f.n_items * streams + 3) / 4);
       L.lds = lr_fast_table_bytes() +
               ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *

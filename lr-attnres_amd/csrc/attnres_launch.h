@@ -16,7 +16,7 @@ struct Launch {
   int nmax;     // base read: register-resident source slots (8/16; more = streaming)
   int teams;    // token teams per workgroup (LR backward; phase 2: waves per workgroup)
   int vb;       // vector bytes (16 or 8) where a kernel family has both layouts
-  int lean;     // LR fast path: no per-token query / gate and no output norm
+  int feat;     // LR fast path: optional code the kernel carries (kFeat* bits of attnres_lr_fast.h)
 };
 
 hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);

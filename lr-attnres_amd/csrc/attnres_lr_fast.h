@@ -37,9 +37,12 @@ namespace attnres {
 
 constexpr int kFastWaves = 4;  // waves per workgroup (independent token streams)
 
-// LEAN instantiations drop the per-token query / gate and output-norm code at
-// compile time (the host picks them when a read has neither): the static-query
-// backward then fits 4 waves per SIMD instead of 3.
+// FEAT selects at compile time which optional code an instantiation carries:
+// kFeatDyn = per-token query and gate, kFeatNorm = output norm.  The host picks
+// the smallest set a read needs (0, kFeatDyn, or all): without them the
+// static-query backward fits 4 waves per SIMD instead of 3, and the gated one
+// 3 instead of 2.
+constexpr int kFeatDyn = 1, kFeatNorm = 2, kFeatAll = 3;
 
 // per-source tables in LDS
 struct SrcTab {
@@ -175,7 +178,7 @@ __device__ __forceinline__ float key_query_dot(const KeySlice<DT, RHC>& kr, cons
 }
 
 // ============================================================== forward
-template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
+template <class DT, int VB, int CB, int NB, int RHC, int FEAT>
 __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   using S = typename DT::S;
   constexpr int E = VB / (int)sizeof(S);        // value elements per lane vector
@@ -217,7 +220,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   const int ph = h0 + (lh < nh ? lh : 0);
   const int ps = has_pair ? lsrc : 0;
   const int kch = p.kch;
-  const bool dyn = !LEAN && p.q_dyn != nullptr;
+  const bool dyn = (FEAT & kFeatDyn) && p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
   const uint64_t kbase = tab->kptr[ps] + (uint64_t)(ph * rh) * sizeof(S);
   const uint32_t kstrb = tab->kstrb[ps];
@@ -338,7 +341,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
       }
 
     // ---- stores
-    if (!LEAN && p.norm_out) {  // one item covers the whole row here
+    if ((FEAT & kFeatNorm) && p.norm_out) {  // one item covers the whole row here
       if (p.out_prenorm) {
         S* xp = global_ptr<S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
@@ -361,7 +364,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
 }
 
 // ============================================================== backward
-template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
+template <class DT, int VB, int CB, int NB, int RHC, int FEAT>
 __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp) {
   using S = typename DT::S;
   constexpr int E = VB / (int)sizeof(S);
@@ -407,7 +410,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   const int ph = h0 + (lh < nh ? lh : 0);
   const int ps = has_pair ? lsrc : 0;
   const int kch = p.kch;
-  const bool dyn = !LEAN && p.q_dyn != nullptr;
+  const bool dyn = (FEAT & kFeatDyn) && p.q_dyn != nullptr;
   const bool has_static = p.q_static != nullptr;
   // query-gradient owner lanes: (head h0 + lane / rh, element lane % rh)
   const int nq = nh * rh;
@@ -465,7 +468,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
     for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gp + eoff[c], gr[c]);
     Raw<DT, E> xr[CB];
-    if (!LEAN && p.norm_out) {
+    if ((FEAT & kFeatNorm) && p.norm_out) {
       const S* xp = global_ptr<const S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(xp + eoff[c], xr[c]);
@@ -491,7 +494,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     }
 
     // ---- upstream gradient through the output norm (item = whole row)
-    if (!LEAN && p.norm_out) {
+    if ((FEAT & kFeatNorm) && p.norm_out) {
       float dot = 0.f;
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
@@ -676,21 +679,21 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 // Launch switch shared by the forward and backward translation units:
 // L.vec = value vector bytes (16), L.wpt = columns per item (1/2), L.nmax =
 // source slots (8/16/32; also 12/14/20/24 for one column and two key chunks),
-// L.teams = key chunks per head slot (2/8); LEANV is the LEAN flag.
-#define ATTNRES_FAST_SWITCH(fn, P, LEANV)                            \
+// L.teams = key chunks per head slot (2/8); FEATV is the FEAT set.
+#define ATTNRES_FAST_SWITCH(fn, P, FEATV)                            \
   switch (L.vec * 10000 + L.wpt * 1000 + L.nmax * 10 + L.teams) {     \
-    case 161082: return fn<DT, 16, 1, 8, 2, LEANV>(P, L, st);        \
-    case 161122: return fn<DT, 16, 1, 12, 2, LEANV>(P, L, st);       \
-    case 161142: return fn<DT, 16, 1, 14, 2, LEANV>(P, L, st);       \
-    case 161162: return fn<DT, 16, 1, 16, 2, LEANV>(P, L, st);       \
-    case 161202: return fn<DT, 16, 1, 20, 2, LEANV>(P, L, st);       \
-    case 161242: return fn<DT, 16, 1, 24, 2, LEANV>(P, L, st);       \
-    case 161322: return fn<DT, 16, 1, 32, 2, LEANV>(P, L, st);       \
-    case 161088: return fn<DT, 16, 1, 8, 8, LEANV>(P, L, st);        \
-    case 161168: return fn<DT, 16, 1, 16, 8, LEANV>(P, L, st);       \
-    case 162082: return fn<DT, 16, 2, 8, 2, LEANV>(P, L, st);        \
-    case 162162: return fn<DT, 16, 2, 16, 2, LEANV>(P, L, st);       \
-    case 162088: return fn<DT, 16, 2, 8, 8, LEANV>(P, L, st);        \
+    case 161082: return fn<DT, 16, 1, 8, 2, FEATV>(P, L, st);        \
+    case 161122: return fn<DT, 16, 1, 12, 2, FEATV>(P, L, st);       \
+    case 161142: return fn<DT, 16, 1, 14, 2, FEATV>(P, L, st);       \
+    case 161162: return fn<DT, 16, 1, 16, 2, FEATV>(P, L, st);       \
+    case 161202: return fn<DT, 16, 1, 20, 2, FEATV>(P, L, st);       \
+    case 161242: return fn<DT, 16, 1, 24, 2, FEATV>(P, L, st);       \
+    case 161322: return fn<DT, 16, 1, 32, 2, FEATV>(P, L, st);       \
+    case 161088: return fn<DT, 16, 1, 8, 8, FEATV>(P, L, st);        \
+    case 161168: return fn<DT, 16, 1, 16, 8, FEATV>(P, L, st);       \
+    case 162082: return fn<DT, 16, 2, 8, 2, FEATV>(P, L, st);        \
+    case 162162: return fn<DT, 16, 2, 16, 2, FEATV>(P, L, st);       \
+    case 162088: return fn<DT, 16, 2, 8, 8, FEATV>(P, L, st);        \
     default: return hipErrorInvalidValue;                            \
   }
 

@@ -3,19 +3,22 @@
 
 namespace attnres {
 
-template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
+template <class DT, int VB, int CB, int NB, int RHC, int FEAT>
 static hipError_t fast_bwd_t(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((lr_bwd_fast_kernel<DT, VB, CB, NB, RHC, LEAN>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds,
+  hipLaunchKernelGGL((lr_bwd_fast_kernel<DT, VB, CB, NB, RHC, FEAT>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds,
                      st, p);
   return hipGetLastError();
 }
 
 template <class DT>
 static hipError_t fast_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t st) {
-  if (L.lean) {
-    ATTNRES_FAST_SWITCH(fast_bwd_t, p, true)
+  if (L.feat == 0) {
+    ATTNRES_FAST_SWITCH(fast_bwd_t, p, 0)
   }
-  ATTNRES_FAST_SWITCH(fast_bwd_t, p, false)
+  if (L.feat == kFeatDyn) {
+    ATTNRES_FAST_SWITCH(fast_bwd_t, p, kFeatDyn)
+  }
+  ATTNRES_FAST_SWITCH(fast_bwd_t, p, kFeatAll)
 }
 
 size_t lr_fast_table_bytes() { return sizeof(SrcTab); }

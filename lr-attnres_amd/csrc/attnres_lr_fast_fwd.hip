@@ -3,19 +3,22 @@
 
 namespace attnres {
 
-template <class DT, int VB, int CB, int NB, int RHC, bool LEAN>
+template <class DT, int VB, int CB, int NB, int RHC, int FEAT>
 static hipError_t fast_fwd_t(const ReadParams& p, const Launch& L, hipStream_t st) {
-  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, VB, CB, NB, RHC, LEAN>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds,
+  hipLaunchKernelGGL((lr_fwd_fast_kernel<DT, VB, CB, NB, RHC, FEAT>), dim3(L.grid), dim3(kFastWaves * kWave), L.lds,
                      st, p);
   return hipGetLastError();
 }
 
 template <class DT>
 static hipError_t fast_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t st) {
-  if (L.lean) {
-    ATTNRES_FAST_SWITCH(fast_fwd_t, p, true)
+  if (L.feat == 0) {
+    ATTNRES_FAST_SWITCH(fast_fwd_t, p, 0)
   }
-  ATTNRES_FAST_SWITCH(fast_fwd_t, p, false)
+  if (L.feat == kFeatDyn) {
+    ATTNRES_FAST_SWITCH(fast_fwd_t, p, kFeatDyn)
+  }
+  ATTNRES_FAST_SWITCH(fast_fwd_t, p, kFeatAll)
 }
 
 hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {
