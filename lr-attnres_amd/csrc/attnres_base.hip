@@ -348,8 +348,7 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
     float a = 0.f;
     if (regular) {
 #pragma unroll 8
-      for (int w = rl; w < rp.n_groups; w += RL)
-        a += rp.partials[rp.slot_major ? (int64_t)slot * rp.n_groups + w : (int64_t)w * rp.n_part + slot];
+      for (int w = rl; w < rp.n_groups; w += RL) a += rp.partials[part_index(rp.layout, w, slot, rp.n_groups, rp.n_part)];
     }
     sh[rl][sl] = a;
     __syncthreads();
@@ -377,8 +376,7 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
   for (int k = 0; k < rp.n_extra; ++k) {
     float b = 0.f;
     for (int w = tid; w < rp.n_groups; w += 1024) {
-      const int slot = rp.part_extra + k;
-      b += rp.partials[rp.slot_major ? (int64_t)slot * rp.n_groups + w : (int64_t)w * rp.n_part + slot];
+      b += rp.partials[part_index(rp.layout, w, rp.part_extra + k, rp.n_groups, rp.n_part)];
     }
     tree[tid] = b;
     __syncthreads();
@@ -470,8 +468,11 @@ static hipError_t reduce_dt(const ReduceParams& rp, hipStream_t st) {
   const int extra = rp.n_extra > 0 ? 1 : 0;
   // slot-major partials: one workgroup per slot reads that slot's rows as one
   // contiguous run
-  if (rp.slot_major && rp.n_part <= 1024)
+  if (rp.layout == kPartSlotMajor && rp.n_part <= 1024)
     hipLaunchKernelGGL((reduce_partials_kernel<DT, 1>), dim3(rp.n_part + extra), dim3(1024), 0, st, rp);
+  else if (rp.layout == kPartTiled)
+    hipLaunchKernelGGL((reduce_partials_kernel<DT, kPartTile>), dim3((rp.n_part + kPartTile - 1) / kPartTile + extra),
+                       dim3(1024), 0, st, rp);
   else if (rp.n_part <= 512)
     hipLaunchKernelGGL((reduce_partials_kernel<DT, 8>), dim3((rp.n_part + 7) / 8 + extra), dim3(1024), 0, st, rp);
   else if (rp.n_part <= 2048)

@@ -518,7 +518,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     rp.partials = bp.partials;
     rp.n_groups = L.grid;
     rp.n_part = PL.n_part;
-    rp.slot_major = fast ? 1 : 0;
+    rp.layout = fast ? kPartSlotMajor : kPartRowMajor;
     rp.part_q = PL.part_q;
     rp.n_q = PL.n_q;
     rp.part_gate = PL.part_gate;
@@ -835,7 +835,8 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
 extern "C" size_t attnres_phase2_backward_workspace_size(const attnres_phase2_desc* d) {
   if (check_phase2(d) != ATTNRES_OK || d->n_tok == 0) return 0;
   const P2Layout PL = phase2_layout(d, true, true, true);
-  return (size_t)bwd_groups(d->n_tok) * PL.n_part * sizeof(float);
+  if (PL.n_part == 0) return 0;
+  return (size_t)bwd_groups(d->n_tok) * part_stride(PL.n_part) * sizeof(float);
 }
 
 extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, void* stream) {
@@ -907,7 +908,7 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
   const P2Layout PL = phase2_layout(d, g->dquery != nullptr, g->dlogit_bias != nullptr, g->dvalue_scale != nullptr);
   const int64_t groups = bwd_groups(d->n_tok);
   if (PL.n_part > 0) {
-    const size_t need = (size_t)groups * PL.n_part * sizeof(float);
+    const size_t need = (size_t)groups * part_stride(PL.n_part) * sizeof(float);
     if (!g->workspace || g->workspace_bytes < need)
       return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
                   g->workspace ? g->workspace_bytes : (size_t)0);
@@ -945,6 +946,7 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     rp.partials = p.partials;
     rp.n_groups = L.grid;
     rp.n_part = PL.n_part;
+    rp.layout = L.teams > 0 ? kPartTiled : kPartRowMajor;  // wave kernels write tiles
     rp.part_q = PL.part_q;
     rp.n_q = PL.n_q;
     rp.part_gate = -1;

@@ -62,10 +62,24 @@ struct ReadBwdParams {
   int32_t part_q, part_gate, part_bias;  // slot offsets (-1 = unused)
 };
 
+// Layouts of the per-workgroup partial sums (workgroup w, slot i):
+//   row-major   [w][i]
+//   slot-major  [i][w]                     (few slots: one reduction workgroup per slot)
+//   tiled       [i / 16][w][i % 16]        (many slots: 64-byte runs both ways)
+constexpr int kPartRowMajor = 0, kPartSlotMajor = 1, kPartTiled = 2;
+constexpr int kPartTile = 16;
+__host__ __device__ inline int64_t part_index(int layout, int64_t w, int i, int n_groups, int n_part) {
+  if (layout == kPartSlotMajor) return (int64_t)i * n_groups + w;
+  if (layout == kPartTiled) return ((int64_t)(i / kPartTile) * n_groups + w) * kPartTile + i % kPartTile;
+  return w * n_part + i;
+}
+// slots per workgroup row in the workspace (tiled rows are padded to whole tiles)
+__host__ __device__ inline int part_stride(int n_part) { return (n_part + kPartTile - 1) / kPartTile * kPartTile; }
+
 struct ReduceParams {
-  const float* partials;      // [n_groups][n_part], or [n_part][n_groups] when slot_major
+  const float* partials;      // layout: kPart*
   int32_t n_groups, n_part;
-  int32_t slot_major;
+  int32_t layout;
   int32_t part_q, n_q;        // static query slots
   int32_t part_gate, n_gate;  // per-site gate slots
   int32_t part_bias, n_bias;

@@ -953,11 +953,11 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
     }
   }
   __syncthreads();
-  float* row = p.partials + (int64_t)blockIdx.x * p.n_part;
+  // tiled partials: 16 consecutive slots of this workgroup are one 64-byte run
   for (int i = threadIdx.x; i < p.n_part; i += blockDim.x) {
     float t = 0.f;
     for (int w2 = 0; w2 < wpb; ++w2) t += smem[w2 * p.n_part + i];
-    row[i] = t;
+    p.partials[part_index(kPartTiled, blockIdx.x, i, gridDim.x, p.n_part)] = t;
   }
 }
 

@@ -247,11 +247,11 @@ def test_phase_host_validation_rejects_bad_descriptions_without_launching():
 def test_phase2_workspace_size_is_a_host_computation():
     lib = H.load()
     d = _p2desc(n_tok=16384, dim=768)
-    # 4096 workgroups x (768 query + 1 bias + 1 value-scale slots)
-    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 4096 * 770 * 4
+    # 4096 workgroups x (768 query + 1 bias + 1 value-scale slots), rows padded to tiles of 16 slots
+    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 4096 * 784 * 4
     d = _p2desc(n_tok=100, dim=768, rank=64, scale_key=1)
-    # LR: 64 query slots, bias, value- and key-scale slots
-    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 100 * 67 * 4
+    # LR: 64 query slots, bias, value- and key-scale slots (67, padded to 80)
+    assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 100 * 80 * 4
     d = _p2desc(n_tok=0, dim=768)
     assert lib.attnres_phase2_backward_workspace_size(ctypes.byref(d)) == 0
 
