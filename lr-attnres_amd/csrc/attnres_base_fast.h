@@ -1,0 +1,400 @@
+// Base AttnRes read (keys = rms_norm of the full values), fast path for 16-bit
+// rows that one wave covers exactly: D = 64 lanes x CB columns x one VB-byte
+// vector (256 / 768 with 8-byte vectors, 512 / 1024 with 16-byte ones).
+//
+// Numerics are those of the step-by-step kernels (the reference's eager op,
+// which the oracle restates): the forward scores the dtype-rounded key
+// rnd(v * inv) (inv = 1/sqrt(<v, v>/D + eps), IEEE), rounds the logit and mixes
+// with dtype-rounded weights; the backward rounds dW, the logit gradient ge,
+// rnd(ge q), the rms-norm gradient and rnd(w g) where the eager op does.  The
+// speed comes from doing the same arithmetic in fewer instructions: row dot
+// products and the mix as v_dot2 on packed 16-bit words, the query-gradient
+// products of two sources as one v_dot2 with (ge_0, ge_1), rnd(a) + rnd(b) as
+// one v_cvt_pk + one v_dot2 with (1, 1), the per-source scalars (inverse rms,
+// softmax) computed once per lane instead of once per source in every lane,
+// and many row sums folded together by wave_sums.  The step-by-step kernels
+// at d=768 spent about twice the token's HBM time in VALU work.
+//
+// Work layout as in the fast LR kernels: four independent one-wave token
+// streams per workgroup, per-source row tables in LDS read as scalars, every
+// load of a token issued before any arithmetic, stores last, non-temporal
+// policy on the row streams.  Source slots past n_src repeat the last source
+// (their rows are cache hits and their values are never used), so the loads
+// over NB slots carry no branches.
+#pragma once
+
+#include "attnres_device.h"
+#include "attnres_launch.h"
+#include "attnres_lr_fast.h"
+#include "attnres_params.h"
+
+namespace attnres {
+
+// this lane's words of the static query (dtype-exact, packed two per word)
+template <class DT, int VB, int CB>
+__device__ __forceinline__ void base_fast_query(const ReadParams& p, int lane, uint32_t (&qw)[CB][VB / 4]) {
+  using S = typename DT::S;
+  constexpr int E = VB / (int)sizeof(S);
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    Raw<DT, E> r;
+    load_raw<DT, E>((const S*)p.q_static + (c * kWave + lane) * E, r);
+#pragma unroll
+    for (int i = 0; i < VB / 4; ++i) qw[c][i] = r.w[i];
+  }
+}
+
+template <class DT, int VB, int CB, int NB, bool KN>
+__global__ void __launch_bounds__(256) base_fwd_fast_kernel(const ReadParams p) {
+  using S = typename DT::S;
+  constexpr int E = VB / (int)sizeof(S);
+  constexpr int W = VB / 4;
+  constexpr int NP = NB <= 4 ? 4 : NB <= 8 ? 8 : 16;  // lanes of the softmax group
+  extern __shared__ float smem[];
+  SrcTab* tab = (SrcTab*)smem;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wslot = uniform_i32(threadIdx.x / kWave);
+  const int N = p.n_src;
+  for (int i = threadIdx.x; i < kMaxSources; i += blockDim.x) {
+    const int j = min(i, N - 1);
+    tab->vptr[i] = (uint64_t)p.val[j];
+    tab->vstrb[i] = (uint32_t)p.vstride[j] * (uint32_t)sizeof(S);
+  }
+  __syncthreads();
+  uint32_t qw[CB][W];
+  base_fast_query<DT, VB, CB>(p, lane, qw);
+
+  const int64_t t0 = (int64_t)blockIdx.x * kFastWaves + wslot;
+  for (int64_t tok = t0 < p.streams ? t0 : p.n_tok; tok < p.n_tok; tok += p.streams) {
+    Raw<DT, E> vr[NB][CB];
+    {
+      uint64_t base[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, tok);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+#pragma unroll
+        for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
+      }
+    }
+    // ---- <v, v> of every slot -> lane s holds source s's inverse rms
+    float inv[NB];
+    if constexpr (KN) {
+      float ssp[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+          for (int i = 0; i < W; ++i) ss = dot2<DT>(vr[s][c].w[i], vr[s][c].w[i], ss);
+        ssp[s] = ss;
+      }
+      float z[NB / 4];
+      wave_sums<NB>(ssp, z);
+      float mine = 0.f;
+#pragma unroll
+      for (int s = 0; s < NB; ++s)
+        if (lane == s) mine = wave_sums_get<NB>(z, s);
+      const float inv_l = 1.0f / sqrtf(mine / (float)p.D + p.eps);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) inv[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l), s));
+    }
+    // ---- logits <rnd(v * inv), q> (or <v, q>) -> lane s holds source s's logit
+    float tp[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      float t = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        if constexpr (KN) {
+          float v[E];
+          unpack<DT, E>(vr[s][c], v);
+#pragma unroll
+          for (int i = 0; i < W; ++i) t = dot2<DT>(pack2<DT>(v[2 * i] * inv[s], v[2 * i + 1] * inv[s]), qw[c][i], t);
+        } else {
+#pragma unroll
+          for (int i = 0; i < W; ++i) t = dot2<DT>(vr[s][c].w[i], qw[c][i], t);
+        }
+      }
+      tp[s] = t;
+    }
+    float z[NB / 4];
+    wave_sums<NB>(tp, z);
+    float lg = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NB; ++s)
+      if (lane == s && s < N) lg = DT::rnd(wave_sums_get<NB>(z, s)) + (p.bias ? p.bias[s] : 0.f);
+    // ---- softmax across lanes 0..NB-1
+    const float mx = group_max(lg, NP);
+    const float ex = lane < N ? expf(lg - mx) : 0.f;
+    const float pw = ex / group_sum(ex, NP);
+    if (p.weights && lane < N) p.weights[tok * N + lane] = pw;
+    // dtype-rounded weights, two sources per word (spare slots weigh 0)
+    const uint32_t wb = lane < N ? bits16<DT>(DT::rnd(pw)) : 0u;
+    uint32_t wp[NB / 2];
+#pragma unroll
+    for (int j = 0; j < NB / 2; ++j)
+      wp[j] = (uint32_t)__builtin_amdgcn_readlane((int)wb, 2 * j) |
+              ((uint32_t)__builtin_amdgcn_readlane((int)wb, 2 * j + 1) << 16);
+    // ---- mix: one v_dot2 per element and source pair
+    float acc[CB][E];
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[c][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB / 2; ++j) {
+      if (2 * j < N) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            acc[c][2 * i] = dot2<DT>(lo_pair(vr[2 * j][c].w[i], vr[2 * j + 1][c].w[i]), wp[j], acc[c][2 * i]);
+            acc[c][2 * i + 1] = dot2<DT>(hi_pair(vr[2 * j][c].w[i], vr[2 * j + 1][c].w[i]), wp[j], acc[c][2 * i + 1]);
+          }
+      }
+    }
+    S* op = global_ptr<S>((uint64_t)p.out) + tok * (int64_t)p.D;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) store_vec<DT, E, true>(op + (c * kWave + lane) * E, acc[c]);
+  }
+}
+
+template <class DT, int VB, int CB, int NB, bool KN>
+__global__ void __launch_bounds__(256) base_bwd_fast_kernel(const ReadBwdParams bp) {
+  using S = typename DT::S;
+  constexpr int E = VB / (int)sizeof(S);
+  constexpr int W = VB / 4;
+  const ReadParams& p = bp.f;
+  extern __shared__ float smem[];
+  SrcTab* tab = (SrcTab*)smem;
+  float* s_fold = smem + kSrcTabFloats;  // [waves][n_part]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wslot = uniform_i32(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int N = p.n_src, D = p.D;
+  const uint32_t rowb = (uint32_t)D * (uint32_t)sizeof(S);
+  for (int i = threadIdx.x; i < kMaxSources; i += blockDim.x) {
+    const int j = min(i, N - 1);
+    tab->vptr[i] = (uint64_t)p.val[j];
+    tab->vstrb[i] = (uint32_t)p.vstride[j] * (uint32_t)sizeof(S);
+    tab->dvptr[i] = (uint64_t)bp.dval[j];
+  }
+  __syncthreads();
+  uint32_t qw[CB][W];
+  base_fast_query<DT, VB, CB>(p, lane, qw);
+  float qacc[CB][E];
+#pragma unroll
+  for (int c = 0; c < CB; ++c)
+#pragma unroll
+    for (int e = 0; e < E; ++e) qacc[c][e] = 0.f;
+  float bacc = 0.f;  // bias slot `lane` (lane < N)
+
+  const int64_t t0 = (int64_t)blockIdx.x * kFastWaves + wslot;
+  for (int64_t tok = t0 < p.streams ? t0 : p.n_tok; tok < p.n_tok; tok += p.streams) {
+    Raw<DT, E> gr[CB];
+    Raw<DT, E> vr[NB][CB];
+    {
+      const S* gp = global_ptr<const S>(row_addr((uint64_t)bp.gout, tok, rowb));
+#pragma unroll
+      for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gp + (c * kWave + lane) * E, gr[c]);
+      uint64_t base[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, tok);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+#pragma unroll
+        for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
+      }
+    }
+    const float* wrow = bp.saved_w + tok * N;
+    float pw[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) pw[s] = wrow[min(s, N - 1)];
+    // ---- stage 1: <g, v> and <v, v> of every slot, summed over the wave
+    float part[2 * NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      float dw = 0.f, ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          dw = dot2<DT>(gr[c].w[i], vr[s][c].w[i], dw);
+          ss = dot2<DT>(vr[s][c].w[i], vr[s][c].w[i], ss);
+        }
+      part[2 * s] = dw;
+      part[2 * s + 1] = ss;
+    }
+    // per-source scalars live in scalar registers (wave-uniform)
+    float b[NB], ge[NB], mr[NB], b_l = 1.f;
+    {
+      float z[NB / 2];
+      wave_sums<2 * NB>(part, z);
+      // lane s: source s's inverse rms (IEEE, as the forward)
+      if constexpr (KN) {
+        float mine = 0.f;
+#pragma unroll
+        for (int s = 0; s < NB; ++s)
+          if (lane == s) mine = wave_sums_get<2 * NB>(z, 2 * s + 1);
+        b_l = 1.0f / sqrtf(mine / (float)D + p.eps);
+      }
+      // ---- softmax backward: dW and the logit gradient rounded like the
+      // reference's 16-bit contraction gradients
+      float wdot = 0.f;
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        part[s] = DT::rnd(wave_sums_get<2 * NB>(z, 2 * s));
+        if (s < N) wdot += pw[s] * part[s];
+      }
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        b[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b_l), s));
+        float dl = 0.f;
+        if (s < N) {
+          dl = pw[s] * (part[s] - wdot);
+          if (lane == s) bacc += dl;
+        }
+        ge[s] = uniform_f32(DT::rnd(dl));                   // 0 past N
+        pw[s] = uniform_f32(s < N ? DT::rnd(pw[s]) : 0.f);  // weight as the mix used it
+      }
+    }
+    // ---- stage 2 (key norm): m_s = <rnd(ge_s q), v_s>, mr_s = m_s inv_s / D
+    if constexpr (KN) {
+      float mp[NB];
+#pragma unroll
+      for (int s = 0; s < NB; ++s) mp[s] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        float q[E];
+        {
+          Raw<DT, E> qr;
+#pragma unroll
+          for (int i = 0; i < W; ++i) qr.w[i] = qw[c][i];
+          unpack<DT, E>(qr, q);
+        }
+#pragma unroll
+        for (int s = 0; s < NB; ++s)
+#pragma unroll
+          for (int i = 0; i < W; ++i)
+            mp[s] = dot2<DT>(pack2<DT>(ge[s] * q[2 * i], ge[s] * q[2 * i + 1]), vr[s][c].w[i], mp[s]);
+      }
+      float z2[NB / 4];
+      wave_sums<NB>(mp, z2);
+      float mine = 0.f;
+#pragma unroll
+      for (int s = 0; s < NB; ++s)
+        if (lane == s) mine = wave_sums_get<NB>(z2, s);
+      const float mr_l = mine * b_l / (float)D;
+#pragma unroll
+      for (int s = 0; s < NB; ++s) mr[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr_l), s));
+    }
+    // Stage 3 recomputes ge q rather than keeping stage 2's products (one
+    // register per element and source): the empty asm hides that they are the
+    // same values, and the barrier keeps stage 3's mr-independent half from
+    // being hoisted above the stage-2 reduction (same register cost).
+#pragma unroll
+    for (int s = 0; s < NB; ++s) asm volatile("" : "+s"(ge[s]));
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- stage 3, per column, two sources at a time:
+    //   dv  = rnd(rnd(w g) + dvk),  dvk = rnd(inv (rnd(ge q) - v inv mr))  (key norm; else rnd(ge q))
+    //   dq += ge rnd(v inv)
+    // rnd(a) + rnd(b) is one v_dot2 of the packed pair with (1, 1), and the
+    // query-gradient products of a source pair one v_dot2 with (ge_0, ge_1).
+    const uint32_t one2 = DT::kCode == 1 ? 0x3f803f80u : 0x3c003c00u;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      float q[E], g[E];
+      {
+        Raw<DT, E> qr;
+#pragma unroll
+        for (int i = 0; i < W; ++i) qr.w[i] = qw[c][i];
+        unpack<DT, E>(qr, q);
+        unpack<DT, E>(gr[c], g);
+      }
+#pragma unroll
+      for (int j = 0; j < NB / 2; ++j) {
+        const int s0 = 2 * j, s1 = 2 * j + 1;
+        if (s0 < N) {
+          const uint32_t gep = uniform_u32(bits16<DT>(ge[s0]) | (bits16<DT>(ge[s1]) << 16));
+          float v0[E], v1[E], d0[E], d1[E];
+          unpack<DT, E>(vr[s0][c], v0);
+          unpack<DT, E>(vr[s1][c], v1);
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const float vb0 = KN ? v0[e] * b[s0] : v0[e];
+            const float vb1 = KN ? v1[e] * b[s1] : v1[e];
+            qacc[c][e] = dot2<DT>(pack2<DT>(vb0, vb1), gep, qacc[c][e]);
+            float dk0, dk1;
+            {
+              Raw<DT, 2> dk;
+              dk.w[0] = pack2<DT>(ge[s0] * q[e], ge[s1] * q[e]);
+              float t[2];
+              unpack<DT, 2>(dk, t);
+              dk0 = t[0];
+              dk1 = t[1];
+            }
+            if constexpr (KN) {
+              dk0 = b[s0] * (dk0 - vb0 * mr[s0]);
+              dk1 = b[s1] * (dk1 - vb1 * mr[s1]);
+            }
+            d0[e] = dot2<DT>(pack2<DT>(pw[s0] * g[e], dk0), one2, 0.f);
+            d1[e] = dot2<DT>(pack2<DT>(pw[s1] * g[e], dk1), one2, 0.f);
+          }
+          S* dvp0 = global_ptr<S>(uniform_u64(row_addr(tab->dvptr[s0], tok, rowb)));
+          store_vec<DT, E, true>(dvp0 + (c * kWave + lane) * E, d0);
+          if (s1 < N) {
+            S* dvp1 = global_ptr<S>(uniform_u64(row_addr(tab->dvptr[s1], tok, rowb)));
+            store_vec<DT, E, true>(dvp1 + (c * kWave + lane) * E, d1);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- fold the waves' accumulators into this workgroup's partial row (slot-major)
+  if (!bp.partials) return;
+  float* fold = s_fold + wslot * bp.n_part;
+  if (bp.part_q >= 0) {
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) fold[bp.part_q + (c * kWave + lane) * E + e] = qacc[c][e];
+  }
+  if (bp.part_bias >= 0 && lane < N) fold[bp.part_bias + lane] = bacc;
+  __syncthreads();
+  for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
+    float a = 0.f;
+    for (int w = 0; w < nwaves; ++w) a += s_fold[w * bp.n_part + i];
+    bp.partials[(int64_t)i * gridDim.x + blockIdx.x] = a;
+  }
+}
+
+// Launch switch: L.vb = vector bytes (8/16), L.wpt = columns (1/2/3), L.nmax =
+// source slots (4/8/12/16); KNV = rms-norm keys (compile time: the key-norm
+// code and the plain-key code are separate instantiations).
+#define ATTNRES_BASE_FAST_SWITCH(fn, P, KNV)                      \
+  switch (L.vb * 1000 + L.wpt * 100 + L.nmax) {              \
+    case 8104: return fn<DT, 8, 1, 4, KNV>(P, L, st);            \
+    case 8108: return fn<DT, 8, 1, 8, KNV>(P, L, st);            \
+    case 8112: return fn<DT, 8, 1, 12, KNV>(P, L, st);           \
+    case 8116: return fn<DT, 8, 1, 16, KNV>(P, L, st);           \
+    case 8304: return fn<DT, 8, 3, 4, KNV>(P, L, st);            \
+    case 8308: return fn<DT, 8, 3, 8, KNV>(P, L, st);            \
+    case 8312: return fn<DT, 8, 3, 12, KNV>(P, L, st);           \
+    case 8316: return fn<DT, 8, 3, 16, KNV>(P, L, st);           \
+    case 16104: return fn<DT, 16, 1, 4, KNV>(P, L, st);          \
+    case 16108: return fn<DT, 16, 1, 8, KNV>(P, L, st);          \
+    case 16112: return fn<DT, 16, 1, 12, KNV>(P, L, st);         \
+    case 16116: return fn<DT, 16, 1, 16, KNV>(P, L, st);         \
+    case 16204: return fn<DT, 16, 2, 4, KNV>(P, L, st);          \
+    case 16208: return fn<DT, 16, 2, 8, KNV>(P, L, st);          \
+    case 16212: return fn<DT, 16, 2, 12, KNV>(P, L, st);         \
+    case 16216: return fn<DT, 16, 2, 16, KNV>(P, L, st);         \
+    default: return hipErrorInvalidValue;                    \
+  }
+
+}  // namespace attnres

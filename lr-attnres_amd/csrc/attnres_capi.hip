@@ -283,6 +283,49 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   return true;
 }
 
+// Base-key fast path (attnres_base_fast.h): 16-bit rows that one wave covers
+// exactly with 8-byte (D = 256, 768) or 16-byte (D = 512, 1024) lane vectors,
+// up to 16 sources, no output norm.  vb / cb / nb = vector bytes, columns per
+// lane, source slots.
+struct BaseFastPlan {
+  int vb, cb, nb;
+};
+
+// Token streams of the fast base kernels: one resident round of waves (16 per
+// CU: four waves on each SIMD, the occupancy both kernels reach at d=768), each
+// walking tokens with that stride.  Measured at C2 (8192 tokens): one round
+// with two tokens per wave beats 8192 one-token waves (forward 18.8 vs 19.8
+// us, backward 52.9 vs 57.7 us with the reduction) and half a round.
+int64_t base_fast_streams() {
+  static const int64_t v = [] {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    return (int64_t)cus * 16;
+  }();
+  return v;
+}
+
+bool base_fast_plan(const attnres_read_desc* d, const Plan& pl, BaseFastPlan* f) {
+  if (d->mode != ATTNRES_MODE_SOFTMAX || pl.lr || !pl.vec || elem_size(d->dtype) != 2) return false;
+  if (d->normalize_output || d->n_src > 16 || !d->query) return false;
+  switch (d->dim) {
+    case 256: f->vb = 8; f->cb = 1; break;
+    case 512: f->vb = 16; f->cb = 1; break;
+    case 768: f->vb = 8; f->cb = 3; break;
+    case 1024: f->vb = 16; f->cb = 2; break;
+    default: return false;
+  }
+  // 32-bit token index and byte strides in the kernels' address math
+  if (d->n_tok > INT32_MAX) return false;
+  for (int s = 0; s < d->n_src; ++s)
+    if ((uint64_t)d->value_row_stride[s] * 2 > UINT32_MAX) return false;
+  const int N = d->n_src;
+  f->nb = N <= 4 ? 4 : N <= 8 ? 8 : N <= 12 ? 12 : 16;
+  return true;
+}
+
 // Optional code the fast LR kernels must carry for a read: 0 (static query,
 // no output norm), 1 (per-token query / gate) or 3 (everything); these are
 // the instantiated sets (the kFeat* bits of attnres_lr_fast.h).
@@ -372,8 +415,20 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       err = launch_lr_forward(d->dtype, p, L, st);
     }
   } else {
-    L.lds = (pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : (size_t)d->n_src + 32) * sizeof(float);
-    err = launch_base_forward(d->dtype, p, L, st);
+    BaseFastPlan f;
+    if (base_fast_plan(d, pl, &f)) {
+      const int64_t cap = base_fast_streams();
+      p.streams = (int32_t)(d->n_tok < cap ? d->n_tok : cap);
+      L.vb = f.vb;
+      L.wpt = f.cb;
+      L.nmax = f.nb;
+      L.grid = (int)((p.streams + 3) / 4);
+      L.lds = lr_fast_table_bytes();
+      err = launch_base_fast_forward(d->dtype, p, L, st);
+    } else {
+      L.lds = (pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : (size_t)d->n_src + 32) * sizeof(float);
+      err = launch_base_forward(d->dtype, p, L, st);
+    }
   }
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "forward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
@@ -461,7 +516,8 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     L.grid = (int)(need < full_groups ? need : full_groups);
   }
   hipStream_t st = (hipStream_t)stream;
-  bool fast = false;  // fast LR backward: partials are slot-major
+  bool fast = false;  // fast LR / base backward: partials are slot-major
+  BaseFastPlan bf;
   hipError_t err;
   if (d->mode == ATTNRES_MODE_AVERAGE) {
     L.lds = 32 * sizeof(float);
@@ -503,6 +559,20 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
         return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS (limit %zu)", L.lds, lds_limit());
       err = launch_lr_backward(d->dtype, bp, L, st);
     }
+  } else if (base_fast_plan(d, pl, &bf)) {
+    // four token streams per workgroup, one resident round of waves and at
+    // most `groups` workgroups (the workspace rows); partials slot-major like
+    // the fast LR backward
+    fast = true;
+    const int64_t cap = groups * 4 < base_fast_streams() ? groups * 4 : base_fast_streams();
+    bp.f.streams = (int32_t)(d->n_tok < cap ? d->n_tok : cap);
+    L.vb = bf.vb;
+    L.wpt = bf.cb;
+    L.nmax = bf.nb;
+    L.grid = (int)((bp.f.streams + 3) / 4);
+    L.lds = lr_fast_table_bytes() + 4 * (size_t)PL.n_part * sizeof(float);
+    if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "base backward needs %zu bytes of LDS", L.lds);
+    err = launch_base_fast_backward(d->dtype, bp, L, st);
   } else {
     size_t fl = pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : 2 * (size_t)d->n_src + 32;
     if ((size_t)L.teams * PL.n_part > fl) fl = (size_t)L.teams * PL.n_part;

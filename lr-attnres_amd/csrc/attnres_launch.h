@@ -31,6 +31,11 @@ hipError_t launch_reduce_partials(int dtype, const ReduceParams& p, hipStream_t 
 hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_lr_fast_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
 size_t lr_fast_table_bytes();  // LDS bytes of the fast kernels' per-source tables
+// base-key fast path (one wave per token, 16-bit rows of 256 / 512 / 768 / 1024):
+// L.vb = vector bytes (8/16), L.wpt = columns per lane, L.nmax = source slots
+// (4/8/12/16); per-source tables in the first lr_fast_table_bytes() of LDS
+hipError_t launch_base_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_base_fast_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
 // cached-logit phases: L.wpt = waves per workgroup; phase-1 backward L.nmax =
 // register slots for the read sites (4, 8 or 16); phase-2 L.nmax = 1 for LR keys
 hipError_t launch_phase1_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);

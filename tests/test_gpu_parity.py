@@ -235,6 +235,44 @@ def test_base_shapes(S, D):
     _base_case(700 + S, torch.bfloat16, 1, 5, D, S, True)
 
 
+@pytest.mark.parametrize("S,D,dtype,key_norm,bias", [
+    (2, 768, torch.bfloat16, True, False), (3, 512, torch.bfloat16, True, True),
+    (4, 1024, torch.float16, True, False), (6, 256, torch.float16, False, True),
+    (11, 768, torch.float16, True, True), (16, 1024, torch.bfloat16, True, False),
+    (16, 768, torch.bfloat16, False, False), (8, 512, torch.float16, True, True),
+    (12, 256, torch.bfloat16, True, False)])
+def test_base_one_wave_rows(S, D, dtype, key_norm, bias):
+    """16-bit rows one wave covers exactly (D = 256, 512, 768, 1024): every
+    column layout and slot count (4 / 8 / 12 / 16) of the one-wave base
+    kernels, with and without key norm and a learned logit bias; 74 tokens
+    leave part of the last workgroup's streams idle."""
+    b = [0.3 * ((i % 3) - 1) for i in range(S)] if bias else None
+    _base_case(900 + S + D, dtype, 2, 37, D, S, key_norm, bias=b)
+
+
+def test_base_one_wave_rows_many_tokens():
+    """More tokens than token streams (each stream walks several tokens); the
+    query gradient sums every token."""
+    g = gen(950)
+    B, T, D, S = 4, 4500, 256, 5
+    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
+    q = torch.randn(D, generator=g) * 0.1
+    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    vd = [leaf(x) for x in vals]
+    qd = leaf(q)
+    out = ops.attention_residual_read(vd, qd, True, source_counts=[1, 2, 2, 2, 1])
+    out.backward(up.to(DEV))
+    torch.cuda.synchronize()
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    qc = q.clone().requires_grad_(True)
+    ref = O.attention_residual_read_ref(vc, qc, True, source_counts=[1, 2, 2, 2, 1])
+    ref.backward(up)
+    assert_close(out, ref, torch.bfloat16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, torch.bfloat16, f"dv{s}")
+    assert_close(qd.grad, qc.grad, torch.bfloat16, "dq", reduced=True)
+
+
 def test_base_row768_fp16_norm_counts():
     """768-element 16-bit rows (three 8-byte columns per wave) with output norm and counts."""
     _base_case(805, torch.float16, 2, 4, 768, 7, True, normalize_output=True, counts=[1, 2, 2, 2, 2, 2, 2])
