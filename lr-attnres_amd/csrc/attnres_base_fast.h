@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(256) base_bwd_fast_kernel(const ReadBwdParams 
     }
   }
 
-  // ---- fold the waves' accumulators into this workgroup's partial row (slot-major)
+  // ---- fold the waves' accumulators into this workgroup's partial row
   if (!bp.partials) return;
   float* fold = s_fold + wslot * bp.n_part;
   if (bp.part_q >= 0) {
@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(256) base_bwd_fast_kernel(const ReadBwdParams 
   for (int i = threadIdx.x; i < bp.n_part; i += blockDim.x) {
     float a = 0.f;
     for (int w = 0; w < nwaves; ++w) a += s_fold[w * bp.n_part + i];
-    bp.partials[(int64_t)i * gridDim.x + blockIdx.x] = a;
+    bp.partials[part_index(bp.part_layout, blockIdx.x, i, gridDim.x, bp.n_part)] = a;
   }
 }
 

@@ -516,7 +516,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     L.grid = (int)(need < full_groups ? need : full_groups);
   }
   hipStream_t st = (hipStream_t)stream;
-  bool fast = false;  // fast LR / base backward: partials are slot-major
+  int partials_layout = kPartRowMajor;  // fast LR backward: slot-major; fast base: tiled or slot-major
   BaseFastPlan bf;
   hipError_t err;
   if (d->mode == ATTNRES_MODE_AVERAGE) {
@@ -536,7 +536,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       if (streams > d->n_tok) streams = d->n_tok;
     }
     if (streams > 0) {
-      fast = true;
+      partials_layout = kPartSlotMajor;
       bp.f.n_items = f.n_items;
       bp.f.nh = f.nh;
       bp.f.kch = f.kch;
@@ -563,7 +563,6 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     // four token streams per workgroup, one resident round of waves and at
     // most `groups` workgroups (the workspace rows); partials slot-major like
     // the fast LR backward
-    fast = true;
     const int64_t cap = groups * 4 < base_fast_streams() ? groups * 4 : base_fast_streams();
     bp.f.streams = (int32_t)(d->n_tok < cap ? d->n_tok : cap);
     L.vb = bf.vb;
@@ -572,6 +571,13 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     L.grid = (int)((bp.f.streams + 3) / 4);
     L.lds = lr_fast_table_bytes() + 4 * (size_t)PL.n_part * sizeof(float);
     if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "base backward needs %zu bytes of LDS", L.lds);
+    // D query slots per workgroup: tiles of 16 (64-byte runs) rather than
+    // slot-major rows, whose 4-byte writes to a new line per slot cost a
+    // partial-line write each (a fifth of the backward's bytes at D=768);
+    // slot-major when the padded tiles would not fit the workspace (tiny inputs)
+    partials_layout =
+        (size_t)L.grid * part_stride(PL.n_part) <= (size_t)groups * PL.n_part ? kPartTiled : kPartSlotMajor;
+    bp.part_layout = partials_layout;
     err = launch_base_fast_backward(d->dtype, bp, L, st);
   } else {
     size_t fl = pl.nmax <= 16 ? (size_t)pl.wpt * pl.nmax + 32 : 2 * (size_t)d->n_src + 32;
@@ -588,7 +594,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     rp.partials = bp.partials;
     rp.n_groups = L.grid;
     rp.n_part = PL.n_part;
-    rp.layout = fast ? kPartSlotMajor : kPartRowMajor;
+    rp.layout = partials_layout;
     rp.part_q = PL.part_q;
     rp.n_q = PL.n_q;
     rp.part_gate = PL.part_gate;

@@ -60,6 +60,7 @@ struct ReadBwdParams {
   float* partials;           // [gridDim.x, n_part] ([n_part, gridDim.x] from the fast LR backward)
   int32_t n_part;            // slots per workgroup: q (R or D) | gate (H) | bias (N)
   int32_t part_q, part_gate, part_bias;  // slot offsets (-1 = unused)
+  int32_t part_layout;       // kPart* layout of `partials` (fast base backward; the others fix theirs)
 };
 
 // Layouts of the per-workgroup partial sums (workgroup w, slot i):

@@ -250,6 +250,14 @@ def test_base_one_wave_rows(S, D, dtype, key_norm, bias):
     _base_case(900 + S + D, dtype, 2, 37, D, S, key_norm, bias=b)
 
 
+@pytest.mark.parametrize("T", [1, 3, 6])
+def test_base_one_wave_rows_few_tokens(T):
+    """One to six tokens with a logit bias: the per-workgroup partial sums
+    (768 query + 5 bias slots) fall back from 16-slot tiles to slot-major rows
+    when the padded tiles would not fit the workspace."""
+    _base_case(960 + T, torch.bfloat16, 1, T, 768, 5, True, bias=[0.2, -0.1, 0.0, 0.4, -0.3])
+
+
 def test_base_one_wave_rows_many_tokens():
     """More tokens than token streams (each stream walks several tokens); the
     query gradient sums every token."""
