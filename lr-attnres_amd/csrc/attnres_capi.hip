@@ -516,7 +516,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     L.grid = (int)(need < full_groups ? need : full_groups);
   }
   hipStream_t st = (hipStream_t)stream;
-  int partials_layout = kPartRowMajor;  // fast LR backward: slot-major; fast base: tiled or slot-major
+  int partials_layout = kPartRowMajor;  // fast LR: slot-major; fast base: tiled (slot-major for tiny inputs)
   BaseFastPlan bf;
   hipError_t err;
   if (d->mode == ATTNRES_MODE_AVERAGE) {
@@ -536,7 +536,6 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       if (streams > d->n_tok) streams = d->n_tok;
     }
     if (streams > 0) {
-      partials_layout = kPartSlotMajor;
       bp.f.n_items = f.n_items;
       bp.f.nh = f.nh;
       bp.f.kch = f.kch;
@@ -552,6 +551,9 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
               ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *
                   sizeof(float);
       if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS", L.lds);
+      // slot-major partials (R + few slots: one reduction workgroup per slot
+      // beats 16-slot tiles here, measured at C3 and C4)
+      partials_layout = kPartSlotMajor;
       err = launch_lr_fast_backward(d->dtype, bp, L, st);
     } else {
       L.lds = lr_bwd_lds(d, pl, PL.n_part);

@@ -57,10 +57,10 @@ struct ReadBwdParams {
   void* dkey[kMaxSources];   // [n_tok, R]
   void* dq_dyn;              // [n_tok, R]
   void* dgate;               // per-token gate gradient [n_tok, H]
-  float* partials;           // [gridDim.x, n_part] ([n_part, gridDim.x] from the fast LR backward)
+  float* partials;           // per-workgroup partial sums, layout part_layout (kPart*)
   int32_t n_part;            // slots per workgroup: q (R or D) | gate (H) | bias (N)
   int32_t part_q, part_gate, part_bias;  // slot offsets (-1 = unused)
-  int32_t part_layout;       // kPart* layout of `partials` (fast base backward; the others fix theirs)
+  int32_t part_layout;       // kPart* layout of `partials` (fast base backward; the fast LR backward writes slot-major, the others row-major)
 };
 
 // Layouts of the per-workgroup partial sums (workgroup w, slot i):
