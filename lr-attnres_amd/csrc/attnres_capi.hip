@@ -821,6 +821,15 @@ bool phase2_wave_plan(const attnres_phase2_desc* d, const PhasePlan& pl, P2Wave*
   return true;
 }
 
+// Base-key phase 2 with the addcmul merge on 16-bit rows one wave covers
+// exactly (D = 256, 512, 768, 1024), without the output norm: the
+// packed-arithmetic kernels of attnres_phase2_fast.hip.
+bool phase2_fast(const attnres_phase2_desc* d, const P2Wave& w) {
+  if (elem_size(d->dtype) != 2 || d->rank != 0 || d->logit_given || d->normalize_output) return false;
+  if (d->merge != ATTNRES_MERGE_ADDCMUL) return false;
+  return d->dim == kWaveSize * (w.vb / 2) * w.cb;
+}
+
 }  // namespace
 
 extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, void* out_prenorm, float* lse,
@@ -944,12 +953,15 @@ extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, v
     const int64_t wgs = (d->n_tok + kPhase2Teams - 1) / kPhase2Teams;
     L.grid = (int)(wgs < kMaxFwdGroups ? wgs : kMaxFwdGroups);
     L.lds = 0;
+    L.feat = d->key_norm ? 1 : 0;
   } else {
     L.wpt = phase2_waves(d, pl);
     L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
     L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
   }
-  hipError_t err = launch_phase2_forward(d->dtype, p, L, (hipStream_t)stream);
+  const bool fast = L.teams > 0 && phase2_fast(d, wv);
+  hipError_t err = fast ? launch_phase2_fast_forward(d->dtype, p, L, (hipStream_t)stream)
+                        : launch_phase2_forward(d->dtype, p, L, (hipStream_t)stream);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 forward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
 }
@@ -1011,12 +1023,14 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     const int64_t cap = groups < kFullBwdGroups ? groups : kFullBwdGroups;
     L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
+    L.feat = d->key_norm ? 1 : 0;
   } else {
     L.wpt = phase2_waves(d, pl);
     L.grid = (int)(groups < kFullBwdGroups ? groups : kFullBwdGroups);
     L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
   }
-  hipError_t err = launch_phase2_backward(d->dtype, p, L, st);
+  const bool fast = L.teams > 0 && phase2_fast(d, wv);
+  hipError_t err = fast ? launch_phase2_fast_backward(d->dtype, p, L, st) : launch_phase2_backward(d->dtype, p, L, st);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 backward launch failed: %s", hipGetErrorString(err));
   if (PL.n_part > 0) {
     ReduceParams rp;

@@ -42,6 +42,10 @@ hipError_t launch_phase1_forward(int dtype, const Phase1Params& p, const Launch&
 hipError_t launch_phase1_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
+// phase 2 with base keys, 16-bit rows of 256 / 512 / 768 / 1024, no output norm:
+// L.vb = vector bytes (8/16), L.wpt = columns per lane, L.feat bit 0 = key norm
+hipError_t launch_phase2_fast_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
+hipError_t launch_phase2_fast_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 // key-producer epilogue: one wave per token, L.teams waves per workgroup,
 // L.vec = 16-byte vectors for the output columns
 hipError_t launch_keyed_split_forward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);

@@ -207,6 +207,21 @@ def test_phase2_matches_oracle(dtype, variant, D, key_norm, bias, bias_tensor, n
     _check_phase2(out, grads, ref_out, ref_grads, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,key_norm,bias_tensor", [(256, True, False), (512, False, True), (768, True, True),
+                                                    (1024, True, False), (768, False, False)])
+def test_phase2_one_wave_rows(dtype, D, key_norm, bias_tensor):
+    """Base keys on 16-bit rows one wave covers exactly, no output norm: the
+    packed-arithmetic phase-2 kernels (every column layout, with and without
+    key norm); 111 tokens leave part of the last workgroup idle."""
+    t = _phase2_case(5000 + D + int(key_norm), dtype, 3, 37, D, "base")
+    m = dict(variant="base", key_norm=key_norm, bias=0.3, bias_tensor=bias_tensor, normalize_output=False,
+             scale=0.125)
+    out, grads = _phase2_hip(t, m)
+    ref_out, ref_grads = _phase2_oracle(t, m)
+    _check_phase2(out, grads, ref_out, ref_grads, dtype)
+
+
 @pytest.mark.parametrize("R", [16, 64, 128, 1024])
 def test_lrid_phase2_key_widths(R):
     t = _phase2_case(40 + R, torch.bfloat16, 1, 6, 512, "lrid", R=R)
