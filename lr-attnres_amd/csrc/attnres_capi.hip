@@ -906,6 +906,19 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   p.dlogits = dlogits;
   Launch L;
   memset(&L, 0, sizeof(L));
+  // one wave per token with packed arithmetic (attnres_phase1_fast.hip):
+  // 16-bit rows one wave covers exactly, <= 4 sites, <= 8 sources, no norm
+  if (pl.vec && elem_size(d->dtype) == 2 && !d->normalize_output && d->n_q <= 4 && d->n_src <= 8 &&
+      (d->dim == 256 || d->dim == 512 || d->dim == 768 || d->dim == 1024)) {
+    L.vb = (d->dim == 256 || d->dim == 768) ? 8 : 16;
+    L.wpt = d->dim / (kWaveSize * (L.vb / 2));
+    L.nmax = d->n_src <= 4 ? 4 : 8;
+    const int64_t streams = d->n_tok < base_fast_streams() ? d->n_tok : base_fast_streams();
+    L.grid = (int)((streams + 3) / 4);
+    hipError_t err = launch_phase1_fast_backward(d->dtype, p, L, (hipStream_t)stream);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 backward launch failed: %s", hipGetErrorString(err));
+    return ATTNRES_OK;
+  }
   L.vec = pl.vec;
   L.vb = pl.vb;
   L.wpt = pl.wpt;

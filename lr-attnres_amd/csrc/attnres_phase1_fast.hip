@@ -1,0 +1,166 @@
+// Phase 1 backward (cached-logit schedule), fast path: 16-bit rows that one
+// wave covers exactly (D = 256 / 768 with 8-byte vectors in 1 / 3 columns,
+// 512 / 1024 with 16-byte ones), at most 4 read sites and 8 sources, no output
+// norm.  Semantics are those of phase1_bwd_kernel (attnres_phase1.hip, after
+// the reference's eager op, attnres_ops.py:3956-3961):
+//   dW[q, s] = rnd(<g[q], v[s]>),  dl = w (dW - sum_s w dW) (+ glse w),
+//   dv[s]    = rnd(sum_q rnd(w[q, s]) g[q]).
+// The general kernel spends its time on fp32 multiply-adds: Q x S row dot
+// products and Q passes per value gradient, each element unpacked again.
+// Here both are v_dot2 on packed words: a dot product costs half an
+// instruction per element, and dv one v_dot2 per element and pair of sites
+// (the upstream rows are interleaved by site pairs once per token).  The
+// Q x S row sums are folded together by wave_sums.  Work layout as the other
+// one-wave kernels: four token streams per workgroup, one resident round of
+// waves, slots past n_src / n_q load a real row (the last one) and weigh 0.
+#include "attnres_device.h"
+#include "attnres_launch.h"
+#include "attnres_params.h"
+
+namespace attnres {
+
+constexpr int kP1FastWaves = 4;  // token streams (waves) per workgroup
+constexpr int kP1FastQ = 4;      // site slots
+
+template <class DT, int VB, int CB, int SB>
+__global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params p) {
+  using S = typename DT::S;
+  constexpr int E = VB / 2;
+  constexpr int W = VB / 4;
+  constexpr int QB = kP1FastQ;
+  constexpr int V = QB * SB;  // dot products per token
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = uniform_i32(threadIdx.x / kWave);
+  const int N = p.n_src, Q = p.n_q, D = p.D, np = p.np;
+  // (site, source) lane of the softmax rows: lane = q * np + s
+  const int sl = lane & (np - 1), ql = lane / np;
+  const bool own = sl < N && ql < Q;
+
+  const int64_t t0 = (int64_t)blockIdx.x * kP1FastWaves + wave;
+  for (int64_t tok = t0; tok < p.n_tok; tok += (int64_t)gridDim.x * kP1FastWaves) {
+    // ---- loads: upstream rows of the sites, value rows of the sources
+    Raw<DT, E> gr[QB][CB], vr[SB][CB];
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      const S* gp = (const S*)p.gout + ((int64_t)min(q, Q - 1) * p.n_tok + tok) * D;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gp + (c * kWave + lane) * E, gr[q][c]);
+    }
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const int j = min(s, N - 1);
+      const S* vp = (const S*)p.val[j] + tok * (int64_t)p.vstride[j];
+#pragma unroll
+      for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
+    }
+    // ---- softmax rows in the (site, source) lane layout
+    const float l = own ? load_any(p.logits, (int64_t)ql * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
+    const float lm = group_max(l, np);
+    const float ex = own ? expf(l - lm) : 0.f;
+    const float wt = ex / group_sum(ex, np);
+
+    // ---- dW[q, s] = <g[q], v[s]>: one v_dot2 per word, all Q x S sums at once
+    float part[V];
+#pragma unroll
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        float d = 0.f;
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+          for (int i = 0; i < W; ++i) d = dot2<DT>(gr[q][c].w[i], vr[s][c].w[i], d);
+        part[q * SB + s] = d;
+      }
+    float z[V / 4];
+    wave_sums<V>(part, z);
+    float dw = 0.f;
+#pragma unroll
+    for (int q = 0; q < QB; ++q)
+#pragma unroll
+      for (int s = 0; s < SB; ++s)
+        if (s < N && lane == q * np + s) dw = wave_sums_get<V>(z, q * SB + s);
+
+    // ---- logits gradient (lane (q, s)): as phase1_bwd_kernel
+    {
+      const float dwb = DT::rnd(dw);  // gradient of the dtype-rounded weights
+      const float inner = group_sum(own ? wt * dwb : 0.f, np);
+      float dl = wt * (dwb - inner);
+      if (p.glse) {
+        const float gl = own ? p.glse[(int64_t)ql * p.n_tok + tok] * wt : 0.f;
+        dl = p.ldt == ATTNRES_DTYPE_F32 ? dl + gl : round_any(round_any(dl, p.ldt) + round_any(gl, p.ldt), p.ldt);
+      } else {
+        dl = round_any(dl, p.ldt);
+      }
+      if (own) store_any(p.dlogits, ((int64_t)ql * N + sl) * p.n_tok + tok, p.ldt, dl);
+    }
+
+    // ---- dv[s] = rnd(sum_q rnd(w[q, s]) g[q]): upstream rows interleaved by
+    // site pairs (element e of sites 2k, 2k+1 in one word), weights packed
+    const uint32_t wb = own ? bits16<DT>(DT::rnd(wt)) : 0u;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int i = 0; i < W; ++i)
+#pragma unroll
+        for (int k = 0; k < QB / 2; ++k) {
+          const uint32_t a = gr[2 * k][c].w[i], b = gr[2 * k + 1][c].w[i];
+          gr[2 * k][c].w[i] = lo_pair(a, b);
+          gr[2 * k + 1][c].w[i] = hi_pair(a, b);
+        }
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      if (s < N) {
+        uint32_t wp[QB / 2];
+#pragma unroll
+        for (int k = 0; k < QB / 2; ++k)
+          wp[k] = (uint32_t)__builtin_amdgcn_readlane((int)wb, (2 * k) * np + s) |
+                  ((uint32_t)__builtin_amdgcn_readlane((int)wb, (2 * k + 1) * np + s) << 16);
+        S* dp = (S*)p.dval[s] + tok * (int64_t)D;
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+          float acc[E];
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            float lo = 0.f, hi = 0.f;
+#pragma unroll
+            for (int k = 0; k < QB / 2; ++k) {
+              lo = dot2<DT>(gr[2 * k][c].w[i], wp[k], lo);
+              hi = dot2<DT>(gr[2 * k + 1][c].w[i], wp[k], hi);
+            }
+            acc[2 * i] = lo;
+            acc[2 * i + 1] = hi;
+          }
+          store_vec<DT, E, true>(dp + (c * kWave + lane) * E, acc);
+        }
+      }
+    }
+  }
+}
+
+// L.vb = vector bytes (8/16), L.wpt = columns per lane (1/2/3), L.nmax =
+// source slots (4/8)
+template <class DT>
+static hipError_t phase1_fast_dt(const Phase1Params& p, const Launch& L, hipStream_t st) {
+  const dim3 g(L.grid), b(kP1FastWaves * kWave);
+  switch (L.vb * 100 + L.wpt * 10 + L.nmax / 4) {
+    case 811: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 1, 4>), g, b, 0, st, p); break;
+    case 812: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 1, 8>), g, b, 0, st, p); break;
+    case 831: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 3, 4>), g, b, 0, st, p); break;
+    case 832: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 3, 8>), g, b, 0, st, p); break;
+    case 1611: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 1, 4>), g, b, 0, st, p); break;
+    case 1612: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 1, 8>), g, b, 0, st, p); break;
+    case 1621: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 2, 4>), g, b, 0, st, p); break;
+    case 1622: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 2, 8>), g, b, 0, st, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_phase1_fast_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st) {
+  if (dtype == ATTNRES_DTYPE_BF16) return phase1_fast_dt<BF16>(p, L, st);
+  if (dtype == ATTNRES_DTYPE_F16) return phase1_fast_dt<F16>(p, L, st);
+  return hipErrorInvalidValue;  // 16-bit types only (the host plan never selects this path for fp32)
+}
+
+}  // namespace attnres

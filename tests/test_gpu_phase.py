@@ -92,6 +92,33 @@ def test_phase1_matches_oracle(dtype, S, Q, D, ldt, norm):
     assert_close(dl, e_dl, dtype if dtype != torch.float32 else ldt, "dlogits", reduced=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,Q,D,ldt,T", [
+    (7, 4, 768, torch.float32, 9),
+    (8, 2, 1024, torch.bfloat16, 9),
+    (2, 1, 512, torch.float16, 9),
+    (5, 3, 256, torch.float32, 9),
+    (1, 4, 768, torch.float32, 9),
+    (6, 4, 768, torch.float32, 2100),   # more tokens than token streams
+])
+def test_phase1_one_wave_rows_backward(dtype, S, Q, D, ldt, T):
+    """16-bit rows one wave covers exactly, <= 4 sites, <= 8 sources, no
+    output norm: the packed-arithmetic phase-1 backward (every column layout,
+    both source slot counts, 16-bit and fp32 logits)."""
+    g = gen(3000 + S * 31 + Q * 7 + D + T)
+    B = 2
+    values = [randn(g, (B, T, D), dtype) for _ in range(S)]
+    logits = randn(g, (Q, S, B, T), ldt, 2.0)
+    go = randn(g, (Q, B, T, D), dtype)
+    glse = randn(g, (Q, B, T), torch.float32)
+    out, lse, dv, dl = _phase1_hip(values, logits, go, glse, False)
+    e_out, e_lse, e_dv, e_dl = _phase1_oracle(values, logits, go, glse, False)
+    assert_close(out, e_out, dtype, "out")
+    for s in range(S):
+        assert_close(dv[s], e_dv[s], dtype, f"dv{s}")
+    assert_close(dl, e_dl, dtype, "dlogits", reduced=True)
+
+
 def test_phase1_unused_lse_and_strided_sources():
     # sources that are strided views (last-dim slices of a wider tensor) and a
     # backward through the output only
