@@ -830,6 +830,20 @@ bool phase2_fast(const attnres_phase2_desc* d, const P2Wave& w) {
   return d->dim == kWaveSize * (w.vb / 2) * w.cb;
 }
 
+// Phase 1 with one wave per token and packed arithmetic
+// (attnres_phase1_fast.hip): 16-bit rows one wave covers exactly, <= 4 sites,
+// <= 8 sources, no output norm.  Fills the launch geometry.
+bool phase1_fast(const attnres_phase1_desc* d, const PhasePlan& pl, Launch* L) {
+  if (!pl.vec || elem_size(d->dtype) != 2 || d->normalize_output || d->n_q > 4 || d->n_src > 8) return false;
+  if (d->dim != 256 && d->dim != 512 && d->dim != 768 && d->dim != 1024) return false;
+  L->vb = (d->dim == 256 || d->dim == 768) ? 8 : 16;
+  L->wpt = d->dim / (kWaveSize * (L->vb / 2));
+  L->nmax = d->n_src <= 4 ? 4 : 8;
+  const int64_t streams = d->n_tok < base_fast_streams() ? d->n_tok : base_fast_streams();
+  L->grid = (int)((streams + 3) / 4);
+  return true;
+}
+
 }  // namespace
 
 extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, void* out_prenorm, float* lse,
@@ -858,6 +872,11 @@ extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, v
   p.out_inv_rms = d->normalize_output ? out_inv_rms : nullptr;
   Launch L;
   memset(&L, 0, sizeof(L));
+  if (phase1_fast(d, pl, &L)) {
+    hipError_t err = launch_phase1_fast_forward(d->dtype, p, L, (hipStream_t)stream);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 forward launch failed: %s", hipGetErrorString(err));
+    return ATTNRES_OK;
+  }
   L.vec = pl.vec;
   L.vb = pl.vb;
   L.wpt = pl.wpt;
@@ -906,15 +925,7 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   p.dlogits = dlogits;
   Launch L;
   memset(&L, 0, sizeof(L));
-  // one wave per token with packed arithmetic (attnres_phase1_fast.hip):
-  // 16-bit rows one wave covers exactly, <= 4 sites, <= 8 sources, no norm
-  if (pl.vec && elem_size(d->dtype) == 2 && !d->normalize_output && d->n_q <= 4 && d->n_src <= 8 &&
-      (d->dim == 256 || d->dim == 512 || d->dim == 768 || d->dim == 1024)) {
-    L.vb = (d->dim == 256 || d->dim == 768) ? 8 : 16;
-    L.wpt = d->dim / (kWaveSize * (L.vb / 2));
-    L.nmax = d->n_src <= 4 ? 4 : 8;
-    const int64_t streams = d->n_tok < base_fast_streams() ? d->n_tok : base_fast_streams();
-    L.grid = (int)((streams + 3) / 4);
+  if (phase1_fast(d, pl, &L)) {
     hipError_t err = launch_phase1_fast_backward(d->dtype, p, L, (hipStream_t)stream);
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 backward launch failed: %s", hipGetErrorString(err));
     return ATTNRES_OK;

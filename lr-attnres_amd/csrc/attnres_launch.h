@@ -40,9 +40,10 @@ hipError_t launch_base_fast_backward(int dtype, const ReadBwdParams& p, const La
 // register slots for the read sites (4, 8 or 16); phase-2 L.nmax = 1 for LR keys
 hipError_t launch_phase1_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase1_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
-// phase-1 backward for 16-bit rows of 256 / 512 / 768 / 1024, <= 4 sites, <= 8
+// phase 1 (forward / backward) for 16-bit rows of 256 / 512 / 768 / 1024, <= 4 sites, <= 8
 // sources, no output norm: L.vb = vector bytes, L.wpt = columns per lane,
 // L.nmax = source slots (4/8); four token streams per workgroup
+hipError_t launch_phase1_fast_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase1_fast_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);

@@ -1,4 +1,4 @@
-// Phase 1 backward (cached-logit schedule), fast path: 16-bit rows that one
+// Phase 1 (cached-logit schedule) backward and forward, fast path: 16-bit rows that one
 // wave covers exactly (D = 256 / 768 with 8-byte vectors in 1 / 3 columns,
 // 512 / 1024 with 16-byte ones), at most 4 read sites and 8 sources, no output
 // norm.  Semantics are those of phase1_bwd_kernel (attnres_phase1.hip, after
@@ -138,29 +138,117 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
   }
 }
 
+// Forward on the same rows: w = softmax(logits) (fp32), lse = max + log(sum),
+// out[q] = rnd(sum_s rnd(w[q, s]) v[s]).  The value rows are interleaved by
+// source pairs once per token; each site then costs one v_dot2 per element
+// and source pair.
+template <class DT, int VB, int CB, int SB>
+__global__ void __launch_bounds__(256) phase1_fwd_fast_kernel(const Phase1Params p) {
+  using S = typename DT::S;
+  constexpr int E = VB / 2;
+  constexpr int W = VB / 4;
+  constexpr int QB = kP1FastQ;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = uniform_i32(threadIdx.x / kWave);
+  const int N = p.n_src, Q = p.n_q, D = p.D, np = p.np;
+  const int sl = lane & (np - 1), ql = lane / np;
+  const bool own = sl < N && ql < Q;
+
+  const int64_t t0 = (int64_t)blockIdx.x * kP1FastWaves + wave;
+  for (int64_t tok = t0; tok < p.n_tok; tok += (int64_t)gridDim.x * kP1FastWaves) {
+    Raw<DT, E> vr[SB][CB];
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const int j = min(s, N - 1);
+      const S* vp = (const S*)p.val[j] + tok * (int64_t)p.vstride[j];
+#pragma unroll
+      for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
+    }
+    // softmax rows and lse in the (site, source) lane layout
+    const float l = own ? load_any(p.logits, (int64_t)ql * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
+    const float lm = group_max(l, np);
+    const float ex = own ? expf(l - lm) : 0.f;
+    const float z = group_sum(ex, np);
+    if (own && sl == 0) p.lse[(int64_t)ql * p.n_tok + tok] = lm + logf(z);
+    const uint32_t wb = own ? bits16<DT>(DT::rnd(ex / z)) : 0u;
+    // value rows interleaved by source pairs
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int i = 0; i < W; ++i)
+#pragma unroll
+        for (int k = 0; k < SB / 2; ++k) {
+          const uint32_t a = vr[2 * k][c].w[i], b = vr[2 * k + 1][c].w[i];
+          vr[2 * k][c].w[i] = lo_pair(a, b);
+          vr[2 * k + 1][c].w[i] = hi_pair(a, b);
+        }
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      if (q < Q) {
+        uint32_t wp[SB / 2];
+#pragma unroll
+        for (int k = 0; k < SB / 2; ++k) {
+          const uint32_t w0 = 2 * k < N ? (uint32_t)__builtin_amdgcn_readlane((int)wb, q * np + 2 * k) : 0u;
+          const uint32_t w1 = 2 * k + 1 < N ? (uint32_t)__builtin_amdgcn_readlane((int)wb, q * np + 2 * k + 1) : 0u;
+          wp[k] = w0 | (w1 << 16);
+        }
+        S* op = (S*)p.out + ((int64_t)q * p.n_tok + tok) * D;
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+          float acc[E];
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            float lo = 0.f, hi = 0.f;
+#pragma unroll
+            for (int k = 0; k < SB / 2; ++k) {
+              if (2 * k < N) {
+                lo = dot2<DT>(vr[2 * k][c].w[i], wp[k], lo);
+                hi = dot2<DT>(vr[2 * k + 1][c].w[i], wp[k], hi);
+              }
+            }
+            acc[2 * i] = lo;
+            acc[2 * i + 1] = hi;
+          }
+          store_vec<DT, E, true>(op + (c * kWave + lane) * E, acc);
+        }
+      }
+    }
+  }
+}
+
 // L.vb = vector bytes (8/16), L.wpt = columns per lane (1/2/3), L.nmax =
 // source slots (4/8)
-template <class DT>
+template <class DT, bool BWD>
 static hipError_t phase1_fast_dt(const Phase1Params& p, const Launch& L, hipStream_t st) {
   const dim3 g(L.grid), b(kP1FastWaves * kWave);
+#define ATTNRES_P1F(VB, CB, SB)                                                                \
+  if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, VB, CB, SB>), g, b, 0, st, p); \
+  else hipLaunchKernelGGL((phase1_fwd_fast_kernel<DT, VB, CB, SB>), g, b, 0, st, p);
   switch (L.vb * 100 + L.wpt * 10 + L.nmax / 4) {
-    case 811: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 1, 4>), g, b, 0, st, p); break;
-    case 812: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 1, 8>), g, b, 0, st, p); break;
-    case 831: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 3, 4>), g, b, 0, st, p); break;
-    case 832: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 8, 3, 8>), g, b, 0, st, p); break;
-    case 1611: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 1, 4>), g, b, 0, st, p); break;
-    case 1612: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 1, 8>), g, b, 0, st, p); break;
-    case 1621: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 2, 4>), g, b, 0, st, p); break;
-    case 1622: hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, 16, 2, 8>), g, b, 0, st, p); break;
+    case 811: ATTNRES_P1F(8, 1, 4) break;
+    case 812: ATTNRES_P1F(8, 1, 8) break;
+    case 831: ATTNRES_P1F(8, 3, 4) break;
+    case 832: ATTNRES_P1F(8, 3, 8) break;
+    case 1611: ATTNRES_P1F(16, 1, 4) break;
+    case 1612: ATTNRES_P1F(16, 1, 8) break;
+    case 1621: ATTNRES_P1F(16, 2, 4) break;
+    case 1622: ATTNRES_P1F(16, 2, 8) break;
     default: return hipErrorInvalidValue;
   }
+#undef ATTNRES_P1F
   return hipGetLastError();
 }
 
+// 16-bit types only (the host plan never selects this path for fp32)
+hipError_t launch_phase1_fast_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st) {
+  if (dtype == ATTNRES_DTYPE_BF16) return phase1_fast_dt<BF16, false>(p, L, st);
+  if (dtype == ATTNRES_DTYPE_F16) return phase1_fast_dt<F16, false>(p, L, st);
+  return hipErrorInvalidValue;
+}
 hipError_t launch_phase1_fast_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st) {
-  if (dtype == ATTNRES_DTYPE_BF16) return phase1_fast_dt<BF16>(p, L, st);
-  if (dtype == ATTNRES_DTYPE_F16) return phase1_fast_dt<F16>(p, L, st);
-  return hipErrorInvalidValue;  // 16-bit types only (the host plan never selects this path for fp32)
+  if (dtype == ATTNRES_DTYPE_BF16) return phase1_fast_dt<BF16, true>(p, L, st);
+  if (dtype == ATTNRES_DTYPE_F16) return phase1_fast_dt<F16, true>(p, L, st);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace attnres
