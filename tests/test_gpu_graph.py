@@ -76,7 +76,8 @@ def test_lr_read_graph_replays_match_eager():
     _check_replays(fn, [*vals, *keys, q, up])
 
 
-def test_base_read_graph_replays_match_eager():
+@pytest.mark.parametrize("normalize_output", [True, False])  # False: the one-wave packed kernels
+def test_base_read_graph_replays_match_eager(normalize_output):
     g = gen(42)
     B, T, D, S = 2, 40, 768, 5
     dt = torch.bfloat16
@@ -85,7 +86,7 @@ def test_base_read_graph_replays_match_eager():
     up = randn(g, (B, T, D), dt).to(DEV)
 
     def fn():
-        out = ops.attention_residual_read(vals, q, True, normalize_output=True)
+        out = ops.attention_residual_read(vals, q, True, normalize_output=normalize_output)
         grads = torch.autograd.grad(out, [*vals, q], up)
         return [out.detach(), *grads]
 
