@@ -198,6 +198,44 @@ int attnres_phase1_backward(const attnres_phase1_desc* desc, const void* grad_ou
                             const void* out_prenorm, const float* out_inv_rms, void* const* dvalues,
                             void* dlogits, void* stream);
 
+/*
+ * Phase 1 from a query bank: the logits of Q queries against the keys of the
+ * S sources, after which the read is attnres_phase1_forward / _backward on
+ * those logits (logits_dtype = dtype):
+ *   key[s, t] = rms_norm(values[s][t]) rounded to dtype (or the value itself),
+ *   logits[q, s, t] = <queries[q], key[s, t]> rounded to dtype.
+ * Replaces the logits half of _attnres_phase1_forward_kernel /
+ *   _attnres_phase1_backward_kernel (attnres_ops.py:785-930) behind
+ *   attention_residual_phase1 (:3862-3907; eager form _attnres_phase1_read_torch
+ *   :2620-2627).
+ */
+typedef struct attnres_keyed_logits_desc {
+  int32_t n_src;            /* S, 1..ATTNRES_MAX_SOURCES */
+  int32_t n_q;              /* Q, 1..ATTNRES_PHASE1_MAX_QUERIES */
+  int32_t dtype;            /* values, queries, logits */
+  int64_t n_tok;
+  int32_t dim;              /* D <= ATTNRES_PHASE_MAX_DIM */
+  int32_t key_norm;
+  float norm_eps;
+  const void* const* values;       /* [S] device pointers, rows of dim elements */
+  const int64_t* value_row_stride; /* [S] elements */
+  const void* queries;             /* device [Q, dim], dtype, contiguous */
+} attnres_keyed_logits_desc;
+
+/* logits [Q, S, n_tok] (dtype); inv_rms [S, n_tok] fp32 (the keys' 1/rms, for
+ * the backward; may be NULL when none follows or without key_norm). */
+int attnres_keyed_logits_forward(const attnres_keyed_logits_desc* desc, void* logits, float* inv_rms, void* stream);
+
+/* Workspace bytes of attnres_keyed_logits_backward (host computation). */
+size_t attnres_keyed_logits_backward_workspace_size(const attnres_keyed_logits_desc* desc);
+
+/* dlogits [Q, S, n_tok] (dtype) -> dvalues[s] [n_tok, dim] dense (overwritten)
+ * and dqueries [Q, dim] (dtype; NULL: not computed, no workspace needed).
+ * inv_rms: the forward's (required with key_norm). */
+int attnres_keyed_logits_backward(const attnres_keyed_logits_desc* desc, const void* dlogits, const float* inv_rms,
+                                  void* const* dvalues, void* dqueries, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 #define ATTNRES_MERGE_ADDCMUL 0 /* inter + (partial - inter) * prob   (attnres_ops.py:2642, 4066) */
 #define ATTNRES_MERGE_LERP 1    /* torch.lerp(inter, partial, prob)   (attnres_ops.py:4159) */
 

@@ -96,6 +96,23 @@ class Phase1Desc(ctypes.Structure):
     ]
 
 
+class KeyedLogitsDesc(ctypes.Structure):
+    """attnres_keyed_logits_desc."""
+
+    _fields_ = [
+        ("n_src", c_int32),
+        ("n_q", c_int32),
+        ("dtype", c_int32),
+        ("n_tok", c_int64),
+        ("dim", c_int32),
+        ("key_norm", c_int32),
+        ("norm_eps", c_float),
+        ("values", POINTER(c_void_p)),
+        ("value_row_stride", POINTER(c_int64)),
+        ("queries", c_void_p),
+    ]
+
+
 class Phase2Desc(ctypes.Structure):
     """attnres_phase2_desc."""
 
@@ -185,6 +202,13 @@ def load() -> ctypes.CDLL:
     lib.attnres_phase1_backward.restype = c_int
     lib.attnres_phase1_backward.argtypes = [POINTER(Phase1Desc), c_void_p, POINTER(c_float), c_void_p,
                                             POINTER(c_float), POINTER(c_void_p), c_void_p, c_void_p]
+    lib.attnres_keyed_logits_forward.restype = c_int
+    lib.attnres_keyed_logits_forward.argtypes = [POINTER(KeyedLogitsDesc), c_void_p, POINTER(c_float), c_void_p]
+    lib.attnres_keyed_logits_backward_workspace_size.restype = c_size_t
+    lib.attnres_keyed_logits_backward_workspace_size.argtypes = [POINTER(KeyedLogitsDesc)]
+    lib.attnres_keyed_logits_backward.restype = c_int
+    lib.attnres_keyed_logits_backward.argtypes = [POINTER(KeyedLogitsDesc), c_void_p, POINTER(c_float),
+                                                  POINTER(c_void_p), c_void_p, c_void_p, c_size_t, c_void_p]
     lib.attnres_phase2_forward.restype = c_int
     lib.attnres_phase2_forward.argtypes = [POINTER(Phase2Desc), c_void_p, c_void_p]
     lib.attnres_phase2_backward.restype = c_int
@@ -421,6 +445,62 @@ def phase1_backward(desc: Phase1, device, dtype, logits_dtype, grad_out, grad_ls
                                      _ptr(dlog), _stream(device))
     _check(rc, "phase-1 backward")
     return dvals, dlog
+
+
+class KeyedLogits:
+    """Descriptor of the query-bank logits: S value row tensors [n_tok, D]
+    (any uniform row stride) and queries [Q, D] (value dtype, contiguous)."""
+
+    def __init__(self, values, queries, key_norm, eps=FLT_EPSILON):
+        n = len(values)
+        self._tensors = (list(values), queries)
+        self.n_src = n
+        self.n_q = queries.size(0)
+        self.n_tok = values[0].size(0)
+        self.D = values[0].size(1)
+        self._vals = (c_void_p * n)(*[t.data_ptr() for t in values])
+        self._vstr = (c_int64 * n)(*[t.stride(0) for t in values])
+        d = KeyedLogitsDesc()
+        d.n_src = n
+        d.n_q = self.n_q
+        d.dtype = DTYPE_CODE[values[0].dtype]
+        d.n_tok = self.n_tok
+        d.dim = self.D
+        d.key_norm = int(bool(key_norm))
+        d.norm_eps = float(eps)
+        d.values = self._vals
+        d.value_row_stride = self._vstr
+        d.queries = queries.data_ptr()
+        self.c = d
+
+
+def keyed_logits_forward(desc: KeyedLogits, device, dtype, for_backward: bool):
+    """Returns (logits [Q, S, n_tok] in the value dtype, inv_rms [S, n_tok] | empty)."""
+    lib = load()
+    logits = torch.empty((desc.n_q, desc.n_src, desc.n_tok), device=device, dtype=dtype)
+    keep = bool(desc.c.key_norm) and for_backward
+    inv = torch.empty((desc.n_src, desc.n_tok) if keep else (0,), device=device, dtype=torch.float32)
+    rc = lib.attnres_keyed_logits_forward(ctypes.byref(desc.c), _ptr(logits), _fptr(inv) if keep else None,
+                                          _stream(device))
+    _check(rc, "keyed-logits forward")
+    return logits, inv
+
+
+def keyed_logits_backward(desc: KeyedLogits, device, dtype, dlogits, inv_rms, want_dq: bool):
+    """Returns (dvalues list of [n_tok, D], dqueries [Q, D] | None)."""
+    lib = load()
+    n = desc.n_src
+    dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, True)
+    dv_arr = (c_void_p * n)(*[t.data_ptr() for t in dvals])
+    dq = torch.empty((desc.n_q, desc.D), device=device, dtype=dtype) if want_dq else None
+    ws_bytes = lib.attnres_keyed_logits_backward_workspace_size(ctypes.byref(desc.c)) if want_dq else 0
+    ws = torch.empty((max(1, ws_bytes),), device=device, dtype=torch.uint8) if want_dq else None
+    keep = inv_rms is not None and inv_rms.numel() > 0
+    rc = lib.attnres_keyed_logits_backward(ctypes.byref(desc.c), _ptr(dlogits), _fptr(inv_rms) if keep else None,
+                                           dv_arr, _ptr(dq) if want_dq else None, _ptr(ws) if want_dq else None,
+                                           ws_bytes, _stream(device))
+    _check(rc, "keyed-logits backward")
+    return dvals, dq
 
 
 class Phase2:

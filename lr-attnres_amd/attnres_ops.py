@@ -661,14 +661,61 @@ def attention_residual_phase1_from_logits(values, logits: Tensor, force_triton: 
     return out.view(Q, B, T, D), lse.view(Q, B, T)
 
 
-def attention_residual_phase1(values, queries: Tensor, key_norm: bool, force_triton: bool = False):
-    """Phase 1 with logits from a query bank (reference: attnres_ops.py:3862-3907).
+class _KeyedLogitsFn(torch.autograd.Function):
+    """Eager autograd of the query-bank logits: inputs (key_norm, queries [Q,D], *value rows)."""
 
-    Not used by the reference model's training path (which caches logits and
-    calls ``attention_residual_phase1_from_logits``); not implemented here.
+    @staticmethod
+    def forward(ctx, key_norm, queries, *values):
+        ctx.set_materialize_grads(False)
+        v0 = values[0]
+        desc = _hip.KeyedLogits(values, queries, key_norm)
+        with _device_ctx(v0.device):
+            logits, inv = _hip.keyed_logits_forward(desc, v0.device, v0.dtype, True)
+        ctx.desc = desc
+        ctx.save_for_backward(queries, inv, *values)
+        return logits
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dlogits):
+        saved = ctx.saved_tensors
+        queries, inv, values = saved[0], saved[1], saved[2:]
+        if dlogits is None:
+            return (None, None, *([None] * len(values)))
+        v0 = values[0]
+        want = ctx.needs_input_grad
+        with _device_ctx(v0.device):
+            dvals, dq = _hip.keyed_logits_backward(ctx.desc, v0.device, v0.dtype, dlogits.contiguous(), inv,
+                                                   bool(want[1]))
+        return (None, dq, *[d if want[2 + i] else None for i, d in enumerate(dvals)])
+
+
+def attention_residual_phase1(values, queries: Tensor, key_norm: bool, force_triton: bool = False):
+    """Phase 1 with logits from a query bank (reference: attnres_ops.py:3862-3907; eager form
+    ``_attnres_phase1_read_torch`` :2620-2627).
+
+    values: S x [B,T,D] (list or stacked [S,B,T,D]); queries [Q,D], cast to the
+    value dtype as the reference does.  The logits ``<queries[q], rms_norm(v_s)>``
+    (value dtype) come from the keyed-logits kernels; the read over them is
+    ``attention_residual_phase1_from_logits``.  Returns (out [Q,B,T,D], lse [Q,B,T]).
     """
-    raise NotImplementedError("attention_residual_phase1 (query-bank form) is not implemented in the HIP build; "
-                              "use attention_residual_phase1_from_logits")
+    srcs = _sources(values)
+    if len(srcs) == 0:
+        raise RuntimeError("Two-phase AttnRes phase1 requires at least one source")
+    _check_sources(srcs, "attention_residual_phase1")
+    B, T, D = srcs[0].shape
+    if queries.dim() != 2 or queries.size(1) != D:
+        raise RuntimeError(f"attention_residual_phase1: queries must be [Q, {D}], got {tuple(queries.shape)}")
+    Q = queries.size(0)
+    if Q < 1 or Q > _hip.PHASE1_MAX_QUERIES:
+        raise RuntimeError(f"attention_residual_phase1: 1 <= Q <= {_hip.PHASE1_MAX_QUERIES}, got {Q}")
+    if D > _hip.PHASE_MAX_DIM:
+        raise RuntimeError(f"attention_residual_phase1: D={D} exceeds {_hip.PHASE_MAX_DIM}")
+    _check_gpu(srcs + [queries], "attention_residual_phase1")
+    q = queries.to(srcs[0].dtype).contiguous()
+    rows = [_rows2d(t) for t in srcs]
+    logits = _KeyedLogitsFn.apply(bool(key_norm), q, *rows)
+    return attention_residual_phase1_from_logits(srcs, logits.view(Q, len(srcs), B, T))
 
 
 @torch.library.custom_op("attnres_hip::phase2", mutates_args=())

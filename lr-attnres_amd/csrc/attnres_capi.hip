@@ -1082,6 +1082,130 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
   return ATTNRES_OK;
 }
 
+// ---------------------------------------------------------------- query-bank logits
+namespace {
+
+constexpr int kKeyedLogitsGroups = 128;  // query-gradient partial rows (token strides)
+
+int check_keyed_logits(const attnres_keyed_logits_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->n_src < 1 || d->n_src > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_src=%d outside [1, %d]", d->n_src, ATTNRES_MAX_SOURCES);
+  if (d->n_q < 1 || d->n_q > ATTNRES_PHASE1_MAX_QUERIES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_q=%d outside [1, %d]", d->n_q, ATTNRES_PHASE1_MAX_QUERIES);
+  if (d->dtype != ATTNRES_DTYPE_F32 && d->dtype != ATTNRES_DTYPE_BF16 && d->dtype != ATTNRES_DTYPE_F16)
+    return fail(ATTNRES_EINVAL, "unknown dtype %d", d->dtype);
+  if (d->n_tok < 0) return fail(ATTNRES_EINVAL, "n_tok=%lld < 0", (long long)d->n_tok);
+  if (d->dim < 1 || d->dim > ATTNRES_PHASE_MAX_DIM)
+    return fail(ATTNRES_EUNSUPPORTED, "dim=%d outside [1, %d]", d->dim, ATTNRES_PHASE_MAX_DIM);
+  if (!d->values || !d->value_row_stride) return fail(ATTNRES_EINVAL, "values / value_row_stride is NULL");
+  const bool live = d->n_tok > 0;
+  for (int s = 0; s < d->n_src; ++s) {
+    if (live && !d->values[s]) return fail(ATTNRES_EINVAL, "values[%d] is NULL", s);
+    if (d->value_row_stride[s] < d->dim || d->value_row_stride[s] > INT32_MAX)
+      return fail(ATTNRES_EINVAL, "value_row_stride[%d]=%lld must be in [dim, 2^31)", s,
+                  (long long)d->value_row_stride[s]);
+  }
+  if (live && !d->queries) return fail(ATTNRES_EINVAL, "queries is NULL");
+  return ATTNRES_OK;
+}
+
+void fill_keyed_logits(const attnres_keyed_logits_desc* d, KeyedLogitsParams* p, Launch* L) {
+  memset(p, 0, sizeof(*p));
+  for (int s = 0; s < d->n_src; ++s) {
+    p->val[s] = d->values[s];
+    p->vstride[s] = (int32_t)d->value_row_stride[s];
+  }
+  p->queries = d->queries;
+  p->n_tok = d->n_tok;
+  p->n_src = d->n_src;
+  p->n_q = d->n_q;
+  p->D = d->dim;
+  p->key_norm = d->key_norm ? 1 : 0;
+  p->eps = d->norm_eps;
+  memset(L, 0, sizeof(*L));
+  L->wpt = (d->dim + 8 * kWaveSize - 1) / (8 * kWaveSize);  // eight elements per lane
+  L->grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
+  L->lds = (size_t)L->wpt * kKLMaxQ * sizeof(float);
+}
+
+int64_t keyed_logits_groups(int64_t n_tok) { return n_tok < kKeyedLogitsGroups ? n_tok : kKeyedLogitsGroups; }
+
+}  // namespace
+
+extern "C" int attnres_keyed_logits_forward(const attnres_keyed_logits_desc* d, void* logits, float* inv_rms,
+                                            void* stream) {
+  int rc = check_keyed_logits(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!logits) return fail(ATTNRES_EINVAL, "logits is NULL");
+  KeyedLogitsParams p;
+  Launch L;
+  fill_keyed_logits(d, &p, &L);
+  p.logits = logits;
+  p.inv = d->key_norm ? inv_rms : nullptr;
+  hipError_t err = launch_keyed_logits_forward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "keyed-logits forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" size_t attnres_keyed_logits_backward_workspace_size(const attnres_keyed_logits_desc* d) {
+  if (check_keyed_logits(d) != ATTNRES_OK || d->n_tok == 0) return 0;
+  return (size_t)keyed_logits_groups(d->n_tok) * d->n_q * d->dim * sizeof(float);
+}
+
+extern "C" int attnres_keyed_logits_backward(const attnres_keyed_logits_desc* d, const void* dlogits,
+                                             const float* inv_rms, void* const* dvalues, void* dqueries,
+                                             void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_keyed_logits(d);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (d->n_tok == 0) {
+    if (dqueries) zero_async(dqueries, (size_t)d->n_q * d->dim * elem_size(d->dtype), st);
+    return ATTNRES_OK;
+  }
+  if (!dlogits || !dvalues) return fail(ATTNRES_EINVAL, "dlogits / dvalues is NULL");
+  for (int s = 0; s < d->n_src; ++s)
+    if (!dvalues[s]) return fail(ATTNRES_EINVAL, "dvalues[%d] is NULL", s);
+  if (d->key_norm && !inv_rms) return fail(ATTNRES_EINVAL, "key_norm backward needs the forward's inv_rms");
+  KeyedLogitsParams p;
+  Launch L;
+  fill_keyed_logits(d, &p, &L);
+  for (int s = 0; s < d->n_src; ++s) p.dval[s] = dvalues[s];
+  p.dlogits = dlogits;
+  p.inv = const_cast<float*>(inv_rms);
+  const int64_t groups = keyed_logits_groups(d->n_tok);
+  if (dqueries) {
+    const size_t need = (size_t)groups * d->n_q * d->dim * sizeof(float);
+    if (!workspace || workspace_bytes < need)
+      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    p.partials = (float*)workspace;
+    p.n_part = d->n_q * d->dim;
+    L.teams = (int)groups;
+  }
+  hipError_t err = launch_keyed_logits_backward(d->dtype, p, L, st);
+  if (err != hipSuccess)
+    return fail(ATTNRES_ELAUNCH, "keyed-logits backward launch failed: %s", hipGetErrorString(err));
+  if (dqueries) {
+    ReduceParams rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.partials = p.partials;
+    rp.n_groups = (int)groups;
+    rp.n_part = p.n_part;
+    rp.layout = kPartRowMajor;
+    rp.part_q = 0;
+    rp.n_q = p.n_part;
+    rp.part_gate = -1;
+    rp.part_bias = -1;
+    rp.part_extra = -1;
+    rp.dquery = dqueries;
+    err = launch_reduce_partials(d->dtype, rp, st);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
+  }
+  return ATTNRES_OK;
+}
+
 // ---------------------------------------------------------------- key-producer epilogue
 namespace {
 

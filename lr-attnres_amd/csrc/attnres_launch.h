@@ -51,6 +51,10 @@ hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch
 // L.vb = vector bytes (8/16), L.wpt = columns per lane, L.feat bit 0 = key norm
 hipError_t launch_phase2_fast_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_fast_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
+// query-bank logits: L.grid token workgroups of L.wpt waves, L.lds = wpt *
+// kKLMaxQ floats; backward L.teams = query-gradient groups
+hipError_t launch_keyed_logits_forward(int dtype, const KeyedLogitsParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_keyed_logits_backward(int dtype, const KeyedLogitsParams& p, const Launch& L, hipStream_t st);
 // key-producer epilogue: one wave per token, L.teams waves per workgroup,
 // L.vec = 16-byte vectors for the output columns
 hipError_t launch_keyed_split_forward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);

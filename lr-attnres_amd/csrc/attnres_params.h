@@ -139,6 +139,22 @@ struct Phase2Params {
   float scale, eps, bias, vscale;
 };
 
+// Logits of a query bank against the sources' keys (phase 1 from a query bank)
+constexpr int kKLMaxQ = 16;
+struct KeyedLogitsParams {
+  const void* val[kMaxSources];
+  void* dval[kMaxSources];     // backward: [n_tok, D] dense
+  int32_t vstride[kMaxSources];
+  const void* queries;         // [n_q, D], value dtype
+  void* logits;                // forward: [n_q, n_src, n_tok], value dtype
+  const void* dlogits;         // backward: same layout
+  float* inv;                  // [n_src, n_tok]: 1/rms of each key (forward writes, backward reads)
+  float* partials;             // backward: [groups, n_q * D] query-gradient partial rows (null: no dqueries)
+  int64_t n_tok;
+  int32_t n_src, n_q, D, key_norm, n_part;
+  float eps;
+};
+
 // Key-producer epilogue: split of the fused [out | key | pad] projection.
 struct KeySplitParams {
   const void* y;     // [n_tok, y_stride]: the projection (GEMM output)

@@ -44,6 +44,8 @@ phase1_from_logits_ref / phase2_*_ref     phase1+phase2 == full read identity
                                           (tests/test_attnres_ops.py:582-610),
                                           golden fixtures with gradients,
                                           fp64 gradcheck
+attention_residual_phase1_ref             one query == the base read (pinned
+                                          above), fp64 brute force of out / lse
 ========================================  ======================================
 """
 
@@ -326,6 +328,21 @@ def phase1_from_logits_ref(values, logits: Tensor, normalize_output: bool = Fals
     return out, torch.logsumexp(logits.float(), dim=1)
 
 
+def attention_residual_phase1_ref(values, queries: Tensor, key_norm: bool):
+    """Phase 1 from a query bank, ``_attnres_phase1_read_torch`` (``attnres_ops.py:2620-2627``,
+    reached from ``attention_residual_phase1`` :3862-3907, which casts the
+    queries to the value dtype first).
+
+    values [S,B,T,D]; queries [Q,D].  Returns (out [Q,B,T,D], lse [Q,B,T]).
+    """
+    v = stack_sources(values)
+    keys = norm(v) if key_norm else v
+    logits = torch.einsum("qd,sbtd->qsbt", queries.to(keys.dtype), keys)
+    lse = torch.logsumexp(logits.float(), dim=1)
+    w = F.softmax(logits.float(), dim=1).to(v.dtype)
+    return torch.einsum("qsbt,sbtd->qbtd", w, v), lse
+
+
 def attention_residual_phase2_ref(partial_value: Tensor, query: Tensor, interblock_output: Tensor,
                                   interblock_lse: Tensor, key_norm: bool, logit_bias=0.0,
                                   normalize_output: bool = False) -> Tensor:
@@ -433,6 +450,7 @@ __all__ = [
     "lrid_block_source",
     "block_count_logit_bias",
     "phase1_from_logits_ref",
+    "attention_residual_phase1_ref",
     "attention_residual_phase2_ref",
     "lrid_attention_residual_phase2_ref",
     "softmax_weights_ref",

@@ -36,7 +36,9 @@ def test_library_exports_every_declared_symbol():
                             "attnres_read_backward_workspace_size", "attnres_read_forward",
                             "attnres_phase1_forward", "attnres_phase1_backward", "attnres_phase2_forward",
                             "attnres_phase2_backward", "attnres_phase2_backward_workspace_size",
-                            "attnres_keyed_split_forward", "attnres_keyed_split_backward"])
+                            "attnres_keyed_split_forward", "attnres_keyed_split_backward",
+                            "attnres_keyed_logits_forward", "attnres_keyed_logits_backward",
+                            "attnres_keyed_logits_backward_workspace_size"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -268,8 +270,37 @@ def test_phase_ops_fail_loudly_on_cpu_tensors():
                                                  torch.zeros(1, 2), 0.5, True)
     with pytest.raises(RuntimeError, match=r"logits must be \[Q, 3"):
         ops.attention_residual_phase1_from_logits(vs, torch.randn(2, 4, 1, 2))
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.attention_residual_phase1(vs, torch.randn(2, 8), True)
+    with pytest.raises(RuntimeError, match=r"queries must be \[Q, 8\]"):
+        ops.attention_residual_phase1(vs, torch.randn(2, 7), True)
+
+
+def _kldesc(n_src=3, n_q=2, n_tok=1000, dim=768, key_norm=1):
+    d = H.KeyedLogitsDesc()
+    d.n_src, d.n_q, d.dtype, d.n_tok, d.dim, d.key_norm = n_src, n_q, 1, n_tok, dim, key_norm
+    d.norm_eps = 1e-6
+    d._vals = (ctypes.c_void_p * n_src)(*([0x1000] * n_src))
+    d._str = (ctypes.c_int64 * n_src)(*([dim] * n_src))
+    d.values = d._vals
+    d.value_row_stride = d._str
+    d.queries = 0x2000
+    return d
+
+
+@needs_lib
+def test_keyed_logits_workspace_and_validation_are_host_computations():
+    lib = H.load()
+    # query-gradient partial rows: min(n_tok, 128) x Q x D floats
+    assert lib.attnres_keyed_logits_backward_workspace_size(ctypes.byref(_kldesc())) == 128 * 2 * 768 * 4
+    assert lib.attnres_keyed_logits_backward_workspace_size(ctypes.byref(_kldesc(n_tok=5))) == 5 * 2 * 768 * 4
+    assert lib.attnres_keyed_logits_backward_workspace_size(ctypes.byref(_kldesc(n_tok=0))) == 0
+    # invalid descriptions: no workspace, and the entry points refuse them before any launch
+    for bad in (_kldesc(n_q=17), _kldesc(n_src=0), _kldesc(dim=4097)):
+        assert lib.attnres_keyed_logits_backward_workspace_size(ctypes.byref(bad)) == 0
+        assert lib.attnres_keyed_logits_forward(ctypes.byref(bad), ctypes.c_void_p(0x3000), None, None) != 0
+    rc = lib.attnres_keyed_logits_forward(ctypes.byref(_kldesc()), None, None, None)
+    assert rc != 0 and b"logits" in lib.attnres_last_error()
 
 
 def _ksdesc(**kw):

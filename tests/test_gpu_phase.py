@@ -119,6 +119,34 @@ def test_phase1_one_wave_rows_backward(dtype, S, Q, D, ldt, T):
     assert_close(dl, e_dl, dtype, "dlogits", reduced=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,Q,D,key_norm", [(3, 2, 256, True), (5, 4, 768, True), (6, 16, 100, False),
+                                            (2, 1, 1024, True), (9, 3, 4096, False)])
+def test_phase1_query_bank_matches_oracle(dtype, S, Q, D, key_norm):
+    """attention_residual_phase1: logits of a query bank against the sources'
+    keys (keyed-logits kernels), then the cached-logit read; gradients into
+    the values (both paths) and the fp32 query bank."""
+    g = gen(4000 + S * 31 + Q * 7 + D)
+    B, T = 2, 7
+    values = [randn(g, (B, T, D), dtype) for _ in range(S)]
+    queries = randn(g, (Q, D), torch.float32, 2.0 / math.sqrt(D))  # logits of order 2
+    go = randn(g, (Q, B, T, D), dtype)
+    glse = randn(g, (Q, B, T), torch.float32)
+    vd = [leaf(x) for x in values]
+    qd = leaf(queries)
+    out, lse = ops.attention_residual_phase1(vd, qd, key_norm)
+    torch.autograd.backward([out, lse], [go.to(DEV), glse.to(DEV)])
+    vc = torch.stack(values).clone().requires_grad_(True)
+    qc = queries.clone().requires_grad_(True)
+    e_out, e_lse = O.attention_residual_phase1_ref(vc, qc, key_norm)
+    torch.autograd.backward([e_out, e_lse], [go, glse])
+    assert_close(out, e_out, dtype, "out")
+    assert_close(lse, e_lse, torch.float32 if dtype == torch.float32 else dtype, "lse", reduced=True)
+    for s in range(S):
+        assert_close(vd[s].grad, vc.grad[s], dtype, f"dv{s}")
+    assert_close(qd.grad, qc.grad, dtype, "dqueries", reduced=True)
+
+
 def test_phase1_unused_lse_and_strided_sources():
     # sources that are strided views (last-dim slices of a wider tensor) and a
     # backward through the output only

@@ -354,6 +354,44 @@ def test_phase1_phase2_composition_equals_full_read():
     assert torch.allclose(merged, full, atol=1e-6, rtol=1e-6)
 
 
+@pytest.mark.parametrize("key_norm", [True, False])
+def test_phase1_query_bank_single_query_is_the_read(key_norm):
+    # one query row: phase 1 from a query bank is the base read with that query
+    # (both are _attnres_*_read_torch in the reference); fp64, so the two
+    # einsum contractions agree to rounding
+    torch.manual_seed(12)
+    values = [torch.randn(2, 3, 8, dtype=torch.float64) for _ in range(4)]
+    q = torch.randn(8, dtype=torch.float64)
+    out, lse = O.attention_residual_phase1_ref(values, q[None], key_norm)
+    read = O.attention_residual_read_torch(values, q, key_norm)
+    assert torch.allclose(out[0], read, atol=1e-12, rtol=1e-12)
+    assert lse.shape == (1, 2, 3)
+
+
+def test_phase1_query_bank_closed_form():
+    # fp64 brute force: out[q] = sum_s softmax_s(<q, v_s / rms(v_s)>) v_s and
+    # lse[q] = log sum_s exp(<q, v_s / rms(v_s)>), query by query
+    torch.manual_seed(13)
+    S, Q, B, T, D = 3, 3, 2, 2, 5
+    v = torch.randn(S, B, T, D, dtype=torch.float64)
+    qs = torch.randn(Q, D, dtype=torch.float64)
+    out, lse = O.attention_residual_phase1_ref(v, qs, True)
+    vn = v.numpy()
+    eps = float(torch.finfo(torch.float64).eps)
+    for qi in range(Q):
+        for b in range(B):
+            for t in range(T):
+                ks = [vn[s, b, t] / np.sqrt(np.mean(vn[s, b, t] ** 2) + eps) for s in range(S)]
+                lg = np.array([float(np.dot(qs[qi].numpy(), k)) for k in ks])
+                w = np.exp(lg - lg.max())
+                w /= w.sum()
+                expect = sum(w[s] * vn[s, b, t] for s in range(S))
+                assert np.allclose(out[qi, b, t].numpy(), expect, atol=1e-12)
+                # the reference takes the lse of float(logits): fp32 precision
+                ref = lg.max() + np.log(np.exp(lg - lg.max()).sum())
+                assert abs(float(lse[qi, b, t]) - ref) < 1e-6 * max(1.0, abs(ref))
+
+
 def test_gated_query_closed_forms():
     qs = torch.randn(2, 4)
     qd = torch.randn(1, 3, 8)
