@@ -1045,9 +1045,10 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     L.wpt = wv.cb;
     const int64_t wgs = (d->n_tok + kPhase2Teams - 1) / kPhase2Teams;
     int64_t cap = groups < kFullBwdGroups ? groups : kFullBwdGroups;
-    // the packed-arithmetic kernels: one resident round of waves, half the
-    // partial rows (measured at p5: 33.0 -> 29.9 us per call)
-    if (phase2_fast(d, wv) && cap > base_fast_streams() / kPhase2Teams) cap = base_fast_streams() / kPhase2Teams;
+    // one resident round of waves: half the partial rows of 2048 workgroups,
+    // and the reduction's chains of dependent loads half as long (measured at
+    // p5: packed kernels 33.0 -> 29.9 us per call)
+    if (cap > base_fast_streams() / kPhase2Teams) cap = base_fast_streams() / kPhase2Teams;
     L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
     L.feat = d->key_norm ? 1 : 0;
