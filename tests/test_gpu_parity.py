@@ -258,6 +258,33 @@ def test_base_one_wave_rows_few_tokens(T):
     _base_case(960 + T, torch.bfloat16, 1, T, 768, 5, True, bias=[0.2, -0.1, 0.0, 0.4, -0.3])
 
 
+def test_base_one_wave_rows_strided_and_aliased_sources():
+    """Sources that are column slices of wider tensors (row stride 832, not
+    768) and one source passed twice: the one-wave base kernels address every
+    row through the per-source stride table; the aliased source's gradient is
+    the sum of its two slots."""
+    g = gen(970)
+    B, T, D, S = 2, 33, 768, 5
+    wide = [randn(g, (B, T, D + 64), torch.bfloat16) for _ in range(S - 1)]
+    q = randn(g, (D,), torch.float32, 0.1)
+    up = randn(g, (B, T, D), torch.bfloat16)
+    wd = [leaf(x) for x in wide]
+    qd = leaf(q)
+    src_d = [w[..., :D] for w in wd]
+    out = ops.attention_residual_read(src_d + [src_d[1]], qd, True)
+    out.backward(up.to(DEV))
+    wc = [x.clone().requires_grad_(True) for x in wide]
+    qc = q.clone().requires_grad_(True)
+    src_c = [w[..., :D] for w in wc]
+    ref = O.attention_residual_read_ref(src_c + [src_c[1]], qc, True)
+    ref.backward(up)
+    assert_close(out, ref, torch.bfloat16, "out")
+    for s in range(S - 1):
+        assert_close(wd[s].grad[..., :D], wc[s].grad[..., :D], torch.bfloat16, f"dv{s}")
+        assert float(wd[s].grad[..., D:].abs().max()) == 0.0
+    assert_close(qd.grad, qc.grad, torch.bfloat16, "dq", reduced=True)
+
+
 def test_base_one_wave_rows_many_tokens():
     """More tokens than token streams (each stream walks several tokens); the
     query gradient sums every token."""
