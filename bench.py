@@ -428,7 +428,7 @@ def main():
 
     ms = time_steps(wl, args.steps, args.warmup, stream, sv)
     f_ms, b_ms = time_kernels(wl, args.steps, stream, sv)
-    api_ms = None if args.no_api else time_api(c, wl, max(5, args.steps // 5), 3)
+    api_ms = None if args.no_api else time_api(c, wl, max(20, args.steps), 5)
 
     fwd_b, bwd_b = bytes_per_token(c)
     n_tok = wl.n_tok

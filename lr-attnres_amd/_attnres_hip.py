@@ -261,7 +261,7 @@ def _row_view_ok(t: torch.Tensor) -> bool:
 
 def as_rows(t: torch.Tensor) -> torch.Tensor:
     """A [B,T,W] tensor whose tokens are uniformly strided rows (copy if not)."""
-    return t if _row_view_ok(t) else t.contiguous()
+    return t if t.is_contiguous() or _row_view_ok(t) else t.contiguous()
 
 
 class Desc:
@@ -333,26 +333,29 @@ def forward(desc: Desc, device, dtype, need_weights: bool, normalize_output: boo
     return out, w, inv, pre
 
 
-def _row_blocks(count: int, n_tok: int, width: int, device, dtype, batched: bool):
-    """``count`` dense [n_tok, width] gradient buffers: separate allocations, or
-    (``batched``) views of one allocation."""
+def _row_blocks(count: int, n_tok: int, width: int, device, dtype, batched: bool, lead=None):
+    """``count`` dense gradient buffers of shape ``lead + (width,)`` (``lead``
+    defaults to ``(n_tok,)``): separate allocations, or (``batched``) views of
+    one allocation."""
+    shape = (tuple(lead) if lead is not None else (n_tok,)) + (width,)
     if not batched:
-        return [torch.empty((n_tok, width), device=device, dtype=dtype) for _ in range(count)]
-    return list(torch.empty((count, n_tok, width), device=device, dtype=dtype).unbind(0))
+        return [torch.empty(shape, device=device, dtype=dtype) for _ in range(count)]
+    return list(torch.empty((count,) + shape, device=device, dtype=dtype).unbind(0))
 
 
 def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, want_dquery: bool,
              want_dgate: bool, want_dbias: bool, query_shape, gate_shape, lr: bool, has_query_dyn: bool,
-             batched: bool = False):
+             batched: bool = False, lead=None):
     """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias).
 
     With ``batched`` the per-source gradients are views of one allocation per
     kind (fewer allocator calls); otherwise each is its own tensor (the
-    library op's outputs may not alias one another)."""
+    library op's outputs may not alias one another).  ``lead`` shapes each
+    per-source gradient as ``lead + (width,)`` (default ``(n_tok,)``)."""
     lib = load()
     n = desc.n_src
-    dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, batched)
-    dkeys = _row_blocks(n, desc.n_tok, desc.R, device, dtype, batched) if lr else []
+    dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, batched, lead)
+    dkeys = _row_blocks(n, desc.n_tok, desc.R, device, dtype, batched, lead) if lr else []
     dq = torch.empty(query_shape, device=device, dtype=dtype) if want_dquery else None
     dqd = torch.empty((desc.n_tok, desc.R), device=device, dtype=dtype) if has_query_dyn else None
     dg = torch.empty(gate_shape, device=device, dtype=dtype) if want_dgate else None

@@ -340,10 +340,8 @@ class _ReadFn(torch.autograd.Function):
                 want_dgate=gate is not None, want_dbias=bias is not None,
                 query_shape=tuple(query.shape) if query is not None else (0,),
                 gate_shape=tuple(gate.shape) if gate is not None else (0,), lr=n_k > 0,
-                has_query_dyn=query_dyn is not None, batched=True)
-        grads = [None]
-        grads += [t.view(B, T, D) for t in dvals]
-        grads += [t.view(B, T, ctx.desc.R) for t in dkeys]
+                has_query_dyn=query_dyn is not None, batched=True, lead=(B, T))
+        grads = [None, *dvals, *dkeys]
         for present, g in zip(has, (dq, dqd.view(query_dyn.shape) if dqd is not None else None, dg, db)):
             if present:
                 grads.append(g)
