@@ -410,7 +410,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the AttnRes read shards "
-              "by tokens with no exchange, see DESIGN.md", file=sys.stderr)
+              "by tokens with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
 
     dev = torch.device("cuda:0")

@@ -6,7 +6,7 @@
  * replaces one of those host launchers; the citation names the reference
  * function (file:line in attnres_ops.py) whose job it takes over.  The Python
  * drop-in module (lr-attnres_amd/attnres_ops.py) binds these symbols with
- * ctypes; INTEGRATION.md shows the binding.
+ * ctypes (lr-attnres_amd/_attnres_hip.py holds the ctypes structures).
  *
  * Conventions
  *  - Plain C types only.  Device buffers are passed as device pointers;
