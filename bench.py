@@ -11,10 +11,11 @@ metric is quoted on.  Prints ONE JSON line.
 
 Besides the contract fields the line carries:
   roofline      HBM roofline of the dominant kernel (the backward), from its
-                average launch duration measured with HIP events on its stream
-  cpu_baseline  the eager PyTorch restatement (oracle/) timed on the host cores
-                on a bounded token sample of the same workload
-  kernels       per-call average durations and algorithmic GB/s of fwd and bwd
+                average launch duration: HIP events that the library records
+                on the launch stream around that kernel alone
+  kernels       average durations and algorithmic GB/s of the fwd and bwd
+                main kernels, and of the whole C calls (``*_call_ms``: the
+                backward call adds the partial-sum reduction)
   api           ms/step through the Python autograd API (custom op + ctypes)
 """
 
@@ -297,6 +298,33 @@ def time_kernels(wl, steps, stream, sv):
     return f, b
 
 
+def time_main_kernels(wl, steps, sv):
+    """Average duration of the forward's and the backward's main kernel alone
+    (the backward's partial-sum reduction excluded): HIP events that the
+    library records on the call's stream around that kernel."""
+    lib = wl.lib
+    steps = min(steps, 128)  # two event pairs per step, 256 pairs in the library
+    if lib.attnres_kernel_timing(1):
+        raise RuntimeError(lib.attnres_last_error().decode())
+    try:
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            wl.fwd(sv)
+            wl.bwd(sv)
+        buf = (ctypes.c_float * (2 * steps))()
+        n = lib.attnres_kernel_times(buf, 2 * steps)
+        if n < 0:
+            raise RuntimeError(lib.attnres_last_error().decode())
+    finally:
+        lib.attnres_kernel_timing(0)
+    per = 1 if wl.fwd_only else 2
+    if n != per * steps:
+        raise RuntimeError(f"expected {per * steps} timed kernels, got {n}")
+    f = sum(buf[i] for i in range(0, n, per)) / steps
+    b = sum(buf[i] for i in range(1, n, per)) / steps if per == 2 else 0.0
+    return f, b
+
+
 def time_api(c, wl, steps, warmup):
     """ms/step through the public autograd API (drop-in module)."""
     import attnres_ops as ops
@@ -428,14 +456,15 @@ def main():
 
     ms = time_steps(wl, args.steps, args.warmup, stream, sv)
     f_ms, b_ms = time_kernels(wl, args.steps, stream, sv)
+    fk_ms, bk_ms = time_main_kernels(wl, args.steps, sv)
     api_ms = None if args.no_api else time_api(c, wl, max(20, args.steps), 5)
 
     fwd_b, bwd_b = bytes_per_token(c)
     n_tok = wl.n_tok
     tok_s = n_tok / (ms / 1e3)
     gbs_step = (fwd_b + bwd_b) * n_tok / (ms / 1e3) / 1e9
-    fwd_gbs = fwd_b * n_tok / (f_ms / 1e3) / 1e9
-    bwd_gbs = bwd_b * n_tok / (b_ms / 1e3) / 1e9 if bwd_b else 0.0
+    fwd_gbs = fwd_b * n_tok / (fk_ms / 1e3) / 1e9
+    bwd_gbs = bwd_b * n_tok / (bk_ms / 1e3) / 1e9 if bwd_b else 0.0
     dom_gbs, dom_name, dom_bytes = (bwd_gbs, "backward", bwd_b) if bwd_b else (fwd_gbs, "forward", fwd_b)
     # HBM bytes per launch of the dominant kernel, measured with rocprofv3
     # FETCH_SIZE / WRITE_SIZE (scaled by a copy of known size) and kept in
@@ -471,8 +500,9 @@ def main():
                      "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
                      "bytes_per_token": dom_bytes, "algorithmic_bytes_per_launch": dom_bytes * n_tok,
                      "traffic": traffic},
-        "kernels": {"forward_ms": round(f_ms, 5), "forward_gbs": round(fwd_gbs, 1),
-                    "backward_ms": round(b_ms, 5), "backward_gbs": round(bwd_gbs, 1),
+        "kernels": {"forward_ms": round(fk_ms, 5), "forward_gbs": round(fwd_gbs, 1),
+                    "backward_ms": round(bk_ms, 5), "backward_gbs": round(bwd_gbs, 1),
+                    "forward_call_ms": round(f_ms, 5), "backward_call_ms": round(b_ms, 5),
                     "bytes_per_token": {"fwd": fwd_b, "bwd": bwd_b}},
         "api": {"ms_per_step": round(api_ms, 4) if api_ms else None},
     }

@@ -109,6 +109,21 @@ int attnres_abi_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* attnres_last_error(void);
 
+/* Opt-in kernel timing for benchmarks.  No counterpart in the reference (its
+ * benchmarks time the Triton launches with CUDA events from Python); it lets
+ * a caller time the read's main kernel alone.  While enabled,
+ * attnres_read_forward and attnres_read_backward record a pair of HIP events
+ * on the call's stream around their main kernel (the backward's partial-sum
+ * reduction stays outside), up to 256 pairs.  Enabling creates the events on
+ * the current device; disabling destroys them.  Process-wide state: not for
+ * concurrent callers.  Returns ATTNRES_OK or an error code. */
+int attnres_kernel_timing(int enable);
+
+/* Waits for the recorded pairs, writes up to max_n durations (ms, in call
+ * order) to ms, and starts a new recording.  Returns the number written, or
+ * a negative error code (timing not enabled, bad buffer, HIP error). */
+int attnres_kernel_times(float* ms, int max_n);
+
 /*
  * Forward read.  Writes out [n_tok, dim] (dtype); when `weights` is not NULL
  * also the fp32 softmax weights [n_tok, heads, n_src] (the backward needs

@@ -221,6 +221,10 @@ def load() -> ctypes.CDLL:
     lib.attnres_keyed_split_backward.restype = c_int
     lib.attnres_keyed_split_backward.argtypes = [POINTER(KeyedSplitDesc), c_void_p, c_void_p, POINTER(c_float),
                                                  c_void_p, c_void_p]
+    lib.attnres_kernel_timing.restype = c_int
+    lib.attnres_kernel_timing.argtypes = [c_int]
+    lib.attnres_kernel_times.restype = c_int
+    lib.attnres_kernel_times.argtypes = [POINTER(c_float), c_int]
     v = lib.attnres_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libattnres_hip ABI {v} != expected {ABI_VERSION}; rebuild the library")

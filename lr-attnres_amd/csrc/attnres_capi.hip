@@ -16,6 +16,26 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Opt-in kernel timing (attnres_kernel_timing): HIP events recorded on the
+// call's stream right before and after the read's main kernel, so that a
+// benchmark times that kernel alone, without the partial-sum reduction that
+// follows it in the backward.  One process-wide set of event pairs, created
+// on the device current at enable time; not for concurrent callers.
+constexpr int kTimerPairs = 256;
+struct KernelTimer {
+  bool on = false;
+  int n = 0;
+  hipEvent_t ev[2 * kTimerPairs];
+};
+KernelTimer g_timer;
+
+inline void timer_begin(hipStream_t st) {
+  if (g_timer.on && g_timer.n < kTimerPairs) (void)hipEventRecord(g_timer.ev[2 * g_timer.n], st);
+}
+inline void timer_end(hipStream_t st) {
+  if (g_timer.on && g_timer.n < kTimerPairs) (void)hipEventRecord(g_timer.ev[2 * g_timer.n++ + 1], st);
+}
+
 int fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -355,6 +375,39 @@ extern "C" int attnres_abi_version(void) { return ATTNRES_ABI_VERSION; }
 
 extern "C" const char* attnres_last_error(void) { return g_last_error.c_str(); }
 
+extern "C" int attnres_kernel_timing(int enable) {
+  if (enable && !g_timer.on) {
+    for (int i = 0; i < 2 * kTimerPairs; ++i) {
+      const hipError_t e = hipEventCreate(&g_timer.ev[i]);
+      if (e != hipSuccess) {
+        for (int j = 0; j < i; ++j) (void)hipEventDestroy(g_timer.ev[j]);
+        return fail(ATTNRES_ELAUNCH, "hipEventCreate failed: %s", hipGetErrorString(e));
+      }
+    }
+    g_timer.on = true;
+    g_timer.n = 0;
+  } else if (!enable && g_timer.on) {
+    for (int i = 0; i < 2 * kTimerPairs; ++i) (void)hipEventDestroy(g_timer.ev[i]);
+    g_timer.on = false;
+    g_timer.n = 0;
+  }
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_kernel_times(float* ms, int max_n) {
+  if (!g_timer.on) return fail(ATTNRES_EINVAL, "kernel timing is not enabled");
+  if (max_n < 0 || (max_n > 0 && !ms)) return fail(ATTNRES_EINVAL, "bad output buffer");
+  const int n = g_timer.n < max_n ? g_timer.n : max_n;
+  for (int i = 0; i < n; ++i) {
+    hipError_t e = hipEventSynchronize(g_timer.ev[2 * i + 1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms[i], g_timer.ev[2 * i], g_timer.ev[2 * i + 1]);
+    if (e != hipSuccess) return fail(ATTNRES_ELAUNCH, "kernel timing event failed: %s", hipGetErrorString(e));
+  }
+  const int recorded = g_timer.n;
+  g_timer.n = 0;
+  return recorded < max_n ? recorded : max_n;
+}
+
 extern "C" size_t attnres_read_backward_workspace_size(const attnres_read_desc* d) {
   if (check_desc(d) != ATTNRES_OK) return 0;
   const PartLayout L = part_layout(d, true, true, true);
@@ -389,6 +442,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
   L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;
+  timer_begin(st);
   if (d->mode == ATTNRES_MODE_AVERAGE) {
     L.lds = 32 * sizeof(float);
     err = launch_average_forward(d->dtype, p, L, st);
@@ -430,6 +484,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       err = launch_base_forward(d->dtype, p, L, st);
     }
   }
+  timer_end(st);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "forward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
 }
@@ -519,6 +574,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   int partials_layout = kPartRowMajor;  // fast LR: slot-major; fast base: tiled (slot-major for tiny inputs)
   BaseFastPlan bf;
   hipError_t err;
+  timer_begin(st);
   if (d->mode == ATTNRES_MODE_AVERAGE) {
     L.lds = 32 * sizeof(float);
     err = launch_average_backward(d->dtype, bp, L, st);
@@ -588,6 +644,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "base backward needs %zu bytes of LDS", L.lds);
     err = launch_base_backward(d->dtype, bp, L, st);
   }
+  timer_end(st);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
 
   if (PL.n_part > 0) {

@@ -38,7 +38,8 @@ def test_library_exports_every_declared_symbol():
                             "attnres_phase2_backward", "attnres_phase2_backward_workspace_size",
                             "attnres_keyed_split_forward", "attnres_keyed_split_backward",
                             "attnres_keyed_logits_forward", "attnres_keyed_logits_backward",
-                            "attnres_keyed_logits_backward_workspace_size"])
+                            "attnres_keyed_logits_backward_workspace_size", "attnres_kernel_timing",
+                            "attnres_kernel_times"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -345,3 +346,13 @@ def test_keyed_split_fails_loudly_on_cpu_tensors():
     with pytest.raises(RuntimeError, match="columns"):
         ops.lrid_fused_projection_split(torch.randn(2, 3, 70), 64, 16)
 
+
+
+@needs_lib
+def test_kernel_times_need_timing_enabled():
+    # host-only paths: disabling when off and reading times when off make no HIP call
+    lib = H.load()
+    assert lib.attnres_kernel_timing(0) == 0
+    buf = (ctypes.c_float * 4)()
+    assert lib.attnres_kernel_times(buf, 4) == -1
+    assert b"not enabled" in lib.attnres_last_error()
