@@ -418,6 +418,44 @@ def test_weights_sum_to_one_and_match_oracle():
     assert float((w.cpu() - ref).abs().max()) <= 1e-6
 
 
+
+def test_kernel_timing_records_one_pair_per_call_and_changes_no_result():
+    import ctypes
+    g = gen(1150)
+    B, T, D, S, R, Hh = 2, 64, 1024, 13, 64, 4
+    vd = [randn(g, (B, T, D), torch.bfloat16).to(DEV) for _ in range(S)]
+    kd = [randn(g, (B, T, R), torch.bfloat16).to(DEV) for _ in range(S)]
+    qd = randn(g, (Hh, R // Hh), torch.bfloat16, 0.5).to(DEV)
+    go = randn(g, (B * T, D), torch.bfloat16).to(DEV)
+    desc = H.Desc(vd, kd, qd, None, None, None, Hh, 0.25, True, False, H.MODE_SOFTMAX, 0, False)
+
+    def run():
+        out, w, inv, pre = H.forward(desc, DEV, torch.bfloat16, True, False, True)
+        grads = H.backward(desc, DEV, torch.bfloat16, go, pre, inv, w, want_dquery=True, want_dgate=False,
+                           want_dbias=False, query_shape=tuple(qd.shape), gate_shape=(0,), lr=True,
+                           has_query_dyn=False)
+        return out, grads[0], grads[1], grads[2]
+
+    plain = run()
+    lib = H.load()
+    assert lib.attnres_kernel_timing(1) == 0
+    try:
+        timed = run()
+        timed2 = run()
+        buf = (ctypes.c_float * 8)()
+        n = lib.attnres_kernel_times(buf, 8)
+        assert n == 4, lib.attnres_last_error()  # fwd, bwd, fwd, bwd
+        assert all(0.0 < buf[i] < 1000.0 for i in range(n))
+        assert lib.attnres_kernel_times(buf, 8) == 0  # read resets the recording
+    finally:
+        assert lib.attnres_kernel_timing(0) == 0
+    torch.cuda.synchronize()
+    for a, b in ((plain, timed), (plain, timed2)):
+        assert torch.equal(a[0], b[0])
+        for x, y in zip(a[1] + a[2], b[1] + b[2]):
+            assert torch.equal(x, y)
+        assert torch.equal(a[3], b[3])
+
 def test_backward_is_deterministic():
     g = gen(1200)
     B, T, D, S, R, Hh = 4, 256, 1024, 13, 64, 4
