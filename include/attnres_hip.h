@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 4
+#define ATTNRES_ABI_VERSION 5
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -85,6 +85,14 @@ typedef struct attnres_read_desc {
   int32_t gate_per_token;
   int32_t gate_act;                /* ATTNRES_GATE_* */
   const float* logit_bias;         /* [n_src] fp32 added to every logit of a source, or NULL */
+  int32_t key_dtype;               /* ATTNRES_DTYPE_* of the LR keys (and of their gradients); the
+                                      reference's eager read (attnres_ops.py:4163-4192) norms keys of
+                                      any dtype in fp32 and rounds them to the value dtype, so with a
+                                      key dtype other than the value dtype the logits are computed in
+                                      the value dtype when key_norm and in the key dtype without it;
+                                      the query (static or per-token) must be in that logit dtype and
+                                      its gradient is written in it.  No gate with mixed dtypes.  Base
+                                      and average reads ignore it. */
 } attnres_read_desc;
 
 /* Gradient buffers for attnres_read_backward. */
@@ -94,9 +102,9 @@ typedef struct attnres_read_grads {
   const float* out_inv_rms;  /* [n_tok] from the forward (when normalize_output) */
   const float* weights;      /* [n_tok, heads, n_src] softmax weights saved by the forward */
   void* const* dvalues;      /* [n_src] device pointers, each [n_tok, dim] dense */
-  void* const* dkeys;        /* [n_src] device pointers, each [n_tok, rank] dense (LR); NULL base */
-  void* dquery;              /* static query gradient (dtype, same shape as query) or NULL */
-  void* dquery_dyn;          /* [n_tok, rank] dense or NULL */
+  void* const* dkeys;        /* [n_src] device pointers, each [n_tok, rank] dense in key_dtype (LR); NULL base */
+  void* dquery;              /* static query gradient (the query's dtype and shape) or NULL */
+  void* dquery_dyn;          /* [n_tok, rank] dense (the query's dtype) or NULL */
   void* dgate;               /* gradient of gate (same shape as gate) or NULL */
   float* dbias;              /* [n_src] fp32 or NULL */
   void* workspace;           /* device scratch for deterministic cross-token reductions */

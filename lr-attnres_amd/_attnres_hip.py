@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_SOURCES = 64
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -54,6 +54,7 @@ class ReadDesc(ctypes.Structure):
         ("gate_per_token", c_int32),
         ("gate_act", c_int32),
         ("logit_bias", POINTER(c_float)),
+        ("key_dtype", c_int32),
     ]
 
 
@@ -283,6 +284,11 @@ class Desc:
         self.D = D
         self.R = keys[0].size(-1) if keys else 0
         self.heads = heads
+        # gradient dtypes: keys' for the key gradients, the query's (the
+        # logit dtype of an LR read) for the query gradients
+        self.key_dtype = keys[0].dtype if keys else v0.dtype
+        qref = query if query is not None else query_dyn
+        self.query_dtype = qref.dtype if qref is not None else v0.dtype
         self._vals = (c_void_p * n)(*[t.data_ptr() for t in values])
         self._vstr = (c_int64 * n)(*[t.stride(1) for t in values])
         if keys:
@@ -312,6 +318,7 @@ class Desc:
         d.gate_per_token = int(bool(gate_per_token))
         d.gate_act = gate_act
         d.logit_bias = _fptr(bias)
+        d.key_dtype = DTYPE_CODE[self.key_dtype]
         self.c = d
 
 
@@ -359,9 +366,9 @@ def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, wan
     lib = load()
     n = desc.n_src
     dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, batched, lead)
-    dkeys = _row_blocks(n, desc.n_tok, desc.R, device, dtype, batched, lead) if lr else []
-    dq = torch.empty(query_shape, device=device, dtype=dtype) if want_dquery else None
-    dqd = torch.empty((desc.n_tok, desc.R), device=device, dtype=dtype) if has_query_dyn else None
+    dkeys = _row_blocks(n, desc.n_tok, desc.R, device, desc.key_dtype, batched, lead) if lr else []
+    dq = torch.empty(query_shape, device=device, dtype=desc.query_dtype) if want_dquery else None
+    dqd = torch.empty((desc.n_tok, desc.R), device=device, dtype=desc.query_dtype) if has_query_dyn else None
     dg = torch.empty(gate_shape, device=device, dtype=dtype) if want_dgate else None
     db = torch.empty((n,), device=device, dtype=torch.float32) if want_dbias else None
     g = ReadGrads()

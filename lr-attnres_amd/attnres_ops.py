@@ -57,6 +57,35 @@ def is_fused_attnres_available() -> bool:
     return _hip.available()
 
 
+def _lrid_list_head_dims(values, keys, num_heads: int):
+    """(value head width, key head width), or None when ``num_heads`` does not
+    split both widths (reference: attnres_ops.py:4319-4330)."""
+    try:
+        H = int(num_heads)
+    except (TypeError, ValueError):
+        return None
+    if H < 1:
+        return None
+    D = values[0].size(-1)
+    R = keys[0].size(-1)
+    if D % H != 0 or R % H != 0:
+        return None
+    return D // H, R // H
+
+
+def _lrid_list_dims_within_triton_limits(values, keys, num_heads: int) -> bool:
+    """The reference's head-width limits of its direct Triton LR kernel
+    (value heads <= 4096, key heads <= 256; attnres_ops.py:4333-4338), kept
+    with the same answers because the reference's tests import and assert it
+    (tests/test_attnres_ops.py:515-520).  The HIP read here has no such limit:
+    wider heads take its general kernels."""
+    head_dims = _lrid_list_head_dims(values, keys, num_heads)
+    if head_dims is None:
+        return False
+    value_head_dim, key_head_dim = head_dims
+    return value_head_dim <= 4096 and key_head_dim <= 256
+
+
 # ---------------------------------------------------------------- argument handling
 
 # Logit biases given as host numbers (python floats or lists) become small
@@ -154,10 +183,19 @@ def _check_sources(srcs, what):
     for t in srcs:
         if t.shape != first.shape:
             raise RuntimeError(f"{what}: every source must have shape {tuple(first.shape)}, got {tuple(t.shape)}")
-        if t.dtype != first.dtype:
-            raise RuntimeError(f"{what}: every source must have dtype {first.dtype}, got {t.dtype}")
-    if first.dtype not in _ALLOWED:
-        raise RuntimeError(f"{what}: dtype {first.dtype} is not supported (fp32, bf16, fp16)")
+        if t.dtype not in _ALLOWED:
+            raise RuntimeError(f"{what}: dtype {t.dtype} is not supported (fp32, bf16, fp16)")
+
+
+def _promote(srcs):
+    """Sources of mixed dtypes in their common (promoted) dtype, as the
+    reference's eager read stacks them (``_as_stacked``, attnres_ops.py:58-61,
+    used at :2224, :3940 and :4246; ``torch.stack`` promotes).  Sources already
+    in that dtype are passed as they are."""
+    common = srcs[0].dtype
+    for t in srcs[1:]:
+        common = torch.promote_types(common, t.dtype)
+    return [t if t.dtype == common else t.to(common) for t in srcs]
 
 
 def _norm(x: Tensor) -> Tensor:
@@ -378,6 +416,10 @@ def attention_residual_read(values, query: Tensor, key_norm: bool, force_triton:
     if len(srcs) == 1:
         return _norm(srcs[0]) if normalize_output else srcs[0]
     dev = _check_gpu(srcs + [query], "attention_residual_read")
+    # the reference casts the query to the first source's dtype (attnres_ops.py:2516),
+    # and its eager read to the stacked sources' dtype (:2184)
+    query = query.to(srcs[0].dtype)
+    srcs = _promote(srcs)
     dtype = srcs[0].dtype
     D = srcs[0].size(-1)
     query = query.to(dtype)
@@ -407,13 +449,16 @@ def attention_residual_average_read(values, normalize_output: bool = False, forc
     if len(srcs) == 1:
         return _norm(srcs[0]) if normalize_output else srcs[0]
     _check_gpu(srcs, "attention_residual_average_read")
-    srcs = [_hip.as_rows(t) for t in srcs]
+    srcs = [_hip.as_rows(t) for t in _promote(srcs)]
     return _run(srcs, [], None, None, None, None, 1, 1.0, False, normalize_output, _hip.MODE_AVERAGE)
 
 
 # ---------------------------------------------------------------- public API: LR read
 
 def _lr_common(values, keys, num_heads, what):
+    """Values and keys as lists of [B, T, W] tensors, each list in its common
+    (promoted) dtype.  The first key's own dtype is returned too: the
+    reference casts the query to it (attnres_ops.py:4866-4870)."""
     vs = _sources(values)
     ks = _sources(keys)
     if len(vs) != len(ks):
@@ -427,7 +472,7 @@ def _lr_common(values, keys, num_heads, what):
         raise RuntimeError(f"{what}: keys must be [B, T, R] with the values' B, T")
     if H < 1 or D % H or R % H:
         raise RuntimeError(f"{what}: num_heads={H} must divide n_embd={D} and rank={R}")
-    return vs, ks, H, D, R
+    return _promote(vs), _promote(ks), H, D, R, ks[0].dtype
 
 
 def lrid_attention_residual_read(values, keys, query: Tensor, num_heads: int, logit_scale: float, key_norm: bool,
@@ -440,15 +485,16 @@ def lrid_attention_residual_read(values, keys, query: Tensor, num_heads: int, lo
     cast to the key dtype first, as in the reference.  The optional output
     rms-norm is fused for any number of heads.
     """
-    vs, ks, H, D, R = _lr_common(values, keys, num_heads, "lrid_attention_residual_read")
-    query = query.to(ks[0].dtype)
+    vs, ks, H, D, R, k0_dtype = _lr_common(values, keys, num_heads, "lrid_attention_residual_read")
+    query = query.to(k0_dtype)
     if len(vs) == 1:
         return _norm(vs[0]) if normalize_output else vs[0]
     dev = _check_gpu(vs + ks + [query], "lrid_attention_residual_read")
-    dtype = vs[0].dtype
-    if ks[0].dtype != dtype:
-        ks = [k.to(dtype) for k in ks]
-        query = query.to(dtype)
+    # Keys of another dtype than the values stay in their dtype: the eager read
+    # norms them in fp32 and rounds them to the value dtype (attnres_ops.py:4179-4180),
+    # so the logits are a value-dtype contraction with key_norm and a key-dtype
+    # one without it; the query is cast to that dtype (:4182).
+    query = query.to(vs[0].dtype if key_norm else ks[0].dtype)
     B, T, _ = vs[0].shape
     bias = _source_logit_bias(source_counts, source_logit_biases, len(vs), dev)
     vs = [_hip.as_rows(t) for t in vs]
@@ -480,7 +526,7 @@ def lrid_attention_residual_read_gated(values, keys, static_query: Optional[Tens
     deterministically).  Not present in the reference, which composes the query
     eagerly and then reads with an input-dependent query.
     """
-    vs, ks, H, D, R = _lr_common(values, keys, num_heads, "lrid_attention_residual_read_gated")
+    vs, ks, H, D, R, _ = _lr_common(values, keys, num_heads, "lrid_attention_residual_read_gated")
     dtype = vs[0].dtype
     B, T, _ = vs[0].shape
     dev = _check_gpu(vs + ks + [dynamic_query], "lrid_attention_residual_read_gated")
@@ -636,6 +682,7 @@ def attention_residual_phase1_from_logits(values, logits: Tensor, force_triton: 
     if len(srcs) == 0:
         raise RuntimeError("Cached-logit AttnRes phase1 requires at least one source")
     _check_sources(srcs, "attention_residual_phase1_from_logits")
+    srcs = _promote(srcs)  # the eager read stacks the sources (attnres_ops.py:3940)
     B, T, D = srcs[0].shape
     S = len(srcs)
     if logits.dim() != 4 or logits.size(1) != S or tuple(logits.shape[2:]) != (B, T):
@@ -701,6 +748,7 @@ def attention_residual_phase1(values, queries: Tensor, key_norm: bool, force_tri
     if len(srcs) == 0:
         raise RuntimeError("Two-phase AttnRes phase1 requires at least one source")
     _check_sources(srcs, "attention_residual_phase1")
+    srcs = _promote(srcs)
     B, T, D = srcs[0].shape
     if queries.dim() != 2 or queries.size(1) != D:
         raise RuntimeError(f"attention_residual_phase1: queries must be [Q, {D}], got {tuple(queries.shape)}")

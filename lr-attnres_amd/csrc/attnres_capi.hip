@@ -101,6 +101,10 @@ int check_desc(const attnres_read_desc* d) {
     if (d->dim % d->heads || d->rank % d->heads)
       return fail(ATTNRES_EINVAL, "heads=%d must divide dim=%d and rank=%d", d->heads, d->dim, d->rank);
     if (!d->keys || !d->key_row_stride) return fail(ATTNRES_EINVAL, "LR read needs keys and key_row_stride");
+    if (d->key_dtype != ATTNRES_DTYPE_F32 && d->key_dtype != ATTNRES_DTYPE_BF16 && d->key_dtype != ATTNRES_DTYPE_F16)
+      return fail(ATTNRES_EINVAL, "unknown key dtype %d", d->key_dtype);
+    if (d->key_dtype != d->dtype && d->gate)
+      return fail(ATTNRES_EUNSUPPORTED, "a gated query needs keys in the value dtype");
     for (int s = 0; s < d->n_src; ++s) {
       if (live && !d->keys[s]) return fail(ATTNRES_EINVAL, "keys[%d] is NULL", s);
       if (d->key_row_stride[s] < d->rank || d->key_row_stride[s] > INT32_MAX)
@@ -116,6 +120,14 @@ int check_desc(const attnres_read_desc* d) {
       return fail(ATTNRES_EINVAL, "unknown gate activation %d", d->gate_act);
   }
   return ATTNRES_OK;
+}
+
+// dtype of the LR logit path: the reference norms keys in fp32 and rounds them
+// to the value dtype, so with key_norm the logits are a value-dtype
+// contraction; without it they stay in the key dtype (attnres_ops.py:4179-4186)
+int logit_dtype(const attnres_read_desc* d) {
+  if (d->mode != ATTNRES_MODE_SOFTMAX || d->rank == 0) return d->dtype;
+  return d->key_norm ? d->dtype : d->key_dtype;
 }
 
 // Geometry shared by forward and backward.  `extra` are the other [n_tok, dim]
@@ -158,7 +170,7 @@ int make_plan(const attnres_read_desc* d, const void* const* extra, int n_extra,
     return fail(ATTNRES_EUNSUPPORTED, "dim=%d needs %d waves per token (max 16) on the %s path", d->dim, pl->wpt,
                 vec ? "vector" : "unaligned");
   pl->key_vec = 0;
-  if (pl->lr) {
+  if (pl->lr && d->key_dtype == d->dtype) {  // (keys of another dtype take the scalar key path)
     const int rh = d->rank / d->heads;
     bool kv = rh % EV == 0;
     for (int s = 0; kv && s < d->n_src; ++s) kv = aligned16(d->keys[s]) && ((d->key_row_stride[s] * es) % 16 == 0);
@@ -202,6 +214,8 @@ void fill_params(const attnres_read_desc* d, const Plan& pl, ReadParams* p) {
   p->key_vec = pl.key_vec;
   p->scale = pl.lr ? d->logit_scale : 1.0f;
   p->eps = d->norm_eps;
+  p->kdt = pl.lr ? d->key_dtype : d->dtype;
+  p->ldt = logit_dtype(d);
 }
 
 struct PartLayout {
@@ -298,6 +312,7 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
         break;
       }
   }
+  if (N < lr_fast_slot_floor(f->cb, f->rhc, f->nb)) return false;  // (the kernels assume the floor)
   if (f->cb == 2 && f->rhc == 8 && f->nb == 16) return false;  // no register room
   if (f->cb == 1 && f->rhc == 8 && f->vb == 16 && f->nb == 32) return false;  // not instantiated
   return true;
@@ -515,7 +530,8 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     // gradients of the cross-token quantities are zero
     hipStream_t st = (hipStream_t)stream;
     const int es = elem_size(d->dtype);
-    if (softmax && g->dquery && d->query) zero_async(g->dquery, (size_t)(lr ? d->rank : d->dim) * es, st);
+    if (softmax && g->dquery && d->query)
+      zero_async(g->dquery, (size_t)(lr ? d->rank : d->dim) * elem_size(logit_dtype(d)), st);
     if (softmax && g->dgate && d->gate && !d->gate_per_token) zero_async(g->dgate, (size_t)d->heads * es, st);
     if (softmax && g->dbias && d->logit_bias) zero_async(g->dbias, (size_t)d->n_src * 4, st);
     return ATTNRES_OK;
@@ -604,7 +620,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       L.feat = feat;
       L.grid = (int)((f.n_items * streams + 3) / 4);
       L.lds = lr_fast_table_bytes() +
-              ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads)) + 4 * (size_t)PL.n_part) *
+              ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads + 1)) + 4 * (size_t)PL.n_part) *
                   sizeof(float);
       if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS", L.lds);
       // slot-major partials (R + few slots: one reduction workgroup per slot
@@ -666,7 +682,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     rp.part_extra = -1;
     rp.n_extra = 0;
     rp.dextra = nullptr;
-    err = launch_reduce_partials(d->dtype, rp, st);
+    err = launch_reduce_partials(logit_dtype(d), rp, st);  // the query gradient is in the logit dtype
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
   }
   return ATTNRES_OK;

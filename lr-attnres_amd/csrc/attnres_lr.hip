@@ -25,16 +25,25 @@ namespace attnres {
 
 constexpr int kSrcGroup = 8;
 
-// query element j of head h for token tok (fp32; composed queries are rounded
-// to the tensor dtype, as the reference casts the composed query)
+// Keys are read through the key dtype (p.kdt) and the logit path -- query,
+// rounded keys, logits and their gradients -- is rounded in the logit dtype
+// (p.ldt).  Both equal the value dtype unless keys of another dtype are read
+// (the reference norms such keys in fp32 and rounds them to the value dtype:
+// attnres_ops.py:4179-4186); the fast kernels handle only equal dtypes.
+__device__ __forceinline__ int dtype_bytes(int code) { return code == 0 ? 4 : 2; }
+
+// query element j of head h for token tok (fp32 of a logit-dtype value;
+// composed queries are rounded to that dtype, as the reference casts the
+// composed query)
 template <class DT>
 struct QueryView {
-  const typename DT::S* qs;
-  const typename DT::S* qd;
+  const void* qs;
+  const void* qd;
+  int ldt;
   float gf;
   __device__ __forceinline__ float at(int j) const {
-    float q = qs ? DT::load1(qs + j) : 0.f;
-    if (qd) q = DT::rnd(q + gf * DT::load1(qd + j));
+    float q = qs ? load_any(qs, j, ldt) : 0.f;
+    if (qd) q = round_any(q + gf * load_any(qd, j, ldt), ldt);
     return q;
   }
 };
@@ -42,9 +51,11 @@ struct QueryView {
 template <class DT>
 __device__ __forceinline__ QueryView<DT> query_view(const ReadParams& p, int64_t tok, int h) {
   using S = typename DT::S;
+  const int qb = dtype_bytes(p.ldt);
   QueryView<DT> v;
-  v.qs = p.q_static ? (const S*)p.q_static + h * p.rh : nullptr;
-  v.qd = p.q_dyn ? (const S*)p.q_dyn + tok * p.q_dyn_stride + h * p.rh : nullptr;
+  v.qs = p.q_static ? (const char*)p.q_static + (int64_t)h * p.rh * qb : nullptr;
+  v.qd = p.q_dyn ? (const char*)p.q_dyn + (tok * p.q_dyn_stride + (int64_t)h * p.rh) * qb : nullptr;
+  v.ldt = p.ldt;
   v.gf = 1.f;
   if (v.qd && p.gate) {
     const S* gp = (const S*)p.gate + (p.gate_per_token ? tok * p.H : 0) + h;
@@ -53,21 +64,28 @@ __device__ __forceinline__ QueryView<DT> query_view(const ReadParams& p, int64_t
   return v;
 }
 
-// Sum of squares of one key slice (rh elements).
+// byte address of the key slice of (source s, head h) for token tok
+__device__ __forceinline__ const char* key_slice(const ReadParams& p, int s, int64_t tok, int h) {
+  return (const char*)p.key[s] + (tok * (int64_t)p.kstride[s] + (int64_t)h * p.rh) * dtype_bytes(p.kdt);
+}
+
+// Sum of squares of one key slice (rh elements): 16-byte loads when the keys
+// have the value dtype and are aligned for them, else one element at a time.
 template <class DT>
-__device__ __forceinline__ float key_sumsq(const typename DT::S* kp, int rh, bool vec) {
+__device__ __forceinline__ float key_sumsq(const ReadParams& p, const char* kp) {
   constexpr int KV = 16 / (int)sizeof(typename DT::S);
+  const int rh = p.rh;
   float ss = 0.f;
-  if (vec) {
+  if (p.key_vec) {
     for (int j = 0; j < rh; j += KV) {
       float k[KV];
-      load_vec<DT, KV>(kp + j, k);
+      load_vec<DT, KV>((const typename DT::S*)kp + j, k);
 #pragma unroll
       for (int i = 0; i < KV; ++i) ss += k[i] * k[i];
     }
   } else {
     for (int j = 0; j < rh; ++j) {
-      const float k = DT::load1(kp + j);
+      const float k = load_any(kp, j, p.kdt);
       ss += k * k;
     }
   }
@@ -79,31 +97,30 @@ template <class DT>
 __device__ float lr_logit(const ReadParams& p, int64_t tok, int h, int s) {
   using S = typename DT::S;
   constexpr int KV = 16 / (int)sizeof(S);
-  const int rh = p.rh;
-  const S* kp = (const S*)p.key[s] + tok * (int64_t)p.kstride[s] + h * rh;
+  const int rh = p.rh, ldt = p.ldt;
+  const char* kp = key_slice(p, s, tok, h);
   const QueryView<DT> q = query_view<DT>(p, tok, h);
-  const bool vec = p.key_vec != 0;
   float inv = 1.f;
-  if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(kp, rh, vec) / (float)rh + p.eps);
+  if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(p, kp) / (float)rh + p.eps);
   float dot = 0.f;
-  if (vec) {
+  if (p.key_vec) {
     for (int j = 0; j < rh; j += KV) {
       float k[KV];
-      load_vec<DT, KV>(kp + j, k);
+      load_vec<DT, KV>((const S*)kp + j, k);
 #pragma unroll
       for (int i = 0; i < KV; ++i) {
-        const float kh = p.key_norm ? DT::rnd(k[i] * inv) : k[i];
+        const float kh = p.key_norm ? round_any(k[i] * inv, ldt) : k[i];
         dot += kh * q.at(j + i);
       }
     }
   } else {
     for (int j = 0; j < rh; ++j) {
-      float k = DT::load1(kp + j);
-      const float kh = p.key_norm ? DT::rnd(k * inv) : k;
+      float k = load_any(kp, j, p.kdt);
+      const float kh = p.key_norm ? round_any(k * inv, ldt) : k;
       dot += kh * q.at(j);
     }
   }
-  float logit = DT::rnd(DT::rnd(dot) * p.scale);
+  float logit = round_any(round_any(dot, ldt) * p.scale, ldt);
   if (p.bias) logit += p.bias[s];
   return logit;
 }
@@ -395,30 +412,33 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
       for (int t = 0; t < N; ++t) dot += s_p[h * N + t] * s_dw[h * N + t];
       const float dl = s_p[pi] * (s_dw[pi] - dot);
       s_dl[pi] = dl;
-      const float ge = DT::rnd(DT::rnd(dl) * p.scale);
+      const int ldt = p.ldt;
+      const float ge = round_any(round_any(dl, ldt) * p.scale, ldt);
       s_ge[pi] = ge;
 
-      const S* kp = (const S*)p.key[s] + tok * (int64_t)p.kstride[s] + h * rh;
+      const char* kp = key_slice(p, s, tok, h);
       const QueryView<DT> q = query_view<DT>(p, tok, h);
       float inv = 1.f;
-      if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(kp, rh, p.key_vec != 0) / (float)rh + p.eps);
+      if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(p, kp) / (float)rh + p.eps);
       float m = 0.f;
       for (int j = 0; j < rh; ++j) {
-        const float k = DT::load1(kp + j);
-        const float kh = p.key_norm ? DT::rnd(k * inv) : k;
+        const float k = load_any(kp, j, p.kdt);
+        const float kh = p.key_norm ? round_any(k * inv, ldt) : k;
         s_kh[s * R + h * rh + j] = kh;
-        if (p.key_norm) m += DT::rnd(ge * q.at(j)) * (k * inv);
+        if (p.key_norm) m += round_any(ge * q.at(j), ldt) * (k * inv);
       }
-      S* dkp = (S*)bp.dkey[s] + tok * (int64_t)R + h * rh;
+      // dk in the key dtype: the rms-norm backward of the rounded-key gradient
+      // (fp32), or that gradient itself without key_norm
+      void* dkp = (char*)bp.dkey[s] + (tok * (int64_t)R + h * rh) * dtype_bytes(p.kdt);
       const float mr = m / (float)rh;
       for (int j = 0; j < rh; ++j) {
-        const float dkh = DT::rnd(ge * q.at(j));
+        const float dkh = round_any(ge * q.at(j), ldt);
         float dk = dkh;
         if (p.key_norm) {
-          const float yk = DT::load1(kp + j) * inv;
-          dk = DT::rnd(inv * (dkh - yk * mr));
+          const float yk = load_any(kp, j, p.kdt) * inv;
+          dk = inv * (dkh - yk * mr);
         }
-        DT::store1(dkp + j, dk);
+        store_any(dkp, j, p.kdt, dk);
       }
     }
     team_sync(wpt);
@@ -428,12 +448,12 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
       const int h = j / rh;
       float a = 0.f;
       for (int s = 0; s < N; ++s) a += s_ge[h * N + s] * s_kh[s * R + j];
-      const float t = p.q_dyn ? DT::rnd(a) : a;
+      const float t = p.q_dyn ? round_any(a, p.ldt) : a;
       if (bp.part_q >= 0) s_acc[bp.part_q + j] += t;
       if (p.q_dyn) {
         const QueryView<DT> q = query_view<DT>(p, tok, h);
-        if (bp.dq_dyn) DT::store1((S*)bp.dq_dyn + tok * (int64_t)R + j, DT::rnd(q.gf * t));
-        if (p.gate) s_dq[j] = t * DT::load1(q.qd + (j - h * rh));
+        if (bp.dq_dyn) store_any(bp.dq_dyn, tok * (int64_t)R + j, p.ldt, round_any(q.gf * t, p.ldt));
+        if (p.gate) s_dq[j] = t * load_any(q.qd, j - h * rh, p.ldt);
       }
     }
     if (bp.part_bias >= 0) {

@@ -67,10 +67,12 @@ __device__ __forceinline__ uint64_t row_addr(uint64_t base, int64_t tok, uint32_
   return base + (uint64_t)(uint32_t)tok * strideb;
 }
 
-// byte address of source s's row for token tok (the table has kMaxSources
-// slots, so reading a slot past n_src is harmless; its value is never used)
+// byte address of source s's row for a wave-uniform token tok (the table
+// has kMaxSources slots, so reading a slot past n_src is harmless; its value
+// is never used).  The table entries move to scalar registers first, so the
+// address arithmetic runs on the scalar unit.
 __device__ __forceinline__ uint64_t row_base(const SrcTab* tab, int s, int64_t tok) {
-  return row_addr(tab->vptr[s], tok, tab->vstrb[s]);
+  return row_addr(uniform_u64(tab->vptr[s]), tok, uniform_u32(tab->vstrb[s]));
 }
 
 
@@ -189,10 +191,13 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   const int wslot = uniform_i32(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
-  // LDS: source tables | static query [R] | per wave: rounded weights [64]
+  __builtin_assume(N >= lr_fast_slot_floor(CB, RHC, NB));
+  // LDS: source tables | static query [R] | per wave: the softmax weights, 64
+  // words (16-bit types: the rounded weights of lanes 2i and 2i + 1 packed in
+  // word i; fp32: one word per lane)
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
-  float* s_w = s_q + R + wslot * 64;
+  uint32_t* s_w = (uint32_t*)(s_q + R) + wslot * 64;
   // slots past n_src repeat the last source, so the unrolled loads over NB
   // slots read the table at constant offsets (their values are never used)
   for (int i = threadIdx.x; i < kMaxSources; i += blockDim.x) {
@@ -224,6 +229,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   const bool has_static = p.q_static != nullptr;
   const uint64_t kbase = tab->kptr[ps] + (uint64_t)(ph * rh) * sizeof(S);
   const uint32_t kstrb = tab->kstrb[ps];
+  const float bias = (p.bias && has_pair) ? p.bias[ps] : 0.f;  // token-invariant
 
   // lanes past the row end load from the row start (valid memory) and store nothing
   int eoff[CB], hd[CB];
@@ -262,7 +268,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, t);
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
-      const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+      const S* vp = global_ptr<const S>(base[s]);
 #pragma unroll
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + eoff[c], vr[s][c]);
     }
@@ -278,8 +284,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
       QSlice<DT, RHC> q;
       token_query<DT, RHC>(qstat, qr, dyn, gf, q);
       const float dot = key_query_dot<DT, RHC>(kr, q, p.key_norm, inv, kch);
-      logit = DT::rnd(DT::rnd(dot) * p.scale);
-      if (p.bias) logit += p.bias[ps];
+      logit = DT::rnd(DT::rnd(dot) * p.scale) + bias;
     }
     // softmax over each head's np-lane group (lanes without a pair carry -inf / 0)
     const float lmax = group_max(logit, np);
@@ -287,10 +292,13 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     const float pw = ex / group_sum(ex, np);
     if constexpr (sizeof(S) == 2) {
       // 16-bit weights, zero for lanes without a pair (so an odd source count
-      // pairs its last source with a zero weight)
-      ((uint16_t*)s_w)[lane] = (uint16_t)(has_pair ? bits16<DT>(DT::rnd(pw)) : 0u);
+      // pairs its last source with a zero weight); even lanes store the word
+      // of their pair with lane + 1
+      const float wr = has_pair ? DT::rnd(pw) : 0.f;
+      const uint32_t hi = bits16<DT>(lane_xor1(wr));
+      if ((lane & 1) == 0) s_w[lane >> 1] = bits16<DT>(wr) | (hi << 16);
     } else {
-      if (has_pair) s_w[lane] = pw;
+      s_w[lane] = __float_as_uint(has_pair ? pw : 0.f);
     }
     wave_sync();
 
@@ -301,13 +309,12 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[c][e] = 0.f;
     if constexpr (sizeof(S) == 2) {
-      const uint32_t* s_wp = (const uint32_t*)s_w;
 #pragma unroll
       for (int s = 0; s < NB; s += 2) {
         if (s < N) {
 #pragma unroll
           for (int c = 0; c < CB; ++c) {
-            const uint32_t wp = s_wp[(hd[c] * np + s) >> 1];
+            const uint32_t wp = s_w[(hd[c] * np + s) >> 1];
 #pragma unroll
             for (int i = 0; i < E / 2; ++i) {
               acc[c][2 * i] = dot2<DT>(lo_pair(vr[s][c].w[i], vr[s + 1][c].w[i]), wp, acc[c][2 * i]);
@@ -324,7 +331,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
           for (int c = 0; c < CB; ++c) {
             float v[E];
             unpack<DT, E>(vr[s][c], v);
-            const float w = s_w[hd[c] * np + s];
+            const float w = __uint_as_float(s_w[hd[c] * np + s]);
 #pragma unroll
             for (int e = 0; e < E; ++e) acc[c][e] += w * v[e];
           }
@@ -360,6 +367,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     for (int c = 0; c < CB; ++c)
       if (ok[c]) store_vec<DT, E, true>(op + eoff[c], acc[c]);
     if (has_pair && p.weights) p.weights[(tok * H + ph) * N + ps] = pw;
+    wave_sync();  // this token's weights are read before the next token writes them
   }
 }
 
@@ -376,15 +384,18 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   const int wslot = uniform_i32(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
+  __builtin_assume(N >= lr_fast_slot_floor(CB, RHC, NB));
   // LDS: source tables | static query [R] | per wave: p [64], dW [64], dl [64],
   // contributions [nh*np][rh] | fold [nwaves][n_part]
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
-  const int wave_floats = 3 * 64 + p.np * p.nh * rh;
+  const int wave_floats = 3 * 64 + p.np * p.nh * (rh + 1);
   float* s_p = s_q + R + wslot * wave_floats;
   float* s_dw = s_p + 64;
   float* s_dl = s_dw + 64;
-  float* s_c = s_dl + 64;  // [npairs][rh] = ge * khat
+  // s_c rows are rh + 1 floats apart: with an odd stride the pair lanes' writes
+  // and the owner lanes' reads fall in distinct LDS banks
+  float* s_c = s_dl + 64;  // [npairs][rh + 1] = ge * khat
   float* s_fold = s_q + R + nwaves * wave_floats;
   for (int i = threadIdx.x; i < kMaxSources; i += blockDim.x) {
     const int j = min(i, N - 1);
@@ -480,7 +491,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
       for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, tok);
 #pragma unroll
       for (int s = 0; s < NB; ++s) {
-        const S* vp = global_ptr<const S>(uniform_u64(base[s]));
+        const S* vp = global_ptr<const S>(base[s]);
 #pragma unroll
         for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + eoff[c], vr[s][c]);
       }
@@ -580,7 +591,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
           for (int i = 0; i < KV; ++i) {
             const int jj = j * KV + i;
             const float kh = p.key_norm ? DT::rnd(k[i] * kinv) : k[i];
-            s_c[lane * rh + jj] = ge * kh;
+            s_c[lane * (rh + 1) + jj] = ge * kh;
             if (p.key_norm) {
               const float dkh = DT::rnd(ge * q.get(jj));
               m += dkh * (k[i] * kinv);
@@ -595,7 +606,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     // ---- query gradient and bias accumulation (owner lanes)
     float dqt = 0.f;
     if (q_owner) {
-      for (int s = 0; s < N; ++s) dqt += s_c[(qh * np + s) * rh + qj];
+      for (int s = 0; s < N; ++s) dqt += s_c[(qh * np + s) * (rh + 1) + qj];
       if (dyn) dqt = DT::rnd(dqt);
       qacc += dqt;
     }
@@ -625,14 +636,26 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
       if (s < N) {
-        S* dvp = global_ptr<S>(uniform_u64(row_addr(tab->dvptr[s], tok, rowb)));
+        S* dvp = global_ptr<S>(row_addr(uniform_u64(tab->dvptr[s]), tok, rowb));
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
           if (ok[c]) {
             const float w = DT::rnd(s_p[hd[c] * np + s]);
+            // 16-bit types: g again from its packed (dtype-exact) words, so
+            // the unpacked row is not held through the dW loop
+            float gv[E];
+            if constexpr (sizeof(S) == 2) {
+              Raw<DT, E> r;
+#pragma unroll
+              for (int i = 0; i < E / 2; ++i) r.w[i] = gpk[c][i];
+              unpack<DT, E>(r, gv);
+            } else {
+#pragma unroll
+              for (int e = 0; e < E; ++e) gv[e] = g[c][e];
+            }
             float dv[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) dv[e] = DT::rnd(w * g[c][e]);
+            for (int e = 0; e < E; ++e) dv[e] = DT::rnd(w * gv[e]);
             store_vec<DT, E, true>(dvp + eoff[c], dv);
           }
         }

@@ -19,6 +19,16 @@ constexpr int kMaxBwdGroups = 4096;
 constexpr int kFullBwdGroups = 2048;
 constexpr int kMaxFwdGroups = 65536;
 
+// Smallest source count for which the host launches a fast LR kernel with nb
+// value slots (it picks the smallest instantiated slot count that holds N:
+// 8/12/14/16/20/24/32 for one column and two key chunks, else 8/16/32).  The
+// kernels assume it, so their per-slot branches below it fold away.
+__host__ __device__ constexpr int lr_fast_slot_floor(int cb, int rhc, int nb) {
+  if (cb == 1 && rhc == 2)
+    return nb <= 8 ? 1 : nb <= 12 ? 9 : nb <= 14 ? 13 : nb <= 16 ? 15 : nb <= 20 ? 17 : nb <= 24 ? 21 : 25;
+  return nb <= 8 ? 1 : nb <= 16 ? 9 : 17;
+}
+
 struct ReadParams {
   const void* val[kMaxSources];
   const void* key[kMaxSources];
@@ -46,6 +56,8 @@ struct ReadParams {
   // with the same item index walk the tokens with stride `streams`
   int32_t n_items, nh, kch, streams;
   int32_t np;  // lanes per head in the (head, source) pair layout: next power of two >= n_src
+  int32_t kdt;  // dtype code of the LR keys and their gradients (the value dtype unless the desc says otherwise)
+  int32_t ldt;  // dtype code of the LR logit path: query, rounded keys, logits, their gradients
 };
 
 struct ReadBwdParams {

@@ -50,7 +50,7 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 4
+    assert lib.attnres_abi_version() == 5
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()
@@ -106,6 +106,7 @@ def _desc(n_src=3, n_tok=16, dim=64, rank=16, heads=2, **kw):
     d = H.ReadDesc()
     d.n_src, d.dtype, d.n_tok, d.dim, d.rank, d.heads = n_src, 1, n_tok, dim, rank, heads
     d.mode, d.key_norm, d.logit_scale, d.norm_eps = 0, 1, 0.25, H.FLT_EPSILON
+    d.key_dtype = 1
     d.values, d.value_row_stride = vals, vstr
     if rank:
         d.keys, d.key_row_stride = keys, kstr
@@ -126,6 +127,9 @@ def test_host_validation_rejects_bad_descriptions_without_launching():
         (dict(rank=0, heads=2), -1, b"heads == 1"),
         (dict(dtype=7), -1, b"dtype"),
         (dict(query=None), -1, b"query"),
+        (dict(key_dtype=9), -1, b"key dtype"),
+        (dict(key_dtype=0, gate=0x5000, query_dyn=0x6000, query_dyn_row_stride=16, gate_act=2), -2,
+         b"gated query needs keys in the value dtype"),
     ]
     for kw, code, msg in cases:
         n_src = kw.pop("n_src", 3)
@@ -356,3 +360,28 @@ def test_kernel_times_need_timing_enabled():
     buf = (ctypes.c_float * 4)()
     assert lib.attnres_kernel_times(buf, 4) == -1
     assert b"not enabled" in lib.attnres_last_error()
+
+
+def test_lrid_list_dims_within_triton_limits_keeps_the_reference_answers():
+    """tests/test_attnres_ops.py:515-520 of the reference, against the drop-in."""
+    values = [torch.empty(1, 1, 1024), torch.empty(1, 1, 1024)]
+    keys = [torch.empty(1, 1, 512), torch.empty(1, 1, 512)]
+    assert not ops._lrid_list_dims_within_triton_limits(values, keys, num_heads=1)
+    assert ops._lrid_list_dims_within_triton_limits(values, keys, num_heads=2)
+    assert ops._lrid_list_head_dims(values, keys, 3) is None
+    assert ops._lrid_list_head_dims(values, keys, "x") is None
+    assert ops._lrid_list_head_dims(values, keys, 4) == (256, 128)
+
+
+def test_mixed_dtype_sources_are_promoted_like_torch_stack():
+    a = torch.randn(1, 2, 8)
+    b = torch.randn(1, 2, 8).to(torch.bfloat16)
+    c = torch.randn(1, 2, 8).to(torch.float16)
+    out = ops._promote([b, a, c])
+    assert [t.dtype for t in out] == [torch.stack([b, a, c]).dtype] * 3
+    assert out[1] is a  # sources already in the common dtype are not copied
+    assert ops._promote([b, b])[0] is b
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attention_residual_read([a, b], torch.zeros(8), True)
+    with pytest.raises(RuntimeError, match="not supported"):
+        ops.attention_residual_read([a, a.double()], torch.zeros(8), True)

@@ -1,0 +1,172 @@
+"""GPU parity at the benchmark configurations' full sizes: every token of the
+HIP read (forward and backward, through the drop-in API) against the CPU
+oracle on the same seeded inputs, including the cross-token query and gate
+gradients.
+
+The fast kernels walk tokens in stride rounds (a wave processes token t, then
+t + streams, ...); comparing every token covers every round of the launch the
+benchmark times, not just the first.  Inputs are generated in fp32 on the CPU
+with a seeded generator and cast, in a fixed order (values, keys, query, gate,
+upstream gradient).  Tolerances are those of gpu_util.assert_close; its report
+lists how many elements exceed the flat 2e-2 bound (each checked to be a
+single-ulp case at a magnitude where one bf16 ulp exceeds 2e-2).
+"""
+
+import pytest
+import torch
+
+from oracle import attnres_oracle as O
+import attnres_ops as ops
+import _attnres_hip as H
+from gpu_util import DEV, assert_close, leaf
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    H.load()
+
+
+def _randn(g, shape, dtype, std=1.0):
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+def test_config1_full_size():
+    """C1: base read, fp32, B2 T128 d128 N4, rms-norm keys, q ~ N(0, 0.02)."""
+    g = torch.Generator().manual_seed(1)
+    B, T, D, S = 2, 128, 128, 4
+    vals = [_randn(g, (B, T, D), torch.float32) for _ in range(S)]
+    q = _randn(g, (D,), torch.float32, 0.02)
+    up = _randn(g, (B, T, D), torch.float32)
+    vd, qd = [leaf(x) for x in vals], leaf(q)
+    out = ops.attention_residual_read(vd, qd, True)
+    out.backward(up.to(DEV))
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    qc = q.clone().requires_grad_(True)
+    ref = O.attention_residual_read_ref(vc, qc, True)
+    ref.backward(up)
+    assert_close(out, ref, torch.float32, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, torch.float32, f"dv{s}")
+    assert_close(qd.grad, qc.grad, torch.float32, "dq")
+
+
+def c2_sources(g, B, T, D, n_blocks):
+    """C2's sources as its definition states: the token embedding and
+    ``n_blocks`` block summaries, each the sum of two N(0, 1) sublayer outputs
+    times count**-1 = 1/2, in bf16 arithmetic as the model forms them
+    (model.py:990-1001: partial sums in the model dtype, then the scale)."""
+    emb = _randn(g, (B, T, D), BF16)
+    out = [emb]
+    for _ in range(n_blocks):
+        a = _randn(g, (B, T, D), BF16)
+        b = _randn(g, (B, T, D), BF16)
+        out.append((a + b) * 0.5)
+    return out
+
+
+def test_config2_full_size_all_tokens():
+    """C2: base read, bf16, B8 T1024 d768, embedding + 6 two-output block
+    summaries, rms-norm keys; all 8192 tokens and the query gradient."""
+    g = torch.Generator().manual_seed(2)
+    B, T, D = 8, 1024, 768
+    vals = c2_sources(g, B, T, D, 6)
+    q = _randn(g, (D,), torch.float32, 0.02)
+    up = _randn(g, (B, T, D), BF16)
+    vd, qd = [leaf(x) for x in vals], leaf(q)
+    out = ops.attention_residual_read(vd, qd, True)
+    out.backward(up.to(DEV))
+    vc = [x.requires_grad_(True) for x in vals]
+    qc = q.clone().requires_grad_(True)
+    ref = O.attention_residual_read_ref(vc, qc, True)
+    ref.backward(up)
+    assert_close(out, ref, BF16, "out")
+    for s in range(len(vals)):
+        assert_close(vd[s].grad, vc[s].grad, BF16, f"dv{s}")
+    assert_close(qd.grad, qc.grad, BF16, "dq", reduced=True)
+
+
+def test_config3_full_size_all_tokens():
+    """C3 (the metric configuration): LR read, bf16, B8 T2048 d1024 N13 r64
+    H4, scale 0.25, rms-norm keys; all 16384 tokens (both stride rounds of the
+    fast kernels) and the static-query gradient over all of them."""
+    g = torch.Generator().manual_seed(3)
+    B, T, D, S, R, Hh = 8, 2048, 1024, 13, 64, 4
+    vals = [_randn(g, (B, T, D), BF16) for _ in range(S)]
+    keys = [_randn(g, (B, T, R), BF16) for _ in range(S)]
+    q = _randn(g, (Hh, R // Hh), torch.float32, 0.02)
+    up = _randn(g, (B, T, D), BF16)
+    vd, kd, qd = [leaf(x) for x in vals], [leaf(x) for x in keys], leaf(q)
+    out = ops.lrid_attention_residual_read(vd, kd, qd, Hh, 0.25, True)
+    out.backward(up.to(DEV))
+    vc = [x.requires_grad_(True) for x in vals]
+    kc = [x.requires_grad_(True) for x in keys]
+    qc = q.clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref(vc, kc, qc, Hh, 0.25, True)
+    ref.backward(up)
+    assert_close(out, ref, BF16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, BF16, f"dv{s}")
+        assert_close(kd[s].grad, kc[s].grad, BF16, f"dk{s}")
+    assert_close(qd.grad, qc.grad, BF16, "dq", reduced=True)
+
+
+def test_config3_full_size_without_key_norm():
+    """C3 with key_norm off (the configuration leaves it open): every token's
+    output and gradients, and the query gradient."""
+    g = torch.Generator().manual_seed(33)
+    B, T, D, S, R, Hh = 8, 2048, 1024, 13, 64, 4
+    vals = [_randn(g, (B, T, D), BF16) for _ in range(S)]
+    keys = [_randn(g, (B, T, R), BF16) for _ in range(S)]
+    q = _randn(g, (Hh, R // Hh), torch.float32, 0.02)
+    up = _randn(g, (B, T, D), BF16)
+    vd, kd, qd = [leaf(x) for x in vals], [leaf(x) for x in keys], leaf(q)
+    out = ops.lrid_attention_residual_read(vd, kd, qd, Hh, 0.25, False)
+    out.backward(up.to(DEV))
+    vc = [x.requires_grad_(True) for x in vals]
+    kc = [x.requires_grad_(True) for x in keys]
+    qc = q.clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref(vc, kc, qc, Hh, 0.25, False)
+    ref.backward(up)
+    assert_close(out, ref, BF16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, BF16, f"dv{s}")
+        assert_close(kd[s].grad, kc[s].grad, BF16, f"dk{s}")
+    assert_close(qd.grad, qc.grad, BF16, "dq", reduced=True)
+
+
+def test_config4_full_size_all_tokens():
+    """C4: LR read with a per-token sigmoid-gated dynamic query, bf16, B4 T4096
+    d2048 N17 r128 H8; all 16384 tokens (four stride rounds of the fast
+    backward), per-token query and gate gradients, and the static-query
+    gradient over all tokens."""
+    g = torch.Generator().manual_seed(4)
+    B, T, D, S, R, Hh = 4, 4096, 2048, 17, 128, 8
+    vals = [_randn(g, (B, T, D), BF16) for _ in range(S)]
+    keys = [_randn(g, (B, T, R), BF16) for _ in range(S)]
+    qs = _randn(g, (Hh, R // Hh), BF16, 0.02)
+    qdyn = _randn(g, (B, T, R), BF16)
+    gate = _randn(g, (B, T, Hh), BF16)
+    up = _randn(g, (B, T, D), BF16)
+    vd, kd = [leaf(x) for x in vals], [leaf(x) for x in keys]
+    qsd, qdd, gd = leaf(qs), leaf(qdyn), leaf(gate)
+    out = ops.lrid_attention_residual_read_gated(vd, kd, qsd, qdd, gd, Hh, 0.25, True, gate_activation="sigmoid")
+    out.backward(up.to(DEV))
+    vc = [x.requires_grad_(True) for x in vals]
+    kc = [x.requires_grad_(True) for x in keys]
+    qsc, qdc, gc = (x.clone().requires_grad_(True) for x in (qs, qdyn, gate))
+    qq = O.gated_query_ref(qsc.float(), qdc.float(), gc.float(), Hh, "sigmoid")
+    ref = O.lrid_attention_residual_read_ref(vc, kc, qq, Hh, 0.25, True)
+    ref.backward(up)
+    assert_close(out, ref, BF16, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, BF16, f"dv{s}")
+        assert_close(kd[s].grad, kc[s].grad, BF16, f"dk{s}")
+    assert_close(qdd.grad, qdc.grad, BF16, "dq_dyn")
+    assert_close(gd.grad, gc.grad, BF16, "dgate")
+    assert_close(qsd.grad, qsc.grad, BF16, "dq_static", reduced=True)

@@ -313,38 +313,6 @@ def test_base_row768_fp16_norm_counts():
     _base_case(805, torch.float16, 2, 4, 768, 7, True, normalize_output=True, counts=[1, 2, 2, 2, 2, 2, 2])
 
 
-def test_config2_full_size_token_subset():
-    """C2 (B8 T1024 d768 N7 bf16, rms-norm keys) at full size, checked on a
-    token subset; the query gradient over all tokens by linearity."""
-    g = gen(2)
-    B, T, D, S = 8, 1024, 768, 7
-    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
-    q = torch.randn(D, generator=g) * 0.02
-    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
-    vd = [leaf(x) for x in vals]
-    qd = leaf(q)
-    out = ops.attention_residual_read(vd, qd, True)
-    out.backward(up.to(DEV))
-    torch.cuda.synchronize()
-    sel = (slice(5, 6), slice(200, 264))
-    vc = [x[sel].clone().requires_grad_(True) for x in vals]
-    qc = q.clone().requires_grad_(True)
-    ref = O.attention_residual_read_ref(vc, qc, True)
-    ref.backward(up[sel])
-    assert_close(out[sel], ref, torch.bfloat16, "out")
-    for s in range(S):
-        assert_close(vd[s].grad[sel], vc[s].grad, torch.bfloat16, f"dv{s}")
-    halves = []
-    for part in (slice(0, 4), slice(4, 8)):
-        qh = leaf(q)
-        o = ops.attention_residual_read([x.detach()[part] for x in vd], qh, True)
-        o.backward(up[part].to(DEV))
-        halves.append(qh.grad)
-    full = qd.grad.float().cpu()
-    summed = (halves[0].float() + halves[1].float()).cpu()
-    assert float((full - summed).abs().max()) <= 2e-2 * max(1.0, float(full.abs().max()))
-
-
 def test_base_options():
     _base_case(801, torch.bfloat16, 2, 3, 64, 3, True, counts=[1, 3, 2])
     _base_case(802, torch.float32, 1, 4, 32, 4, True, bias=[0.0, 0.7, -0.3, 1.1])
@@ -490,81 +458,6 @@ def test_empty_and_single_source():
         ops.attention_residual_read([x] * 65, torch.randn(64, device=DEV), True)
 
 
-def test_config3_full_size_token_subset():
-    """C3 (B8 T2048 d1024 N13 r64 H4 bf16) at full size: tokens are independent,
-    so the oracle on a token subset checks the full-size launch exactly; the
-    static-query gradient over all tokens is checked by linearity (sum of the
-    gradients of two token halves)."""
-    g = gen(3)
-    B, T, D, S, R, Hh = 8, 2048, 1024, 13, 64, 4
-    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
-    keys = [torch.randn(B, T, R, generator=g).to(torch.bfloat16) for _ in range(S)]
-    q = (torch.randn(Hh, R // Hh, generator=g) * 0.02)
-    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
-    vd = [leaf(x) for x in vals]
-    kd = [leaf(x) for x in keys]
-    qd = leaf(q)
-    out = ops.lrid_attention_residual_read(vd, kd, qd, Hh, 0.25, True)
-    out.backward(up.to(DEV))
-    torch.cuda.synchronize()
-    sel = (slice(3, 4), slice(1000, 1064))
-    vc = [x[sel].clone().requires_grad_(True) for x in vals]
-    kc = [x[sel].clone().requires_grad_(True) for x in keys]
-    qc = q.clone().requires_grad_(True)
-    ref = O.lrid_attention_residual_read_ref(vc, kc, qc, Hh, 0.25, True)
-    ref.backward(up[sel])
-    assert_close(out[sel], ref, torch.bfloat16, "out")
-    for s in range(S):
-        assert_close(vd[s].grad[sel], vc[s].grad, torch.bfloat16, f"dv{s}")
-        assert_close(kd[s].grad[sel], kc[s].grad, torch.bfloat16, f"dk{s}")
-    # linearity of the cross-token reduction
-    halves = []
-    for part in (slice(0, 4), slice(4, 8)):
-        qh = leaf(q)
-        o = ops.lrid_attention_residual_read([x.detach()[part] for x in vd], [x.detach()[part] for x in kd], qh,
-                                             Hh, 0.25, True)
-        o.backward(up[part].to(DEV))
-        halves.append(qh.grad)
-    full = qd.grad.float().cpu()
-    summed = (halves[0].float() + halves[1].float()).cpu()
-    assert float((full - summed).abs().max()) <= 2e-2 * max(1.0, float(full.abs().max()))
-
-
-def test_config4_full_size_token_subset():
-    """C4 (B4 T4096 d2048 N17 r128 H8 bf16, per-token sigmoid-gated dynamic
-    query) at full size, checked on a token subset: output, value / key /
-    dynamic-query / gate gradients (all per token)."""
-    g = gen(4)
-    B, T, D, S, R, Hh = 4, 4096, 2048, 17, 128, 8
-    vals = [torch.randn(B, T, D, generator=g).to(torch.bfloat16) for _ in range(S)]
-    keys = [torch.randn(B, T, R, generator=g).to(torch.bfloat16) for _ in range(S)]
-    qs = (torch.randn(Hh, R // Hh, generator=g) * 0.02).to(torch.bfloat16)
-    qdyn = torch.randn(B, T, R, generator=g).to(torch.bfloat16)
-    gate = torch.randn(B, T, Hh, generator=g).to(torch.bfloat16)
-    up = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
-    vd = [leaf(x) for x in vals]
-    kd = [leaf(x) for x in keys]
-    qsd, qdd, gd = leaf(qs), leaf(qdyn), leaf(gate)
-    out = ops.lrid_attention_residual_read_gated(vd, kd, qsd, qdd, gd, Hh, 0.25, True, gate_activation="sigmoid")
-    out.backward(up.to(DEV))
-    torch.cuda.synchronize()
-    sel = (slice(2, 3), slice(4000, 4040))
-    vc = [x[sel].clone().requires_grad_(True) for x in vals]
-    kc = [x[sel].clone().requires_grad_(True) for x in keys]
-    qsc = qs.clone().requires_grad_(True)
-    qdc = qdyn[sel].clone().requires_grad_(True)
-    gc = gate[sel].clone().requires_grad_(True)
-    q = O.gated_query_ref(qsc.float(), qdc.float(), gc.float(), Hh, "sigmoid")
-    ref = O.lrid_attention_residual_read_ref(vc, kc, q, Hh, 0.25, True)
-    ref.backward(up[sel])
-    assert_close(out[sel], ref, torch.bfloat16, "out")
-    for s in range(S):
-        assert_close(vd[s].grad[sel], vc[s].grad, torch.bfloat16, f"dv{s}")
-        assert_close(kd[s].grad[sel], kc[s].grad, torch.bfloat16, f"dk{s}")
-    assert_close(qdd.grad[sel], qdc.grad, torch.bfloat16, "dq_dyn")
-    assert_close(gd.grad[sel], gc.grad, torch.bfloat16, "dgate")
-
-
 def test_bf16_rounding_ties_match_torch():
     """The kernels round to bf16 in hardware (v_cvt_pk_bf16_f32); check exact
     round-half-to-even ties against torch's rounding.  With a zero query the
@@ -587,3 +480,77 @@ def test_bf16_rounding_ties_match_torch():
     out_b = ops.attention_residual_read([va.to(DEV), vb.to(DEV)], torch.zeros(D, device=DEV), False)
     ref_b = O.attention_residual_read_ref([va, vb], torch.zeros(D), False)
     assert torch.equal(out_b.cpu(), ref_b)
+
+
+# ------------------------------------------------------------------ mixed dtypes
+
+@pytest.mark.parametrize("kdt,vdt", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.float16)])
+@pytest.mark.parametrize("key_norm", [True, False])
+@pytest.mark.parametrize("dynamic", [False, True])
+def test_lr_keys_in_another_dtype(kdt, vdt, key_norm, dynamic):
+    """Keys in another dtype than the values stay in their dtype: the eager
+    read norms them in fp32 and rounds them to the value dtype, so the logits
+    are a value-dtype contraction with key_norm and a key-dtype one without
+    it (attnres_ops.py:4179-4186); key gradients come back in the key dtype."""
+    g = gen(1300 + int(key_norm) + 2 * int(dynamic))
+    B, T, D, S, R, Hh = 2, 9, 256, 5, 64, 4
+    vals = [randn(g, (B, T, D), vdt) for _ in range(S)]
+    keys = [randn(g, (B, T, R), kdt) for _ in range(S)]
+    q = randn(g, (B, T, Hh, R // Hh) if dynamic else (Hh, R // Hh), torch.float32, 0.5)
+    up = randn(g, (B, T, D), vdt)
+    vd, kd, qd = [leaf(x) for x in vals], [leaf(x) for x in keys], leaf(q)
+    out = ops.lrid_attention_residual_read(vd, kd, qd, Hh, 0.25, key_norm)
+    out.backward(up.to(DEV))
+    vc = [x.clone().requires_grad_(True) for x in vals]
+    kc = [x.clone().requires_grad_(True) for x in keys]
+    qc = q.clone().requires_grad_(True)
+    ref = O.lrid_attention_residual_read_ref(vc, kc, qc, Hh, 0.25, key_norm)
+    ref.backward(up)
+    assert out.dtype == vdt and kd[0].grad.dtype == kdt
+    # every result is downstream of a 16-bit rounding (weights, dW, or the
+    # logits / rounded keys): the 16-bit bound of the coarser dtype applies
+    tol = torch.bfloat16 if torch.bfloat16 in (kdt, vdt) else torch.float16
+    assert_close(out, ref, tol, "out")
+    for s in range(S):
+        assert_close(vd[s].grad, vc[s].grad, tol, f"dv{s}")
+        assert_close(kd[s].grad, kc[s].grad, tol, f"dk{s}")
+    assert_close(qd.grad, qc.grad, tol, "dq", reduced=not dynamic)
+
+
+def test_mixed_dtype_source_lists_are_promoted():
+    """An fp32 embedding next to bf16 block summaries (what a bf16-autocast
+    model hands the read): the sources are read in their common dtype, as the
+    reference's eager read stacks them (attnres_ops.py:58-61, :2224, :3940),
+    for the base read, the LR read (bf16 keys) and phase 1 from logits."""
+    g = gen(1320)
+    B, T, D, S, R, Hh = 2, 6, 256, 5, 32, 2
+    vals = [randn(g, (B, T, D), torch.float32)] + [randn(g, (B, T, D), torch.bfloat16) for _ in range(S - 1)]
+    keys = [randn(g, (B, T, R), torch.bfloat16) for _ in range(S)]
+    qb = randn(g, (D,), torch.float32, 0.1)
+    ql = randn(g, (Hh, R // Hh), torch.float32, 0.5)
+    logits = randn(g, (3, S, B, T), torch.float32, 2.0)
+    up = randn(g, (B, T, D), torch.float32)
+    up1 = randn(g, (3, B, T, D), torch.float32)
+
+    def check(run_gpu, run_ref, name, with_keys=False, upstream=up):
+        vd, kd = [leaf(x) for x in vals], [leaf(x) for x in keys]
+        vc, kc = [x.clone().requires_grad_(True) for x in vals], [x.clone().requires_grad_(True) for x in keys]
+        out = run_gpu(vd, kd)
+        ref = run_ref(vc, kc)
+        assert out.dtype == torch.float32
+        out.backward(upstream.to(DEV))
+        ref.backward(upstream)
+        assert_close(out, ref, torch.float32, f"{name} out")
+        for s in range(S):
+            assert vd[s].grad.dtype == vals[s].dtype
+            assert_close(vd[s].grad, vc[s].grad, vals[s].dtype, f"{name} dv{s}")
+            if with_keys:
+                assert_close(kd[s].grad, kc[s].grad, torch.bfloat16, f"{name} dk{s}")
+
+    check(lambda v, k: ops.attention_residual_read(v, leaf(qb), True),
+          lambda v, k: O.attention_residual_read_ref(v, qb, True), "base")
+    check(lambda v, k: ops.lrid_attention_residual_read(v, k, leaf(ql), Hh, 0.25, True),
+          lambda v, k: O.lrid_attention_residual_read_ref(v, k, ql, Hh, 0.25, True), "lr", with_keys=True)
+    check(lambda v, k: ops.attention_residual_phase1_from_logits(v, logits.to(DEV))[0],
+          lambda v, k: O.phase1_from_logits_ref(v, logits)[0], "phase1", upstream=up1)
