@@ -319,33 +319,6 @@ __device__ __forceinline__ float wave_sums_get(const float (&z)[V / 4], int m) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(z[m >> 2]), 16 * row));
 }
 
-// Reduce-scatter inside aligned groups of W lanes (W = 2, 4, 8 or 16).  On
-// entry every lane holds W values a[0..W); on return lane i of a group holds
-// the sum over the group's lanes of a[i % W].  Each step pairs lane i with a
-// partner that differs in one more bit of i (i ^ 15, i ^ 7, i ^ 2, i ^ 1: the
-// row mirror, the half-row mirror and two quad permutes), keeps the half of
-// its values whose index bit equals that lane bit and adds the partner's copy
-// of the same half: W - 1 DPP adds and 2(W - 1) selects, no LDS round trip.
-// The association order is fixed, so results are deterministic.
-template <int HALF, int CTRL>
-__device__ __forceinline__ void rs_step(float* a, bool upper) {
-#pragma unroll
-  for (int m = 0; m < HALF; ++m) {
-    const float keep = upper ? a[HALF + m] : a[m];
-    const float send = upper ? a[m] : a[HALF + m];
-    a[m] = keep + dpp_f32<CTRL>(send);
-  }
-}
-template <int W>
-__device__ __forceinline__ float group_reduce_scatter(float (&a)[W], int lane) {
-  static_assert(W == 2 || W == 4 || W == 8 || W == 16, "reduce-scatter groups of 2, 4, 8 or 16 lanes");
-  if constexpr (W == 16) rs_step<8, kDppMirror>(a, (lane & 8) != 0);
-  if constexpr (W >= 8) rs_step<4, kDppHalfMirror>(a, (lane & 4) != 0);
-  if constexpr (W >= 4) rs_step<2, kDppXor2>(a, (lane & 2) != 0);
-  rs_step<1, kDppXor1>(a, (lane & 1) != 0);
-  return a[0];
-}
-
 __device__ __forceinline__ float group_max(float x, int width) {
   if (width > 1) x = fmaxf(x, dpp_f32<kDppXor1>(x));
   if (width > 2) x = fmaxf(x, dpp_f32<kDppXor2>(x));
