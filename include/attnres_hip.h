@@ -163,6 +163,23 @@ int attnres_read_backward(const attnres_read_desc* desc, const attnres_read_grad
  * (0 when no cross-token reduction is required).  Host-only; no GPU call. */
 size_t attnres_read_backward_workspace_size(const attnres_read_desc* desc);
 
+/*
+ * attnres_read_backward without a workspace and without allocating.  No
+ * counterpart in the reference (its backward allocates through PyTorch); it
+ * is for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same kernels
+ * and results as attnres_read_backward; grads->workspace is ignored and the
+ * cross-token partial sums go to a fixed array inside the library of
+ * ATTNRES_NOALLOC_SCRATCH_BYTES per GPU, which each GPU holds from the first
+ * call on it until the process ends.  A description whose partial sums need
+ * more (attnres_read_backward_workspace_size) fails with ATTNRES_EWORKSPACE.
+ * Calls no allocator.  Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (from other streams or threads) race.  No state
+ * carries from one call to the next.
+ */
+#define ATTNRES_NOALLOC_SCRATCH_BYTES (32u << 20)
+int attnres_read_backward_noalloc(const attnres_read_desc* desc, const attnres_read_grads* grads, void* stream);
+
 /* ------------------------------------------------------------------------
  * Cached-logit block-training schedule (two phases).
  *

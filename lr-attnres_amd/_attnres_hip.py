@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
 ABI_VERSION = 5
 MAX_SOURCES = 64
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 MODE_SOFTMAX, MODE_AVERAGE = 0, 1
@@ -197,6 +198,8 @@ def load() -> ctypes.CDLL:
     lib.attnres_read_backward.argtypes = [POINTER(ReadDesc), POINTER(ReadGrads), c_void_p]
     lib.attnres_read_backward_workspace_size.restype = c_size_t
     lib.attnres_read_backward_workspace_size.argtypes = [POINTER(ReadDesc)]
+    lib.attnres_read_backward_noalloc.restype = c_int
+    lib.attnres_read_backward_noalloc.argtypes = [POINTER(ReadDesc), POINTER(ReadGrads), c_void_p]
     lib.attnres_phase1_forward.restype = c_int
     lib.attnres_phase1_forward.argtypes = [POINTER(Phase1Desc), c_void_p, c_void_p, POINTER(c_float),
                                            POINTER(c_float), c_void_p]

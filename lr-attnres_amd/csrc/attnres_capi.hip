@@ -5,6 +5,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "attnres_launch.h"
@@ -686,6 +687,59 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
   }
   return ATTNRES_OK;
+}
+
+// ------------------------------------------------------- no-allocation backward
+// The backward's cross-token partial sums in a fixed array inside the library
+// instead of a caller workspace.  Each GPU holds its own copy from the first
+// call on it until the process ends.  In host code `scratch` is only a stand-in
+// for the device symbol: its device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current.  No call clears it:
+// every partial-sum slot the reduction reads is written by the same call.
+static __device__ __align__(256) unsigned char scratch[ATTNRES_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(ATTNRES_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(ATTNRES_EUNSUPPORTED, "device %d outside [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(ATTNRES_ELAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ATTNRES_OK;
+}
+
+}  // namespace
+
+extern "C" int attnres_read_backward_noalloc(const attnres_read_desc* d, const attnres_read_grads* g, void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!g) return fail(ATTNRES_EINVAL, "grads is NULL");
+  const size_t need = attnres_read_backward_workspace_size(d);
+  if (need > (size_t)ATTNRES_NOALLOC_SCRATCH_BYTES)
+    return fail(ATTNRES_EWORKSPACE, "this backward needs %zu bytes of partial sums; the no-allocation entry point "
+                "holds %zu (use attnres_read_backward with a workspace)", need, (size_t)ATTNRES_NOALLOC_SCRATCH_BYTES);
+  attnres_read_grads g2 = *g;
+  g2.workspace = nullptr;
+  g2.workspace_bytes = 0;
+  if (need > 0) {
+    rc = scratch_address(&g2.workspace);
+    if (rc) return rc;
+    g2.workspace_bytes = ATTNRES_NOALLOC_SCRATCH_BYTES;
+  }
+  return attnres_read_backward(d, &g2, stream);
 }
 
 // ====================================================================== phases

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
                             "attnres_keyed_split_forward", "attnres_keyed_split_backward",
                             "attnres_keyed_logits_forward", "attnres_keyed_logits_backward",
                             "attnres_keyed_logits_backward_workspace_size", "attnres_kernel_timing",
-                            "attnres_kernel_times"])
+                            "attnres_kernel_times", "attnres_read_backward_noalloc"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -385,3 +385,17 @@ def test_mixed_dtype_sources_are_promoted_like_torch_stack():
         ops.attention_residual_read([a, b], torch.zeros(8), True)
     with pytest.raises(RuntimeError, match="not supported"):
         ops.attention_residual_read([a, a.double()], torch.zeros(8), True)
+
+
+@needs_lib
+def test_noalloc_backward_rejects_needs_beyond_its_scratch_on_the_host():
+    """A base read with 4096 query slots over 4096 workgroups needs 64 MiB of
+    partial sums, twice the fixed array: refused before anything is launched."""
+    lib = H.load()
+    d = _desc(n_src=8, n_tok=65536, dim=4096, rank=0, heads=1)
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 4096 * 4096 * 4 > H.NOALLOC_SCRATCH_BYTES
+    g = H.ReadGrads()
+    assert lib.attnres_read_backward_noalloc(ctypes.byref(d), ctypes.byref(g), None) == -4
+    assert b"no-allocation entry point holds 33554432" in lib.attnres_last_error()
+    assert lib.attnres_read_backward_noalloc(ctypes.byref(d), None, None) == -1
+    assert lib.attnres_read_backward_noalloc(None, ctypes.byref(g), None) == -1
