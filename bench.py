@@ -51,7 +51,7 @@ CONFIGS = {
 # 6 blocks: up to 6 completed sources read by the 4 sites of the next block);
 # a step is phase 1 once + phase 2 at each of the Q sites, forward and backward
 PHASE_CONFIGS = {
-    "p5": dict(B=16, T=1024, D=768, S=6, Q=4, dtype=torch.bfloat16),
+    "p5": dict(B=16, T=1024, D=768, S=6, Q=4, R=64, dtype=torch.bfloat16),
 }
 
 
@@ -63,7 +63,14 @@ def phase_bytes_per_token(c):
     p1b = Q * D * s + Q * 4 + S * D * s + Q * S * 4 + S * D * s + Q * S * 4
     p2f = 2 * D * s + 4 + D * s
     p2b = 3 * D * s + 4 + 2 * D * s + 4
-    return dict(phase1_fwd=p1f, phase1_bwd=p1b, phase2_fwd=p2f, phase2_bwd=p2b)
+    # block accumulation, averaged over the Q sublayers of a block (the first has no
+    # partial block to read): fwd reads y[:, :D+R] (+ partial value and key) and writes
+    # value, key and the key's 1/rms; bwd reads both gradients, the raw key and 1/rms
+    # and writes the projection's gradient
+    R = c["R"]
+    acf = (D + R) * s + (Q - 1) / Q * (D + R) * s + (D + R) * s + 4
+    acb = (D + R) * s + R * s + 4 + (D + R) * s
+    return dict(phase1_fwd=p1f, phase1_bwd=p1b, phase2_fwd=p2f, phase2_bwd=p2b, accum_fwd=acf, accum_bwd=acb)
 
 
 class PhaseWorkload:
@@ -113,6 +120,20 @@ class PhaseWorkload:
         gr.workspace_bytes = ws
         self.gr = gr
         self.f = lambda t: ctypes.cast(ctypes.c_void_p(t.data_ptr()), ctypes.POINTER(ctypes.c_float))
+        # the block's Q sublayers grow the partial block from their fused projections
+        # [n, D + R]; the last completes it (scale 1/Q)
+        R = c["R"]
+        self.D, self.R = D, R
+        self.ys = [rn(n, D + R) for _ in range(Q)]
+        self.avals = [torch.empty((n, D), device=device, dtype=dt) for _ in range(Q)]
+        self.akeys = [torch.empty((n, R), device=device, dtype=dt) for _ in range(Q)]
+        self.ainv = [torch.empty((n, 1), device=device, dtype=torch.float32) for _ in range(Q)]
+        self.agv = [rn(n, D) for _ in range(Q)]
+        self.agk = [rn(n, R) for _ in range(Q)]
+        self.agy = [torch.empty((n, D + R), device=device, dtype=dt) for _ in range(Q)]
+        self.adesc = [H.block_accum_desc(self.ys[q], D, R, 1, True, self.avals[q - 1] if q else None,
+                                         self.akeys[q - 1] if q else None, q == Q - 1, False, False, 1.0 / Q, None)
+                      for q in range(Q)]
 
     def _ok(self, rc):
         if rc:
@@ -135,13 +156,26 @@ class PhaseWorkload:
         for d in self.p2:
             self._ok(self.lib.attnres_phase2_backward(ctypes.byref(d.c), ctypes.byref(self.gr), sv))
 
+    def accum_fwd(self, sv):
+        for q, d in enumerate(self.adesc):
+            self._ok(self.lib.attnres_block_accum_forward(ctypes.byref(d), ctypes.c_void_p(self.avals[q].data_ptr()),
+                                                          ctypes.c_void_p(self.akeys[q].data_ptr()),
+                                                          self.f(self.ainv[q]), None, sv))
+
+    def accum_bwd(self, sv):
+        for q in reversed(range(len(self.adesc))):
+            self._ok(self.lib.attnres_block_accum_backward(
+                ctypes.byref(self.adesc[q]), ctypes.c_void_p(self.agv[q].data_ptr()), self.D,
+                ctypes.c_void_p(self.agk[q].data_ptr()), self.f(self.ainv[q]), None,
+                ctypes.c_void_p(self.agy[q].data_ptr()), None, None, None, 0, sv))
+
 
 def bench_phase(args, dev):
     c = PHASE_CONFIGS[args.config]
     wl = PhaseWorkload(c, dev)
     stream = torch.cuda.current_stream(dev)
     sv = ctypes.c_void_p(stream.cuda_stream)
-    parts = ("phase1_fwd", "phase1_bwd", "phase2_fwd", "phase2_bwd")
+    parts = ("phase1_fwd", "phase1_bwd", "phase2_fwd", "phase2_bwd", "accum_fwd", "accum_bwd")
     for _ in range(args.warmup):
         for k in parts:
             getattr(wl, k)(sv)
@@ -168,17 +202,20 @@ def bench_phase(args, dev):
     kern = {}
     for k in parts:
         ms = sum(a.elapsed_time(b) for a, b in ev[k]) / args.steps
-        calls = c["Q"] if k.startswith("phase2") else 1
+        calls = c["Q"] if k.startswith(("phase2", "accum")) else 1
         gbs = bpt[k] * wl.n_tok * calls / (ms / 1e3) / 1e9
         kern[k] = {"ms": round(ms, 5), "calls": calls, "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
                    "bytes_per_token": bpt[k]}
     print(json.dumps({
-        "metric": "cached-logit block schedule (phase 1 + Q phase-2 merges) fwd+bwd tokens/s",
+        "metric": "cached-logit block schedule (phase 1 + Q phase-2 merges + Q partial-block accumulations) "
+                  "fwd+bwd tokens/s",
         "value": round(wl.n_tok / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q']} x phase2 (base, key_norm) "
-                               f"B{c['B']} T{c['T']} d{c['D']}", "tokens": wl.n_tok},
+                               f"+ {c['Q']} x block accumulation (r{c['R']}, key_norm, the last completing "
+                               f"the block) B{c['B']} T{c['T']} d{c['D']}", "tokens": wl.n_tok,
+                   "phase_ms": round(sum(kern[k]["ms"] for k in parts if k.startswith("phase")), 5)},
         "kernels": kern}))
 
 

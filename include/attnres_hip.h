@@ -293,7 +293,8 @@ typedef struct attnres_phase2_desc {
   float logit_bias;               /* constant fp32 logit bias (used when logit_bias_dev is NULL) */
   const float* logit_bias_dev;    /* device fp32 scalar bias (learned), or NULL */
   float value_scale;              /* block-summary multiplier of the partial value (1 = none) */
-  const float* value_scale_dev;   /* device fp32 scalar multiplier (learned), or NULL */
+  const float* value_scale_dev;   /* device fp32 scalar multiplier (learned), or NULL; rounded to
+                                     the dtype before it scales (model.py:983-985) */
   int32_t scale_key;              /* LR: multiply the partial key by the same scale */
   const void* partial_value;      /* [n_tok] rows of dim */
   int64_t partial_value_row_stride;
@@ -387,6 +388,62 @@ int attnres_keyed_split_forward(const attnres_keyed_split_desc* desc, void* out,
  * two slice copies and their sum) with one pass. */
 int attnres_keyed_split_backward(const attnres_keyed_split_desc* desc, const void* grad_out, const void* grad_key,
                                  const float* key_inv_rms, void* grad_projected, void* stream);
+
+/*
+ * Block-summary accumulation fused into the key-producer epilogue.
+ *
+ * In the block schedule a sublayer's output and LR key are used only to grow
+ * the live partial block (model.py:2377-2389, 2451-2463):
+ *     partial_value' = partial_value + y[:, :dim]
+ *     partial_key'   = partial_key + key(y)          (key as attnres_keyed_split_forward)
+ * and at a block end the block becomes a source (model.py:990-1028):
+ *     value = partial_value' * scale                 (scale = count^-alpha, or a learned scale)
+ *           = rms_norm(partial_value')               (value_norm; the key is then left as is)
+ *     key   = partial_key' (* scale when scale_key: keys that are not rms-normed)
+ * One pass over y writes partial_value' / partial_key' (complete == 0) or the
+ * block source (complete == 1), so the sublayer output is never written out
+ * on its own and the partial block is read and written once per sublayer.
+ * Every sum and product is rounded to the dtype as the reference's eager ops
+ * round it; a NULL partial (the first sublayer of a block) adds nothing.
+ */
+typedef struct attnres_block_accum_desc {
+  attnres_keyed_split_desc split;  /* the sublayer's fused projection y */
+  int32_t complete;                /* 1: form the completed block source */
+  const void* partial_value;       /* [n_tok, dim] dense, or NULL */
+  const void* partial_key;         /* [n_tok, rank] dense, or NULL */
+  int32_t value_norm;              /* complete: rms-norm the value instead of scaling it */
+  int32_t scale_key;               /* complete (without value_norm): scale the key as well */
+  float value_scale;               /* complete: the scale (used when value_scale_dev is NULL) */
+  const float* value_scale_dev;    /* complete: learned scale, fp32 device scalar, or NULL;
+                                      rounded to the dtype before it scales (model.py:983-985) */
+} attnres_block_accum_desc;
+
+/* value_out [n_tok, dim] and key_out [n_tok, rank] (dense, dtype);
+ * key_inv_rms [n_tok, heads] fp32 when split.key_norm; value_inv_rms [n_tok]
+ * fp32 when complete and value_norm (both for the backward; may be NULL when
+ * none follows).  Replaces the slice / key norm of LRIDFusedProjection
+ * (model.py:363-388) followed by the partial-block adds and
+ * _attnres_block_summary / _lrid_block_source (model.py:990-1028). */
+int attnres_block_accum_forward(const attnres_block_accum_desc* desc, void* value_out, void* key_out,
+                                float* key_inv_rms, float* value_inv_rms, void* stream);
+
+/* Workspace bytes of attnres_block_accum_backward (nonzero only for a learned
+ * scale, whose gradient is a deterministic sum over tokens).  Host-only. */
+size_t attnres_block_accum_backward_workspace_size(const attnres_block_accum_desc* desc);
+
+/* Gradients from grad_value (rows grad_value_row_stride elements apart) and
+ * grad_key (dense) -- either may be NULL (zero):
+ *   grad_projected [n_tok, proj_cols] dense: columns [0, dim) the gradient of
+ *     partial_value' (which is also the gradient of partial_value: read it
+ *     there), [dim, dim + rank) that of the key through its norm, the rest 0;
+ *   grad_partial_key [n_tok, rank]: written only when complete and scale_key
+ *     (otherwise the partial key's gradient is grad_key itself);
+ *   grad_value_scale: fp32 scalar, the learned scale's gradient (NULL: not wanted).
+ * key_inv_rms / value_inv_rms: the forward's. */
+int attnres_block_accum_backward(const attnres_block_accum_desc* desc, const void* grad_value,
+                                 int64_t grad_value_row_stride, const void* grad_key, const float* key_inv_rms,
+                                 const float* value_inv_rms, void* grad_projected, void* grad_partial_key,
+                                 float* grad_value_scale, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -179,6 +179,13 @@ class KeyedSplitDesc(ctypes.Structure):
                 ("projected", c_void_p), ("row_stride", c_int64)]
 
 
+class BlockAccumDesc(ctypes.Structure):
+    """attnres_block_accum_desc (include/attnres_hip.h)."""
+    _fields_ = [("split", KeyedSplitDesc), ("complete", c_int32), ("partial_value", c_void_p),
+                ("partial_key", c_void_p), ("value_norm", c_int32), ("scale_key", c_int32),
+                ("value_scale", c_float), ("value_scale_dev", POINTER(c_float))]
+
+
 def load() -> ctypes.CDLL:
     """Load the HIP library once; raise with a build hint if it is missing."""
     global _lib
@@ -225,6 +232,15 @@ def load() -> ctypes.CDLL:
     lib.attnres_keyed_split_backward.restype = c_int
     lib.attnres_keyed_split_backward.argtypes = [POINTER(KeyedSplitDesc), c_void_p, c_void_p, POINTER(c_float),
                                                  c_void_p, c_void_p]
+    lib.attnres_block_accum_forward.restype = c_int
+    lib.attnres_block_accum_forward.argtypes = [POINTER(BlockAccumDesc), c_void_p, c_void_p, POINTER(c_float),
+                                                POINTER(c_float), c_void_p]
+    lib.attnres_block_accum_backward_workspace_size.restype = c_size_t
+    lib.attnres_block_accum_backward_workspace_size.argtypes = [POINTER(BlockAccumDesc)]
+    lib.attnres_block_accum_backward.restype = c_int
+    lib.attnres_block_accum_backward.argtypes = [POINTER(BlockAccumDesc), c_void_p, c_int64, c_void_p,
+                                                 POINTER(c_float), POINTER(c_float), c_void_p, c_void_p,
+                                                 POINTER(c_float), c_void_p, c_size_t, c_void_p]
     lib.attnres_kernel_timing.restype = c_int
     lib.attnres_kernel_timing.argtypes = [c_int]
     lib.attnres_kernel_times.restype = c_int
@@ -651,3 +667,54 @@ def keyed_split_backward(y2d, n: int, P: int, dim: int, rank: int, heads: int, k
                                           _fptr(inv) if key_norm else None, _ptr(gy), _stream(device))
     _check(rc, "keyed split backward")
     return gy
+
+
+def block_accum_desc(y2d, dim: int, rank: int, heads: int, key_norm: bool, partial_value, partial_key,
+                     complete: bool, value_norm: bool, scale_key: bool, scale_value: float, scale_tensor):
+    """Descriptor of one block accumulation over a projection y [n_tok, proj_cols]; partial rows dense."""
+    n, P = y2d.size(0), y2d.size(1)
+    d = BlockAccumDesc()
+    d.split = keyed_split_desc(y2d.dtype, n, P, y2d.stride(0) if n > 1 else P, y2d.data_ptr() if n else None, dim,
+                               rank, heads, key_norm)
+    d.complete = int(bool(complete))
+    d.partial_value = partial_value.data_ptr() if partial_value is not None else None
+    d.partial_key = partial_key.data_ptr() if partial_key is not None else None
+    d.value_norm = int(bool(value_norm))
+    d.scale_key = int(bool(scale_key))
+    d.value_scale = float(scale_value)
+    d.value_scale_dev = _fptr(scale_tensor)
+    return d
+
+
+def block_accum_forward(d: BlockAccumDesc, device, dtype, dim: int, rank: int, heads: int, key_norm: bool,
+                        value_norm: bool):
+    """(value [n, dim], key [n, rank], key_inv_rms [n, heads] | [0], value_inv_rms [n] | [0])."""
+    lib = load()
+    n = d.split.n_tok
+    value = torch.empty((n, dim), device=device, dtype=dtype)
+    key = torch.empty((n, rank), device=device, dtype=dtype)
+    kinv = torch.empty((n, heads) if key_norm else (0,), device=device, dtype=torch.float32)
+    vinv = torch.empty((n,) if value_norm else (0,), device=device, dtype=torch.float32)
+    rc = lib.attnres_block_accum_forward(ctypes.byref(d), _ptr(value), _ptr(key), _fptr(kinv) if key_norm else None,
+                                         _fptr(vinv) if value_norm else None, _stream(device))
+    _check(rc, "block accumulation forward")
+    return value, key, kinv, vinv
+
+
+def block_accum_backward(d: BlockAccumDesc, device, dtype, grad_value, grad_key, kinv, vinv, want_dpk: bool,
+                         want_dscale: bool):
+    """(grad_projected [n, proj_cols], grad_partial_key [n, rank] | None, grad_scale fp32 [1] | None).
+    grad_value may be a row-strided [n, dim] view."""
+    lib = load()
+    n, P = d.split.n_tok, d.split.proj_cols
+    gy = torch.empty((n, P), device=device, dtype=dtype)
+    dpk = torch.empty((n, d.split.rank), device=device, dtype=dtype) if want_dpk else None
+    ds = torch.empty((1,), device=device, dtype=torch.float32) if want_dscale else None
+    ws_bytes = lib.attnres_block_accum_backward_workspace_size(ctypes.byref(d)) if want_dscale else 0
+    ws = torch.empty((max(1, ws_bytes),), device=device, dtype=torch.uint8) if ws_bytes else None
+    rc = lib.attnres_block_accum_backward(
+        ctypes.byref(d), _ptr(grad_value), grad_value.stride(0) if grad_value is not None else 0, _ptr(grad_key),
+        _fptr(kinv) if kinv is not None and kinv.numel() else None, _fptr(vinv) if vinv is not None and vinv.numel() else None,
+        _ptr(gy), _ptr(dpk), _fptr(ds), _ptr(ws), ws_bytes, _stream(device))
+    _check(rc, "block accumulation backward")
+    return gy, dpk, ds

@@ -26,7 +26,10 @@ head, static queries, projection keys; no KV cache, no base AttnRes, no
 split-sublayer mode), and the live partial block is handed to phase 2 raw
 with ``partial_scale = count**-alpha`` instead of being multiplied out first
 (``fold_block_summary``; the result is bit-identical, the kernel applies the
-same rounding).  Module and parameter names match the reference's, so a
+same rounding), and with pre-norm sublayers each sublayer's fused projection
+goes straight into ``lrid_block_accumulate``, which splits it, norms the key,
+adds both to the partial block and, at a block end, forms the block source in
+one pass (``fuse_block_accumulation``; bit-identical too).  Module and parameter names match the reference's, so a
 reference state dict for this configuration loads with ``load_state_dict``.
 
 The read functions are looked up on ``ops`` (default: the HIP-backed
@@ -101,6 +104,7 @@ class DecoderConfig:
     lrid_use_logit_scale: bool = True
     lrid_logit_scale: Optional[float] = None
     fold_block_summary: bool = True
+    fuse_block_accumulation: bool = True
 
     def __post_init__(self):
         if self.norm_pos not in {"before", "after", "both"}:
@@ -193,8 +197,13 @@ class KeyedOutputProjection(nn.Module):
         self.key_norm = config.attnres_key_norm
         self.ops = ops
         self.proj = nn.Linear(input_dim, output_dim + config.lrid_projection_rank, bias=False)
+        # set by the decoder when it folds the projection into the partial block itself
+        self.emit_projection = False
 
     def forward(self, x: Tensor):
+        """``(output, key)``, or ``(projection, None)`` with ``emit_projection``."""
+        if self.emit_projection:
+            return self.proj(x), None
         return self.ops.lrid_fused_projection_split(self.proj(x), self.output_dim, self.rank, self.heads,
                                                     self.key_norm)
 
@@ -333,6 +342,10 @@ class Decoder(nn.Module):
             modules["lrid_queries"] = nn.ParameterList(
                 [nn.Parameter(torch.empty(config.lrid_num_heads, head_dim)) for _ in range(2 * config.n_layer)])
         self.transformer = nn.ModuleDict(modules)
+        if self._fused_accumulation():
+            for layer in self.transformer.layers:
+                layer.attn.c_proj.emit_projection = True
+                layer.mlp.fc2.emit_projection = True
         if not config.weight_tying:
             self.lm_head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
         self.reset_parameters()
@@ -386,6 +399,13 @@ class Decoder(nn.Module):
         """Reads return the normed input of the next sublayer (``model.py:2238-2244``)."""
         c = self.config
         return c.norm_pos == "before" and c.attnres_fuse_read_norm and c.lrid_num_heads == 1
+
+    def _fused_accumulation(self) -> bool:
+        """Sublayers hand over their projection and ``lrid_block_accumulate`` grows the
+        partial block from it; only for pre-norm sublayers (a post-norm acts on the
+        output before it is added)."""
+        c = self.config
+        return c.use_attnres and c.fuse_block_accumulation and c.norm_pos == "before"
 
     def _block_scale(self, count: int) -> float:
         """``count ** -alpha`` (``model.py:955-959``, ``:979-988``)."""
@@ -485,20 +505,34 @@ class Decoder(nn.Module):
             return phase2(value, key, q, inter, lse, c.lrid_logit_scale, c.attnres_key_norm,
                           normalize_output=fused_norm, logit_bias=self._count_bias(count))
 
-        def add(out: Tensor, key: Tensor, site_after: int):
+        def add(out: Tensor, key: Optional[Tensor], site_after: int):
             nonlocal partial, partial_key, count, phase
-            if partial is None:
-                partial, partial_key, count = out, key, 1
+            complete = site_after in self.block_ends
+            if key is None:
+                # ``out`` is the sublayer's fused projection: split, key norm, partial-block add
+                # and, at a block end, the block source in one pass (model.py:2377-2389, 1003-1018)
+                value, key = ops.lrid_block_accumulate(
+                    out, partial, partial_key, c.n_embd, rank, c.lrid_num_heads, c.attnres_key_norm,
+                    complete=complete, partial_scale=self._block_scale(count + 1) if complete else 1.0,
+                    scale_key=complete and not c.attnres_key_norm)
+                if not complete:
+                    partial, partial_key, count = value, key, count + 1
+                    return
+                count += 1
             else:
-                partial, partial_key, count = partial + out, partial_key + key, count + 1
-            if site_after in self.block_ends:
+                if partial is None:
+                    partial, partial_key, count = out, key, 1
+                else:
+                    partial, partial_key, count = partial + out, partial_key + key, count + 1
+                if not complete:
+                    return
                 value, key = summary(partial, partial_key, count)
-                done_values.append(value)
-                done_logits.append(site_logits(value, key, site_after, count))
-                done_first.append(site_after)
-                partial = partial_key = None
-                count = 0
-                phase = None
+            done_values.append(value)
+            done_logits.append(site_logits(value, key, site_after, count))
+            done_first.append(site_after)
+            partial = partial_key = None
+            count = 0
+            phase = None
 
         for layer_idx, block in enumerate(self.transformer.layers):
             h = read(2 * layer_idx)

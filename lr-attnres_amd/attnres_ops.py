@@ -1121,3 +1121,109 @@ def lrid_fused_projection_split(projected: Tensor, output_dim: int, rank: int, n
     else:
         out, key = _KeySplitFn.apply((int(output_dim), int(rank), int(num_heads), bool(key_norm)), y)
     return out.view(*lead, output_dim), key.view(*lead, rank)
+
+
+# ------------------------------------------------------------------ block-summary accumulation
+
+class _BlockAccumFn(torch.autograd.Function):
+    """Eager autograd of the fused block accumulation: inputs (meta, y [n, P],
+    partial value rows [n, D] | None, partial key rows [n, R] | None, learned
+    scale fp32 [1] | None); outputs (value [n, D], key [n, R])."""
+
+    @staticmethod
+    def forward(ctx, meta, y, pv, pk, scale_t):
+        dim, rank, heads, key_norm, complete, value_norm, scale_key, scale_value = meta
+        ctx.set_materialize_grads(False)
+        d = _hip.block_accum_desc(y, dim, rank, heads, key_norm, pv, pk, complete, value_norm, scale_key,
+                                  scale_value, scale_t)
+        with _device_ctx(y.device):
+            value, key, kinv, vinv = _hip.block_accum_forward(d, y.device, y.dtype, dim, rank, heads, key_norm,
+                                                              complete and value_norm)
+        ctx.meta = meta
+        ctx.desc = d
+        ctx.save_for_backward(y, pv, pk, scale_t, kinv, vinv)
+        return value, key
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, g_value, g_key):
+        y, pv, pk, scale_t, kinv, vinv = ctx.saved_tensors
+        dim, rank, heads, key_norm, complete, value_norm, scale_key, scale_value = ctx.meta
+        if g_value is None and g_key is None:
+            return None, None, None, None, None
+        want = ctx.needs_input_grad  # (meta, y, pv, pk, scale)
+        if g_value is not None and g_value.stride(-1) != 1:
+            g_value = g_value.contiguous()
+        gk = g_key.contiguous() if g_key is not None else None
+        key_scaled = complete and scale_key and not value_norm
+        with _device_ctx(y.device):
+            gy, dpk, ds = _hip.block_accum_backward(ctx.desc, y.device, y.dtype, g_value, gk, kinv, vinv,
+                                                    want_dpk=key_scaled and pk is not None and want[3] and gk is not None,
+                                                    want_dscale=scale_t is not None and want[4])
+        # the grown partial value's gradient is also the partial value's: columns [0, D) of gy
+        # (or the incoming gradient itself when nothing scales or norms it)
+        d_pv = None
+        if pv is not None and want[2] and g_value is not None:
+            d_pv = gy[:, :dim] if complete else g_value
+        d_pk = None
+        if pk is not None and want[3] and gk is not None:
+            d_pk = dpk if key_scaled else gk
+        d_s = ds.reshape(scale_t.shape) if ds is not None else None
+        return None, gy if want[1] else None, d_pv, d_pk, d_s
+
+
+def lrid_block_accumulate(projected: Tensor, partial_value: Optional[Tensor], partial_key: Optional[Tensor],
+                          output_dim: int, rank: int, num_heads: int = 1, key_norm: bool = True,
+                          complete: bool = False, partial_scale=1.0, value_norm: bool = False,
+                          scale_key: bool = False):
+    """A sublayer's fused projection added to the live partial block in one pass.
+
+    Not in the reference's op module: the reference model splits the projection
+    (``LRIDFusedProjection.forward``, model.py:363-388, as
+    ``lrid_fused_projection_split``), then adds the output and key to the
+    partial block eagerly (model.py:2377-2389, 2451-2463) and, at a block end,
+    forms the block source with ``_attnres_block_summary`` /
+    ``_lrid_block_source`` (model.py:990-1028).  Here::
+
+        partial_value' = partial_value + projected[..., :D]
+        partial_key'   = partial_key + key(projected)    (per-head rms-norm when key_norm)
+
+    and with ``complete`` the block source instead:
+    ``value = partial_value' * partial_scale`` (float or learned scalar tensor;
+    ``rms_norm(partial_value')`` with ``value_norm``) and ``key = partial_key'``
+    (``* partial_scale`` with ``scale_key``, the model's rule for keys that are
+    not rms-normed).  ``partial_value`` / ``partial_key`` are None for the first
+    sublayer of a block.  Every add and product rounds to the dtype as the
+    eager ops do.  Returns ``(value [..., D], key [..., rank])``.
+    """
+    P = projected.size(-1)
+    if P < output_dim + rank:
+        raise RuntimeError(f"lrid_block_accumulate: projection has {P} columns, needs at least {output_dim + rank}")
+    if projected.dtype not in _ALLOWED:
+        raise RuntimeError(f"lrid_block_accumulate: dtype {projected.dtype} is not supported (fp32, bf16, fp16)")
+    if not complete and (value_norm or scale_key or isinstance(partial_scale, Tensor) or float(partial_scale) != 1.0):
+        raise RuntimeError("lrid_block_accumulate: partial_scale / value_norm / scale_key apply to complete=True only")
+    if value_norm and scale_key:
+        raise RuntimeError("lrid_block_accumulate: value_norm leaves the key unscaled")
+    lead = projected.shape[:-1]
+    n = projected.numel() // P
+    tensors = [projected] + [t for t in (partial_value, partial_key) if t is not None]
+    dev = _check_gpu(tensors, "lrid_block_accumulate")
+    y = projected.reshape(n, P)
+    if y.stride(-1) != 1:
+        y = y.contiguous()
+
+    def rows(t, width, what):
+        if t is None:
+            return None
+        if t.dtype != projected.dtype or t.numel() != n * width:
+            raise RuntimeError(f"lrid_block_accumulate: {what} must be {tuple(lead) + (width,)} in {projected.dtype}")
+        return t.reshape(n, width).contiguous()
+
+    pv = rows(partial_value, output_dim, "partial_value")
+    pk = rows(partial_key, rank, "partial_key")
+    scale_value, scale_t = (1.0, None) if not complete or value_norm else _scalar_arg(partial_scale, dev, "partial_scale")
+    meta = (int(output_dim), int(rank), int(num_heads), bool(key_norm), bool(complete), bool(value_norm),
+            bool(scale_key), scale_value)
+    value, key = _BlockAccumFn.apply(meta, y, pv, pk, scale_t)
+    return value.view(*lead, output_dim), key.view(*lead, rank)

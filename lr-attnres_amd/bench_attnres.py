@@ -69,6 +69,7 @@ def parse_args(argv=None):
     p.add_argument("--attnres_training_torch_phase2", type=_bool, default=True)
     p.add_argument("--attnres_fuse_read_norm", type=_bool, default=True)
     p.add_argument("--fold_block_summary", type=_bool, default=True)
+    p.add_argument("--fuse_block_accumulation", type=_bool, default=True)
     p.add_argument("--dtype", choices=("fp32", "bf16", "fp16"), default="bf16")
     p.add_argument("--phase", choices=("forward", "train"), default="train")
     p.add_argument("--loss", choices=("hidden_mse", "lm"), default="lm")
@@ -98,7 +99,8 @@ def make_config(args, use_attnres, rank):
         attnres_block_count_prior=args.attnres_block_count_prior, attnres_key_norm=args.attnres_key_norm,
         attnres_training_torch_phase2=args.attnres_training_torch_phase2,
         attnres_fuse_read_norm=args.attnres_fuse_read_norm, lrid_rank=rank or 64, lrid_num_heads=1,
-        lrid_use_logit_scale=True, fold_block_summary=args.fold_block_summary)
+        lrid_use_logit_scale=True, fold_block_summary=args.fold_block_summary,
+        fuse_block_accumulation=args.fuse_block_accumulation)
 
 
 def training_loss(args, model, idx, targets):

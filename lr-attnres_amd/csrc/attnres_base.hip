@@ -368,9 +368,10 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
     }
     return;
   }
-  // the last workgroup: extra slots are the summands of one fp32 gradient,
-  // each summed over the rows and rounded to the dtype on its own (separate
-  // autograd edges reduced in the dtype), then added in slot order
+  // the last workgroup: extra slots are the summands of one gradient, each
+  // summed over the rows and rounded to the dtype on its own (separate autograd
+  // edges reduced in the dtype), then accumulated in slot order with a rounding
+  // after each add (autograd's accumulation of gradients in the dtype)
   __shared__ float tree[1024];
   float tot = 0.f;
   for (int k = 0; k < rp.n_extra; ++k) {
@@ -384,7 +385,7 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
       if (tid < o) tree[tid] += tree[tid + o];
       __syncthreads();
     }
-    tot += DT::rnd(tree[0]);
+    tot = DT::rnd(tot + DT::rnd(tree[0]));
     __syncthreads();
   }
   if (tid == 0 && rp.dextra) rp.dextra[0] = tot;

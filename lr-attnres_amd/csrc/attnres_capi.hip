@@ -1417,10 +1417,139 @@ extern "C" int attnres_keyed_split_backward(const attnres_keyed_split_desc* d, c
   Launch L;
   fill_keyed_split(d, &p, &L, vec);
   p.gout = grad_out;
+  p.gout_stride = d->dim;
   p.gkey = grad_key;
   p.inv = const_cast<float*>(key_inv_rms);
   p.gy = grad_projected;
   hipError_t err = launch_keyed_split_backward(d->dtype, p, L, (hipStream_t)stream);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "keyed split backward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+// ---------------------------------------------------------------- block accumulation
+namespace {
+
+constexpr int kAccumBwdGroups = 1024;  // backward workgroups at most (the learned-scale partial rows)
+
+int check_block_accum(const attnres_block_accum_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  int rc = check_keyed_split(&d->split);
+  if (rc) return rc;
+  if (d->complete != 0 && d->complete != 1) return fail(ATTNRES_EINVAL, "complete must be 0 or 1, got %d", d->complete);
+  if (!d->complete && (d->value_norm || d->scale_key || d->value_scale_dev))
+    return fail(ATTNRES_EINVAL, "value_norm / scale_key / value_scale_dev apply to the completed block source only");
+  if (d->value_norm && (d->scale_key || d->value_scale_dev))
+    return fail(ATTNRES_EINVAL, "value_norm takes no scale (the key stays as it is)");
+  return ATTNRES_OK;
+}
+
+bool accum_wants_scale_grad(const attnres_block_accum_desc* d) {
+  return d->complete && !d->value_norm && d->value_scale_dev;
+}
+
+int64_t accum_bwd_groups(int64_t n_tok) {
+  const int64_t wgs = (n_tok + kKeySplitTeams - 1) / kKeySplitTeams;
+  return wgs < kAccumBwdGroups ? wgs : kAccumBwdGroups;
+}
+
+void fill_block_accum(const attnres_block_accum_desc* d, KeySplitParams* p) {
+  p->accum = d->complete ? 2 : 1;
+  p->pv = d->partial_value;
+  p->pk = d->partial_key;
+  p->value_norm = d->complete && d->value_norm ? 1 : 0;
+  p->scale_key = d->complete && d->scale_key ? 1 : 0;
+  p->vscale = d->value_scale;
+  p->scale_dev = d->complete ? d->value_scale_dev : nullptr;
+}
+
+}  // namespace
+
+extern "C" size_t attnres_block_accum_backward_workspace_size(const attnres_block_accum_desc* d) {
+  if (check_block_accum(d) != ATTNRES_OK || d->split.n_tok == 0 || !accum_wants_scale_grad(d)) return 0;
+  return (size_t)accum_bwd_groups(d->split.n_tok) * 2 * sizeof(float);
+}
+
+extern "C" int attnres_block_accum_forward(const attnres_block_accum_desc* d, void* value_out, void* key_out,
+                                           float* key_inv_rms, float* value_inv_rms, void* stream) {
+  int rc = check_block_accum(d);
+  if (rc) return rc;
+  const attnres_keyed_split_desc* sd = &d->split;
+  if (sd->n_tok == 0) return ATTNRES_OK;
+  if (!sd->projected || !value_out || !key_out) return fail(ATTNRES_EINVAL, "projected / value_out / key_out is NULL");
+  const int es = elem_size(sd->dtype);
+  const bool vec = (sd->dim * es) % 16 == 0 && (sd->row_stride * es) % 16 == 0 && aligned16(sd->projected) &&
+                   aligned16(value_out) && (!d->partial_value || aligned16(d->partial_value));
+  KeySplitParams p;
+  Launch L;
+  fill_keyed_split(sd, &p, &L, vec);
+  fill_block_accum(d, &p);
+  p.out = value_out;
+  p.key = key_out;
+  p.inv = sd->key_norm ? key_inv_rms : nullptr;
+  p.vinv = p.value_norm ? value_inv_rms : nullptr;
+  hipError_t err = launch_keyed_split_forward(sd->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "block accumulation forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_block_accum_backward(const attnres_block_accum_desc* d, const void* grad_value,
+                                            int64_t grad_value_row_stride, const void* grad_key,
+                                            const float* key_inv_rms, const float* value_inv_rms,
+                                            void* grad_projected, void* grad_partial_key, float* grad_value_scale,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_block_accum(d);
+  if (rc) return rc;
+  const attnres_keyed_split_desc* sd = &d->split;
+  hipStream_t st = (hipStream_t)stream;
+  const bool want_ds = grad_value_scale && accum_wants_scale_grad(d);
+  if (sd->n_tok == 0) {
+    if (want_ds) zero_async(grad_value_scale, sizeof(float), st);
+    return ATTNRES_OK;
+  }
+  if (!sd->projected || !grad_projected) return fail(ATTNRES_EINVAL, "projected / grad_projected is NULL");
+  if (sd->key_norm && !key_inv_rms) return fail(ATTNRES_EINVAL, "key_norm backward needs the forward's key_inv_rms");
+  if (d->complete && d->value_norm && grad_value && !value_inv_rms)
+    return fail(ATTNRES_EINVAL, "value_norm backward needs the forward's value_inv_rms");
+  if (grad_value && grad_value_row_stride < sd->dim)
+    return fail(ATTNRES_EINVAL, "grad_value_row_stride=%lld < dim", (long long)grad_value_row_stride);
+  const int es = elem_size(sd->dtype);
+  const bool vec = (sd->dim * es) % 16 == 0 && (sd->proj_cols * es) % 16 == 0 && (sd->row_stride * es) % 16 == 0 &&
+                   aligned16(sd->projected) && aligned16(grad_projected) && (!d->partial_value || aligned16(d->partial_value)) &&
+                   (!grad_value || (aligned16(grad_value) && (grad_value_row_stride * es) % 16 == 0));
+  KeySplitParams p;
+  Launch L;
+  fill_keyed_split(sd, &p, &L, vec);
+  fill_block_accum(d, &p);
+  p.gout = grad_value;
+  p.gout_stride = grad_value_row_stride;
+  p.gkey = grad_key;
+  p.inv = const_cast<float*>(key_inv_rms);
+  p.vinv = const_cast<float*>(value_inv_rms);
+  p.gy = grad_projected;
+  p.dpk = (p.scale_key && !p.value_norm) ? grad_partial_key : nullptr;
+  if (want_ds) {
+    L.grid = (int)accum_bwd_groups(sd->n_tok);
+    const size_t need = (size_t)L.grid * 2 * sizeof(float);
+    if (!workspace || workspace_bytes < need)
+      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need, workspace ? workspace_bytes : (size_t)0);
+    p.partials = (float*)workspace;
+  }
+  hipError_t err = launch_keyed_split_backward(sd->dtype, p, L, st);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "block accumulation backward launch failed: %s", hipGetErrorString(err));
+  if (want_ds) {
+    // the value and key edges' sums, each rounded to the dtype, then added
+    ReduceParams rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.partials = p.partials;
+    rp.n_groups = L.grid;
+    rp.n_part = 2;
+    rp.layout = kPartRowMajor;
+    rp.part_q = rp.part_gate = rp.part_bias = -1;
+    rp.part_extra = 0;
+    rp.n_extra = p.scale_key ? 2 : 1;
+    rp.dextra = grad_value_scale;
+    err = launch_reduce_partials(sd->dtype, rp, st);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
+  }
   return ATTNRES_OK;
 }

@@ -68,6 +68,12 @@ struct F16 {
   __device__ __forceinline__ static void store1(S* p, float x) { *p = (S)f32_to_f16_bits(x); }
 };
 
+// A block summary's scale: a python number scales in fp32; a scale tensor takes
+// the value dtype first (model.py:985 casts the learned scale; a 0-dim fp32
+// device tensor multiplying a 16-bit tensor is cast to that dtype the same way)
+template <class DT>
+__device__ __forceinline__ float summary_scale(const float* dev, float host) { return dev ? DT::rnd(*dev) : host; }
+
 // ---------------------------------------------------------------- vectors
 // A "vector" is E consecutive elements loaded or stored with one access:
 // 16 bytes on the fast path (8 bf16/fp16 or 4 fp32), one element otherwise.

@@ -179,6 +179,17 @@ struct KeySplitParams {
   int64_t n_tok, y_stride;
   int32_t D, R, P, H, hd, key_norm;
   float eps;
+  // block-summary accumulation (attnres_block_accum_*): 0 = plain split
+  int32_t accum;          // 1: add to the partial block; 2: form the completed block source
+  const void* pv;         // partial value rows [n_tok, D] dense, or null
+  const void* pk;         // partial key rows [n_tok, R] dense, or null
+  int32_t value_norm, scale_key;
+  float vscale;           // summary scale when scale_dev is null
+  const float* scale_dev; // learned summary scale (fp32 scalar) or null
+  float* vinv;            // [n_tok] 1/rms of the summary value (value_norm)
+  int64_t gout_stride;    // backward: elements between rows of gout
+  void* dpk;              // backward: partial-key gradient [n_tok, R] (complete with scale_key)
+  float* partials;        // backward: learned-scale gradient partial sums [gridDim.x][2]
 };
 
 }  // namespace attnres

@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(512) phase2_fwd_kernel(const Phase2Params p) {
   const int D = p.D, bd = blockDim.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave, wpt = bd / kWave;
   const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
-  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float vs = summary_scale<DT>(p.scale_dev, p.vscale);
   const float bias = p.bias_dev ? *p.bias_dev : p.bias;
 
   float qv[CB][E], qk[kP2KPT];
@@ -229,7 +229,7 @@ __global__ void __launch_bounds__(512) phase2_bwd_kernel(const Phase2Params p) {
   const int D = p.D, bd = blockDim.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave, wpt = bd / kWave;
   const Cols<CB, E> cl(p.ncols, D, lane, wave, wpt);
-  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float vs = summary_scale<DT>(p.scale_dev, p.vscale);
   const float bias = p.bias_dev ? *p.bias_dev : p.bias;
 
   float qv[CB][E], qk[kP2KPT];
@@ -575,7 +575,7 @@ __global__ void __launch_bounds__(256) phase2_wave_fwd_kernel(const Phase2Params
   using S = typename DT::S;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, wpb = blockDim.x / kWave;
   const Cols<CB, E> cl(p.ncols, p.D, lane, 0, 1);
-  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float vs = summary_scale<DT>(p.scale_dev, p.vscale);
   const float bias = p.bias_dev ? *p.bias_dev : p.bias;
   float qv[CB][E], qk[kP2KPT];
   p2w_queries<DT, E, CB, LR>(p, cl, lane, qv, qk);
@@ -635,7 +635,7 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, wpb = blockDim.x / kWave;
   const int D = p.D;
   const Cols<CB, E> cl(p.ncols, D, lane, 0, 1);
-  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float vs = summary_scale<DT>(p.scale_dev, p.vscale);
   const float bias = p.bias_dev ? *p.bias_dev : p.bias;
   const bool base_key = !LR && !p.logit_given;
 

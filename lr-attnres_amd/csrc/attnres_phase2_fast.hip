@@ -120,7 +120,7 @@ __global__ void __launch_bounds__(256) phase2_fwd_fast_kernel(const Phase2Params
   constexpr int W = VB / 4;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = uniform_i32(threadIdx.x / kWave);
-  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float vs = summary_scale<DT>(p.scale_dev, p.vscale);
   const float bias = p.bias_dev ? *p.bias_dev : p.bias;
   float q[CB][E];
   p2fast_query<DT, VB, CB>(p, lane, q);
@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(256) phase2_bwd_fast_kernel(const Phase2Params
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = uniform_i32(threadIdx.x / kWave);
   const int D = p.D;
-  const float vs = p.scale_dev ? *p.scale_dev : p.vscale;
+  const float vs = summary_scale<DT>(p.scale_dev, p.vscale);
   const float bias = p.bias_dev ? *p.bias_dev : p.bias;
   const bool want_sv = p.part_scale >= 0;
   float q[CB][E];

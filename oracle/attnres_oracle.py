@@ -40,6 +40,10 @@ gated_query_ref                           closed form (zero gate -> static)
 block_* helpers                           the reference tests' known answers
 lrid_fused_projection_split_ref           the reference model itself: whole-model
                                           golden vectors (tests/golden/model_*)
+lrid_block_accumulate_ref                 composition of the pinned split and
+                                          block_* helpers; the decoder built on
+                                          it reproduces the reference-model
+                                          golden vectors
 phase1_from_logits_ref / phase2_*_ref     phase1+phase2 == full read identity
                                           (tests/test_attnres_ops.py:582-610),
                                           golden fixtures with gradients,
@@ -271,6 +275,16 @@ def block_count_scale(count: int, alpha) -> float | Tensor:
     return float(count) ** (-float(alpha))
 
 
+def _as_value_dtype(s, value: Tensor):
+    """A scale tensor as the reference multiplies by it on the GPU: in the value
+    dtype.  The learned scale is cast explicitly (``model.py:983-985``); a
+    learned alpha leaves ``count ** -alpha`` a 0-dim fp32 device tensor, and
+    multiplying a 16-bit tensor by one casts it to that dtype first (the CPU
+    kernel would keep it in fp32 -- this oracle runs on the CPU, so it casts
+    explicitly).  A python number stays in fp32."""
+    return s.to(value.dtype) if isinstance(s, Tensor) else s
+
+
 def block_summary(partial_sum: Tensor, count: int, alpha=1.0, value_norm: bool = False,
                   scale=None) -> Tensor:
     """Block source value, ``model.py:990-1001``.
@@ -281,7 +295,7 @@ def block_summary(partial_sum: Tensor, count: int, alpha=1.0, value_norm: bool =
     if value_norm:
         return norm(partial_sum)
     s = block_count_scale(count, alpha) if scale is None else scale
-    return partial_sum * s
+    return partial_sum * _as_value_dtype(s, partial_sum)
 
 
 def lrid_block_source(partial_sum: Tensor, partial_key: Tensor, count: int, alpha=1.0,
@@ -293,7 +307,7 @@ def lrid_block_source(partial_sum: Tensor, partial_key: Tensor, count: int, alph
     """
     if value_norm:
         return norm(partial_sum), partial_key
-    s = block_count_scale(count, alpha) if scale is None else scale
+    s = _as_value_dtype(block_count_scale(count, alpha) if scale is None else scale, partial_sum)
     value = partial_sum * s
     key = partial_key
     if key is not None and not key_norm:
@@ -406,6 +420,29 @@ def lrid_fused_projection_split_ref(projected: Tensor, output_dim: int, rank: in
     return out, key
 
 
+def lrid_block_accumulate_ref(projected: Tensor, partial_value, partial_key, output_dim: int, rank: int,
+                              num_heads: int = 1, key_norm: bool = True, complete: bool = False,
+                              partial_scale=1.0, value_norm: bool = False, scale_key: bool = False):
+    """The eager sequence the fused block accumulation replaces: the fused
+    projection split (``model.py:374-378``), the partial-block adds
+    (``model.py:2377-2389, 2451-2463``) and, with ``complete``, the block source
+    (``_lrid_block_source``, ``model.py:1003-1018``: the value scaled, or
+    rms-normed with value_norm, and a scale tensor cast to the key dtype
+    before it scales the key)."""
+    out, key = lrid_fused_projection_split_ref(projected, output_dim, rank, num_heads, key_norm)
+    value = out if partial_value is None else partial_value + out
+    k = key if partial_key is None else partial_key + key
+    if not complete:
+        return value, k
+    if value_norm:
+        return norm(value), k
+    s = _as_value_dtype(partial_scale, value)
+    value = value * s
+    if scale_key:
+        k = k * (s.to(k.dtype) if isinstance(s, Tensor) else s)
+    return value, k
+
+
 def softmax_weights_ref(values_or_keys, query: Tensor, num_heads: int, logit_scale: float, key_norm: bool,
                         base: bool, source_counts=None, source_logit_biases=None) -> Tensor:
     """fp32 softmax weights [S,B,T,H] of a read (what the kernels save).
@@ -450,6 +487,7 @@ __all__ = [
     "lrid_block_source",
     "block_count_logit_bias",
     "phase1_from_logits_ref",
+    "lrid_block_accumulate_ref",
     "attention_residual_phase1_ref",
     "attention_residual_phase2_ref",
     "lrid_attention_residual_phase2_ref",

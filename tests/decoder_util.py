@@ -42,6 +42,12 @@ class OracleOps:
         return O.lrid_fused_projection_split_ref(projected, output_dim, rank, num_heads, key_norm)
 
     @staticmethod
+    def lrid_block_accumulate(projected, partial_value, partial_key, output_dim, rank, num_heads=1, key_norm=True,
+                              complete=False, partial_scale=1.0, value_norm=False, scale_key=False):
+        return O.lrid_block_accumulate_ref(projected, partial_value, partial_key, output_dim, rank, num_heads,
+                                           key_norm, complete, partial_scale, value_norm, scale_key)
+
+    @staticmethod
     def lrid_attention_residual_phase2(pv, pk, q, inter, lse, scale, key_norm, force_triton=False,
                                        normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False):
         return _phase2(pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias, partial_scale,

@@ -39,7 +39,9 @@ def test_library_exports_every_declared_symbol():
                             "attnres_keyed_split_forward", "attnres_keyed_split_backward",
                             "attnres_keyed_logits_forward", "attnres_keyed_logits_backward",
                             "attnres_keyed_logits_backward_workspace_size", "attnres_kernel_timing",
-                            "attnres_kernel_times", "attnres_read_backward_noalloc"])
+                            "attnres_kernel_times", "attnres_read_backward_noalloc",
+                            "attnres_block_accum_forward", "attnres_block_accum_backward",
+                            "attnres_block_accum_backward_workspace_size"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -63,7 +65,8 @@ def test_abi_version_and_error_reporting():
 
 STRUCTS = ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads"),
            (H.Phase1Desc, "attnres_phase1_desc"), (H.Phase2Desc, "attnres_phase2_desc"),
-           (H.Phase2Grads, "attnres_phase2_grads"), (H.KeyedSplitDesc, "attnres_keyed_split_desc"))
+           (H.Phase2Grads, "attnres_phase2_grads"), (H.KeyedSplitDesc, "attnres_keyed_split_desc"),
+           (H.BlockAccumDesc, "attnres_block_accum_desc"))
 
 
 def _c_layout():
@@ -399,3 +402,77 @@ def test_noalloc_backward_rejects_needs_beyond_its_scratch_on_the_host():
     assert b"no-allocation entry point holds 33554432" in lib.attnres_last_error()
     assert lib.attnres_read_backward_noalloc(ctypes.byref(d), None, None) == -1
     assert lib.attnres_read_backward_noalloc(None, ctypes.byref(g), None) == -1
+
+
+def _badesc(**kw):
+    d = H.BlockAccumDesc()
+    d.split = _ksdesc()
+    d.complete = 1
+    d.value_scale = 0.5
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@needs_lib
+def test_block_accum_host_validation_rejects_bad_descriptions_without_launching():
+    lib = H.load()
+    out, key = ctypes.c_void_p(0x6000), ctypes.c_void_p(0x7000)
+    scale = ctypes.cast(ctypes.c_void_p(0x9000), ctypes.POINTER(ctypes.c_float))
+    cases = [
+        (dict(complete=2), b"complete"),
+        (dict(complete=0, value_norm=1), b"completed block source only"),
+        (dict(complete=0, scale_key=1), b"completed block source only"),
+        (dict(complete=0, value_scale_dev=scale), b"completed block source only"),
+        (dict(value_norm=1, scale_key=1), b"value_norm"),
+        (dict(value_norm=1, value_scale_dev=scale), b"value_norm"),
+    ]
+    for kw, msg in cases:
+        d = _badesc(**kw)
+        assert lib.attnres_block_accum_forward(ctypes.byref(d), out, key, None, None, None) == -1, kw
+        assert msg in lib.attnres_last_error(), (kw, lib.attnres_last_error())
+        assert lib.attnres_block_accum_backward_workspace_size(ctypes.byref(d)) == 0
+    # the split's own checks apply
+    d = _badesc()
+    d.split.heads = 3
+    assert lib.attnres_block_accum_forward(ctypes.byref(d), out, key, None, None, None) == -1
+    assert b"heads" in lib.attnres_last_error()
+    # workspace only for a learned scale's gradient, one fp32 pair per backward workgroup
+    assert lib.attnres_block_accum_backward_workspace_size(ctypes.byref(_badesc())) == 0
+    d = _badesc(value_scale_dev=scale)
+    ws = lib.attnres_block_accum_backward_workspace_size(ctypes.byref(d))
+    assert ws > 0 and ws % 8 == 0
+    rc = lib.attnres_block_accum_backward(ctypes.byref(d), None, 0, None, ctypes.cast(ctypes.c_void_p(0x8000), ctypes.POINTER(ctypes.c_float)),
+                                          None, ctypes.c_void_p(0xa000), None, scale, None, 0, None)
+    assert rc == -4 and b"workspace" in lib.attnres_last_error()
+    # the backward needs the forward's inverse rms values
+    d = _badesc()
+    assert lib.attnres_block_accum_backward(ctypes.byref(d), None, 0, None, None, None, ctypes.c_void_p(0xa000),
+                                            None, None, None, 0, None) == -1
+    assert b"key_inv_rms" in lib.attnres_last_error()
+    d = _badesc(value_norm=1)
+    d.split.key_norm = 0
+    assert lib.attnres_block_accum_backward(ctypes.byref(d), ctypes.c_void_p(0xb000), 768, None, None, None,
+                                            ctypes.c_void_p(0xa000), None, None, None, 0, None) == -1
+    assert b"value_inv_rms" in lib.attnres_last_error()
+    d = _badesc()
+    d.split.key_norm = 0
+    assert lib.attnres_block_accum_backward(ctypes.byref(d), ctypes.c_void_p(0xb000), 700, None, None, None,
+                                            ctypes.c_void_p(0xa000), None, None, None, 0, None) == -1
+    assert b"grad_value_row_stride" in lib.attnres_last_error()
+    # nothing to do for zero tokens
+    d = _badesc()
+    d.split.n_tok = 0
+    assert lib.attnres_block_accum_forward(ctypes.byref(d), None, None, None, None, None) == 0
+
+
+def test_block_accumulate_rejects_bad_calls_on_the_host():
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lrid_block_accumulate(torch.randn(2, 3, 80), None, None, 64, 16)
+    with pytest.raises(RuntimeError, match="columns"):
+        ops.lrid_block_accumulate(torch.randn(2, 3, 70), None, None, 64, 16)
+    with pytest.raises(RuntimeError, match="complete=True only"):
+        ops.lrid_block_accumulate(torch.randn(2, 3, 80), None, None, 64, 16, partial_scale=0.5)
+    with pytest.raises(RuntimeError, match="value_norm"):
+        ops.lrid_block_accumulate(torch.randn(2, 3, 80), None, None, 64, 16, complete=True, value_norm=True,
+                                  scale_key=True)

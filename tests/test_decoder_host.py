@@ -18,11 +18,13 @@ from decoder_util import OracleOps, build_from_case, lm_step, load_model_case, m
 CASES = sorted(model_index())
 
 
-@pytest.mark.parametrize("fold", [True, False])
+@pytest.mark.parametrize("fold,fuse", [(True, True), (True, False), (False, False)])
 @pytest.mark.parametrize("name", CASES)
-def test_decoder_matches_reference_model(name, fold):
+def test_decoder_matches_reference_model(name, fold, fuse):
+    """Also pins the oracle's block accumulation (``fuse``: split, partial-block
+    adds and block source composed in ``lrid_block_accumulate_ref``)."""
     t, meta = load_model_case(name)
-    model = build_from_case(t, meta, OracleOps, fold_block_summary=fold)
+    model = build_from_case(t, meta, OracleOps, fold_block_summary=fold, fuse_block_accumulation=fuse)
     hidden, loss = lm_step(model, t["idx"], t["targets"])
     assert torch.equal(hidden, t["hidden"])
     assert torch.equal(loss.reshape(1), t["loss"])

@@ -84,6 +84,19 @@ class CheckingOps:
         self.calls.append(("split",))
         return out, key
 
+    def lrid_block_accumulate(self, projected, partial_value, partial_key, output_dim, rank, num_heads=1,
+                              key_norm=True, complete=False, partial_scale=1.0, value_norm=False, scale_key=False):
+        value, key = ops.lrid_block_accumulate(projected, partial_value, partial_key, output_dim, rank, num_heads,
+                                               key_norm, complete, partial_scale, value_norm, scale_key)
+        cpu = lambda t: t.cpu() if t is not None else None  # noqa: E731
+        e_value, e_key = O.lrid_block_accumulate_ref(cpu(projected), cpu(partial_value), cpu(partial_key), output_dim,
+                                                     rank, num_heads, key_norm, complete, partial_scale, value_norm,
+                                                     scale_key)
+        assert torch.equal(value.cpu(), e_value)
+        assert_close(key, e_key, projected.dtype, "accumulated key")
+        self.calls.append(("accumulate", complete))
+        return value, key
+
     def _phase2(self, fn, merge, pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias,
                 partial_scale, scale_key):
         out = fn(pv, pk, q, inter, lse, scale, key_norm, normalize_output=normalize_output, logit_bias=logit_bias,
@@ -134,6 +147,45 @@ def test_config5_every_read_matches_oracle(torch_phase2):
     # three in-block sites of each block (site 1..3 read the embedding alone in phase 1).
     assert n1 == 6
     assert n2 == 18
+    # every sublayer grows the partial block in one fused pass; 6 of them end a block
+    assert sum(1 for c in checker.calls if c[0] == "accumulate") == 24
+    assert sum(1 for c in checker.calls if c == ("accumulate", True)) == 6
+
+
+def test_fused_block_accumulation_is_bit_identical_to_the_split_path():
+    """The decoder with sublayer projections folded by lrid_block_accumulate
+    against the same weights with the split + eager adds: hidden state, loss
+    and every gradient bit for bit (the kernels round as the eager ops do)."""
+    cfg = dict(n_layer=4, n_head=4, n_embd=256, mlp_hidden_dim=512, vocab_size=1000, block_size=256,
+               attnres_num_blocks=3, lrid_rank=32, attn_res_query_init="normal")
+    torch.manual_seed(13)
+    with torch.device(DEV):
+        fused = AD.Decoder(AD.DecoderConfig(**cfg, fuse_block_accumulation=True)).to(torch.bfloat16)
+        split = AD.Decoder(AD.DecoderConfig(**cfg, fuse_block_accumulation=False)).to(torch.bfloat16)
+    split.load_state_dict(fused.state_dict())
+    g = torch.Generator().manual_seed(14)
+    idx = torch.randint(0, 1000, (2, 256), generator=g).to(DEV)
+    tgt = torch.randint(0, 1000, (2, 256), generator=g).to(DEV)
+    h_f, l_f = lm_step(fused, idx, tgt)
+    h_s, l_s = lm_step(split, idx, tgt)
+    assert torch.equal(h_f, h_s)
+    assert torch.equal(l_f, l_s)
+    # a second split step tells which gradients the GPU itself reproduces bit for bit
+    # (the attention backward may sum in a varying order); those must match exactly
+    first = {n: p.grad.clone() for n, p in split.named_parameters()}
+    split.zero_grad(set_to_none=True)
+    lm_step(split, idx, tgt)
+    split_params = dict(split.named_parameters())
+    n_exact = 0
+    for pname, p in fused.named_parameters():
+        again = split_params[pname].grad
+        if torch.equal(first[pname], again):
+            assert torch.equal(p.grad, again), pname
+            n_exact += 1
+        else:
+            assert _rel_l2(p.grad, again) <= 1e-2, pname
+    # at least the last MLP projection and the read queries sit after every attention backward
+    assert n_exact >= 1
 
 
 def test_decoder_hip_vs_oracle_cpu_mid_size():
