@@ -68,6 +68,19 @@ struct F16 {
   __device__ __forceinline__ static void store1(S* p, float x) { *p = (S)f32_to_f16_bits(x); }
 };
 
+// one element's raw bits (zero-extended for 16-bit types), converted by bits_to_float
+template <class DT>
+__device__ __forceinline__ uint32_t load_bits1(const typename DT::S* p) {
+  if constexpr (sizeof(typename DT::S) == 4) return __float_as_uint(*p);
+  else return (uint32_t)*p;
+}
+template <class DT>
+__device__ __forceinline__ float bits_to_float(uint32_t u) {
+  if constexpr (DT::kCode == 0) return __uint_as_float(u);
+  else if constexpr (DT::kCode == 1) return __uint_as_float(u << 16);
+  else return f16_bits_to_f32(u);
+}
+
 // A block summary's scale: a python number scales in fp32; a scale tensor takes
 // the value dtype first (model.py:985 casts the learned scale; a 0-dim fp32
 // device tensor multiplying a 16-bit tensor is cast to that dtype the same way)

@@ -19,44 +19,69 @@
 
 namespace attnres {
 
-constexpr int kKsJ = 4;  // key chunks of 64 (R <= 256)
+// A token's key row is held as KJ chunks of 64 lanes (KJ = 1, 2 or 4: R <= 64,
+// 128 or 256), a template parameter so that short keys keep few registers.
+
+// Key rows are short (R <= 256): the lane holds elements r = lane + 64 j for
+// j < nj = ceil(R / 64).  They are loaded as raw bits and converted only after
+// every load of the token has been issued: a 16-bit element converted right
+// after its load makes the wave wait for that load before issuing the next.
+// Lanes past R re-read element R - 1 (in bounds) and convert to 0.
+template <class DT, int KJ>
+__device__ __forceinline__ void key_load(const typename DT::S* row, int R, int nj, int lane, uint32_t (&b)[KJ]) {
+#pragma unroll
+  for (int j = 0; j < KJ; ++j)
+    if (j < nj) b[j] = load_bits1<DT>(row + min(lane + j * kWave, R - 1));
+}
+
+template <class DT, int KJ>
+__device__ __forceinline__ void key_floats(const uint32_t (&b)[KJ], int R, int nj, int lane, float (&f)[KJ]) {
+#pragma unroll
+  for (int j = 0; j < KJ; ++j) f[j] = (j < nj && lane + j * kWave < R) ? bits_to_float<DT>(b[j]) : 0.f;
+}
+
+// the key heads' 1/rms values of the lane's elements (forward's saved values)
+template <int KJ>
+__device__ __forceinline__ void key_inv_load(const KeySplitParams& p, int64_t tok, int nj, int lane, float (&inv)[KJ]) {
+#pragma unroll
+  for (int j = 0; j < KJ; ++j)
+    inv[j] = (p.key_norm && j < nj) ? p.inv[tok * p.H + min(lane + j * kWave, p.R - 1) / p.hd] : 1.f;
+}
 
 // per-element head sums of a[j] over each key head (all lanes get their head's sum)
-__device__ __forceinline__ void head_sums(const KeySplitParams& p, const float (&a)[kKsJ], float (&s)[kKsJ]) {
+template <int KJ>
+__device__ __forceinline__ void head_sums(const KeySplitParams& p, const float (&a)[KJ], float (&s)[KJ]) {
   if (p.hd < kWave) {
 #pragma unroll
-    for (int j = 0; j < kKsJ; ++j) s[j] = group_sum(a[j], p.hd);
+    for (int j = 0; j < KJ; ++j) s[j] = group_sum(a[j], p.hd);
   } else {
-    float t[kKsJ];
+    float t[KJ];
 #pragma unroll
-    for (int j = 0; j < kKsJ; ++j) t[j] = wave_sum(a[j]);
+    for (int j = 0; j < KJ; ++j) t[j] = wave_sum(a[j]);
     const int cph = p.hd / kWave;  // chunks per head
 #pragma unroll
-    for (int j = 0; j < kKsJ; ++j) {
+    for (int j = 0; j < KJ; ++j) {
       const int h0 = (j / cph) * cph;
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < kKsJ; ++k)
+      for (int k = 0; k < KJ; ++k)
         if (k >= h0 && k < h0 + cph) acc += t[k];
       s[j] = acc;
     }
   }
 }
 
-template <class DT, int E>
+template <class DT, int E, int KJ>
 __global__ void __launch_bounds__(256) keyed_split_fwd_kernel(const KeySplitParams p) {
   using S = typename DT::S;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, wpb = blockDim.x / kWave;
   const int nv = p.D / E;
   const int64_t stride = (int64_t)gridDim.x * wpb;
+  const int nj = (p.R + kWave - 1) / kWave;
   for (int64_t tok = (int64_t)blockIdx.x * wpb + wave; tok < p.n_tok; tok += stride) {
     const S* yr = (const S*)p.y + tok * p.y_stride;
-    float x[kKsJ];
-#pragma unroll
-    for (int j = 0; j < kKsJ; ++j) {
-      const int r = lane + j * kWave;
-      x[j] = r < p.R ? DT::load1(yr + p.D + r) : 0.f;
-    }
+    uint32_t xb[KJ];
+    key_load<DT, KJ>(yr + p.D, p.R, nj, lane, xb);
     S* orow = (S*)p.out + tok * (int64_t)p.D;
     for (int v = lane; v < nv; v += kWave) {
       Raw<DT, E> t;
@@ -65,14 +90,16 @@ __global__ void __launch_bounds__(256) keyed_split_fwd_kernel(const KeySplitPara
       unpack<DT, E>(t, f);
       store_vec<DT, E, true>(orow + v * E, f);
     }
+    float x[KJ];
+    key_floats<DT, KJ>(xb, p.R, nj, lane, x);
     S* krow = (S*)p.key + tok * (int64_t)p.R;
     if (p.key_norm) {
-      float sq[kKsJ], ss[kKsJ];
+      float sq[KJ], ss[KJ];
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) sq[j] = x[j] * x[j];
-      head_sums(p, sq, ss);
+      for (int j = 0; j < KJ; ++j) sq[j] = x[j] * x[j];
+      head_sums<KJ>(p, sq, ss);
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         const float inv = 1.0f / sqrtf(ss[j] / (float)p.hd + p.eps);
         if (r < p.R) {
@@ -82,7 +109,7 @@ __global__ void __launch_bounds__(256) keyed_split_fwd_kernel(const KeySplitPara
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         if (r < p.R) DT::store1(krow + r, x[j]);
       }
@@ -90,14 +117,25 @@ __global__ void __launch_bounds__(256) keyed_split_fwd_kernel(const KeySplitPara
   }
 }
 
-template <class DT, int E>
+template <class DT, int E, int KJ>
 __global__ void __launch_bounds__(256) keyed_split_bwd_kernel(const KeySplitParams p) {
   using S = typename DT::S;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, wpb = blockDim.x / kWave;
   const int nv = p.D / E;
   const int64_t stride = (int64_t)gridDim.x * wpb;
+  const int nj = (p.R + kWave - 1) / kWave;
   for (int64_t tok = (int64_t)blockIdx.x * wpb + wave; tok < p.n_tok; tok += stride) {
     S* gyr = (S*)p.gy + tok * (int64_t)p.P;
+    // key loads first (raw bits), then the output columns
+    const S* gkr = p.gkey ? (const S*)p.gkey + tok * (int64_t)p.R : nullptr;
+    const bool norm_bwd = p.key_norm && gkr;
+    uint32_t gb[KJ], xb[KJ];
+    float inv[KJ];
+    if (gkr) key_load<DT, KJ>(gkr, p.R, nj, lane, gb);
+    if (norm_bwd) {
+      key_load<DT, KJ>((const S*)p.y + tok * p.y_stride + p.D, p.R, nj, lane, xb);
+      key_inv_load<KJ>(p, tok, nj, lane, inv);
+    }
     // output columns: the output gradient (or zero)
     const S* gor = p.gout ? (const S*)p.gout + tok * p.gout_stride : nullptr;
     for (int v = lane; v < nv; v += kWave) {
@@ -113,35 +151,27 @@ __global__ void __launch_bounds__(256) keyed_split_bwd_kernel(const KeySplitPara
       store_vec<DT, E, true>(gyr + v * E, f);
     }
     // key columns
-    float g[kKsJ];
-    const S* gkr = p.gkey ? (const S*)p.gkey + tok * (int64_t)p.R : nullptr;
+    float g[KJ];
 #pragma unroll
-    for (int j = 0; j < kKsJ; ++j) {
-      const int r = lane + j * kWave;
-      g[j] = (gkr && r < p.R) ? DT::load1(gkr + r) : 0.f;
-    }
-    if (p.key_norm && gkr) {
-      const S* yr = (const S*)p.y + tok * p.y_stride + p.D;
-      float x[kKsJ], gx[kKsJ], dot[kKsJ];
+    for (int j = 0; j < KJ; ++j) g[j] = 0.f;
+    if (gkr) key_floats<DT, KJ>(gb, p.R, nj, lane, g);
+    if (norm_bwd) {
+      float x[KJ], gx[KJ], dot[KJ];
+      key_floats<DT, KJ>(xb, p.R, nj, lane, x);
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
-        const int r = lane + j * kWave;
-        x[j] = r < p.R ? DT::load1(yr + r) : 0.f;
-        gx[j] = g[j] * x[j];
-      }
-      head_sums(p, gx, dot);
+      for (int j = 0; j < KJ; ++j) gx[j] = g[j] * x[j];
+      head_sums<KJ>(p, gx, dot);
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         if (r < p.R) {
-          const float inv = p.inv[tok * p.H + r / p.hd];
-          const float k3 = inv * inv * inv * (dot[j] / (float)p.hd);
-          DT::store1(gyr + p.D + r, inv * g[j] - x[j] * k3);
+          const float k3 = inv[j] * inv[j] * inv[j] * (dot[j] / (float)p.hd);
+          DT::store1(gyr + p.D + r, inv[j] * g[j] - x[j] * k3);
         }
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         if (r < p.R) DT::store1(gyr + p.D + r, g[j]);
       }
@@ -159,7 +189,46 @@ __global__ void __launch_bounds__(256) keyed_split_bwd_kernel(const KeySplitPara
 // -- value * s (or rms_norm(value)), key (* s) -- instead of the sums.  Each
 // add and product is rounded to the dtype, as the reference's eager ops do.
 
-// row v (E elements) of the grown partial value for token tok: pv + y[:D]
+// Rows of up to AV vectors per lane (AV = 2 or 4: D <= 1024 or 2048 for 16-bit
+// types; AV = 0: a loop over the row) are held in registers: every load of a
+// token -- key, partial key, y[:D], partial value -- is issued before the first
+// store.  The stores may alias the loads as far as
+// the compiler knows, so it would otherwise keep each load behind the previous
+// store and serialise a token into several memory round trips.  Longer rows
+// take a loop over the row (twice for the value norm).
+template <class DT, int E, int AV>
+struct AccRow {  // raw bits of the lane's vectors of y[:D] and of the partial value
+  Raw<DT, E> y[AV > 0 ? AV : 1], pv[AV > 0 ? AV : 1];
+};
+
+// issue the loads of the lane's vectors (c < nc); lanes past the row's end
+// re-read its last vector (a cache hit) and drop the result
+template <class DT, int E, int AV>
+__device__ __forceinline__ void acc_row_load(const typename DT::S* yr, const typename DT::S* pvr, int nv, int nc,
+                                             int lane, AccRow<DT, E, AV>& a) {
+#pragma unroll
+  for (int c = 0; c < AV; ++c) {
+    if (c < nc) {
+      const int v = min(lane + c * kWave, nv - 1);
+      load_raw<DT, E, true>(yr + v * E, a.y[c]);
+      if (pvr) load_raw<DT, E, true>(pvr + v * E, a.pv[c]);
+    }
+  }
+}
+
+// vector c of the grown partial value pv + y[:D] from the loaded bits
+template <class DT, int E, int AV>
+__device__ __forceinline__ void acc_row_grown(const AccRow<DT, E, AV>& a, bool has_pv, int c, float (&f)[E]) {
+  unpack<DT, E>(a.y[c], f);
+  if (has_pv) {
+    float b[E];
+    unpack<DT, E>(a.pv[c], b);
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = DT::rnd(b[e] + f[e]);
+  }
+}
+
+// row v (E elements) of the grown partial value for token tok: pv + y[:D] (long rows)
 template <class DT, int E>
 __device__ __forceinline__ void grown_value(const KeySplitParams& p, const typename DT::S* yr, const typename DT::S* pvr,
                                             int v, float (&f)[E]) {
@@ -176,11 +245,14 @@ __device__ __forceinline__ void grown_value(const KeySplitParams& p, const typen
   }
 }
 
-template <class DT, int E>
+template <class DT, int E, int AV, int KJ>
 __global__ void __launch_bounds__(256) block_accum_fwd_kernel(const KeySplitParams p) {
   using S = typename DT::S;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, wpb = blockDim.x / kWave;
   const int nv = p.D / E;
+  const int nc = (nv + kWave - 1) / kWave;  // the host launches AV > 0 only for nc <= AV
+  constexpr bool resident = AV > 0;
+  const int nj = (p.R + kWave - 1) / kWave;
   const int64_t stride = (int64_t)gridDim.x * wpb;
   const bool complete = p.accum == 2;
   const bool vnorm = complete && p.value_norm;
@@ -188,21 +260,26 @@ __global__ void __launch_bounds__(256) block_accum_fwd_kernel(const KeySplitPara
   for (int64_t tok = (int64_t)blockIdx.x * wpb + wave; tok < p.n_tok; tok += stride) {
     const S* yr = (const S*)p.y + tok * p.y_stride;
     const S* pvr = p.pv ? (const S*)p.pv + tok * (int64_t)p.D : nullptr;
+    const S* pkr = p.pk ? (const S*)p.pk + tok * (int64_t)p.R : nullptr;
+    // ---- every load of the token
+    uint32_t xb[KJ], pb[KJ];
+    key_load<DT, KJ>(yr + p.D, p.R, nj, lane, xb);
+    if (pkr) key_load<DT, KJ>(pkr, p.R, nj, lane, pb);
+    AccRow<DT, E, AV> a;
+    if constexpr (resident) acc_row_load<DT, E, AV>(yr, pvr, nv, nc, lane, a);
     // ---- key: split (and per-head norm), + partial key, (* s)
-    float x[kKsJ], k[kKsJ];
+    float x[KJ], pkv[KJ], k[KJ];
+    key_floats<DT, KJ>(xb, p.R, nj, lane, x);
+    if (pkr) key_floats<DT, KJ>(pb, p.R, nj, lane, pkv);
 #pragma unroll
-    for (int j = 0; j < kKsJ; ++j) {
-      const int r = lane + j * kWave;
-      x[j] = r < p.R ? DT::load1(yr + p.D + r) : 0.f;
-      k[j] = x[j];
-    }
+    for (int j = 0; j < KJ; ++j) k[j] = x[j];
     if (p.key_norm) {
-      float sq[kKsJ], ss[kKsJ];
+      float sq[KJ], ss[KJ];
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) sq[j] = x[j] * x[j];
-      head_sums(p, sq, ss);
+      for (int j = 0; j < KJ; ++j) sq[j] = x[j] * x[j];
+      head_sums<KJ>(p, sq, ss);
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         const float inv = 1.0f / sqrtf(ss[j] / (float)p.hd + p.eps);
         k[j] = DT::rnd(x[j] * inv);
@@ -210,18 +287,51 @@ __global__ void __launch_bounds__(256) block_accum_fwd_kernel(const KeySplitPara
       }
     }
     S* krow = (S*)p.key + tok * (int64_t)p.R;
-    const S* pkr = p.pk ? (const S*)p.pk + tok * (int64_t)p.R : nullptr;
 #pragma unroll
-    for (int j = 0; j < kKsJ; ++j) {
+    for (int j = 0; j < KJ; ++j) {
       const int r = lane + j * kWave;
       if (r < p.R) {
-        float kv = pkr ? DT::rnd(DT::load1(pkr + r) + k[j]) : k[j];
+        float kv = pkr ? DT::rnd(pkv[j] + k[j]) : k[j];
         if (complete && !vnorm && p.scale_key) kv = DT::rnd(kv * s);
         DT::store1(krow + r, kv);
       }
     }
     // ---- value: y[:D] + partial value, (* s or rms-normed)
     S* orow = (S*)p.out + tok * (int64_t)p.D;
+    if constexpr (resident) {
+      float f[AV][E];
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < AV; ++c) {
+        if (c < nc) {
+          acc_row_grown<DT, E, AV>(a, pvr != nullptr, c, f[c]);
+          if (vnorm && lane + c * kWave < nv) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) ss += f[c][e] * f[c][e];
+          }
+        }
+      }
+      float inv_v = 1.f;
+      if (vnorm) {
+        inv_v = 1.0f / sqrtf(wave_sum(ss) / (float)p.D + p.eps);
+        if (lane == 0 && p.vinv) p.vinv[tok] = inv_v;
+      }
+#pragma unroll
+      for (int c = 0; c < AV; ++c) {
+        const int v = lane + c * kWave;
+        if (c < nc && v < nv) {
+          if (vnorm) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) f[c][e] = DT::rnd(f[c][e] * inv_v);
+          } else if (complete) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) f[c][e] = DT::rnd(f[c][e] * s);
+          }
+          store_vec<DT, E, true>(orow + v * E, f[c]);
+        }
+      }
+      continue;
+    }
     float inv_v = 1.f;
     if (vnorm) {  // first pass: the grown row's sum of squares
       float ss = 0.f;
@@ -249,81 +359,153 @@ __global__ void __launch_bounds__(256) block_accum_fwd_kernel(const KeySplitPara
   }
 }
 
+// the gradient of the grown value's vector from its upstream gradient g (in place):
+// rms-norm backward, or the scale (adding rnd(g * value) to the scale's gradient)
 template <class DT, int E>
+__device__ __forceinline__ void grown_grad(bool vnorm, bool complete, bool want_ds, float s, float inv_v, float k3,
+                                           const float (&f)[E], float (&g)[E], float& acc_v) {
+  if (vnorm) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) g[e] = DT::rnd(inv_v * g[e] - f[e] * k3);
+  } else if (complete) {
+    if (want_ds) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc_v += DT::rnd(g[e] * f[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) g[e] = DT::rnd(g[e] * s);
+  }
+}
+
+// G: the grown value may be read back (value norm or a learned scale's gradient);
+// without it the kernel keeps fewer registers
+template <class DT, int E, int AV, int KJ, bool G>
 __global__ void __launch_bounds__(256) block_accum_bwd_kernel(const KeySplitParams p) {
   using S = typename DT::S;
   __shared__ float s_fold[2 * 16];  // two sums per wave (at most 16 waves)
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, wpb = blockDim.x / kWave;
   const int nv = p.D / E;
+  const int nc = (nv + kWave - 1) / kWave;  // the host launches AV > 0 only for nc <= AV
+  constexpr bool resident = AV > 0;
+  const int nj = (p.R + kWave - 1) / kWave;
   const int64_t stride = (int64_t)gridDim.x * wpb;
   const bool complete = p.accum == 2;
-  const bool vnorm = complete && p.value_norm;
+  const bool vnorm = G && complete && p.value_norm;
   const float s = complete ? summary_scale<DT>(p.scale_dev, p.vscale) : 1.f;
-  const bool want_ds = complete && !vnorm && p.partials;
+  const bool want_ds = G && complete && !vnorm && p.partials;
+  const bool key_ds = want_ds && p.scale_key && p.gkey;
+  // the grown value is read back only for the norm's backward or the scale's gradient
+  const bool need_grown = p.gout && (vnorm || want_ds);
   float acc_v = 0.f, acc_k = 0.f;  // learned-scale gradient: sum of rnd(g * grown value / key)
   for (int64_t tok = (int64_t)blockIdx.x * wpb + wave; tok < p.n_tok; tok += stride) {
     const S* yr = (const S*)p.y + tok * p.y_stride;
     const S* pvr = p.pv ? (const S*)p.pv + tok * (int64_t)p.D : nullptr;
-    S* gyr = (S*)p.gy + tok * (int64_t)p.P;
+    const S* pkr = p.pk ? (const S*)p.pk + tok * (int64_t)p.R : nullptr;
     const S* gor = p.gout ? (const S*)p.gout + tok * p.gout_stride : nullptr;
-    // ---- value columns: the grown partial value's gradient
-    float dot = 0.f;
-    if (vnorm && gor) {  // rms-norm backward needs <g, x> over the row first
-      for (int v = lane; v < nv; v += kWave) {
-        float f[E], g[E];
-        grown_value<DT, E>(p, yr, pvr, v, f);
-        load_vec<DT, E, true>(gor + v * E, g);
+    const S* gkr = p.gkey ? (const S*)p.gkey + tok * (int64_t)p.R : nullptr;
+    S* gyr = (S*)p.gy + tok * (int64_t)p.P;
+    // ---- every load of the token
+    uint32_t xb[KJ], gb[KJ], pb[KJ];
+    float inv[KJ];
+    key_load<DT, KJ>(yr + p.D, p.R, nj, lane, xb);
+    if (gkr) key_load<DT, KJ>(gkr, p.R, nj, lane, gb);
+    if (key_ds && pkr) key_load<DT, KJ>(pkr, p.R, nj, lane, pb);
+    key_inv_load<KJ>(p, tok, nj, lane, inv);
+    Raw<DT, E> graw[AV > 0 ? AV : 1];
+    AccRow<DT, E, AV> a;
+    if constexpr (resident) {
+      if (gor) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) dot += g[e] * f[e];
+        for (int c = 0; c < AV; ++c)
+          if (c < nc) load_raw<DT, E, true>(gor + min(lane + c * kWave, nv - 1) * E, graw[c]);
       }
-      dot = wave_sum(dot);
+      if (need_grown) acc_row_load<DT, E, AV>(yr, pvr, nv, nc, lane, a);
     }
     const float inv_v = (vnorm && gor) ? p.vinv[tok] : 1.f;  // the host requires vinv with a value gradient
-    const float k3 = inv_v * inv_v * inv_v * (dot / (float)p.D);
-    for (int v = lane; v < nv; v += kWave) {
-      float g[E];
-      if (gor) {
-        load_vec<DT, E, true>(gor + v * E, g);
-      } else {
+    float x[KJ], g[KJ], pkv[KJ];
 #pragma unroll
-        for (int e = 0; e < E; ++e) g[e] = 0.f;
-      }
-      if (vnorm && gor) {
-        float f[E];
-        grown_value<DT, E>(p, yr, pvr, v, f);
+    for (int j = 0; j < KJ; ++j) g[j] = pkv[j] = 0.f;
+    key_floats<DT, KJ>(xb, p.R, nj, lane, x);
+    if (gkr) key_floats<DT, KJ>(gb, p.R, nj, lane, g);
+    if (key_ds && pkr) key_floats<DT, KJ>(pb, p.R, nj, lane, pkv);
+    // ---- value columns: the grown partial value's gradient
+    if constexpr (resident) {
+      float gv[AV][E], f[AV][E];
+      float dot = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) g[e] = DT::rnd(inv_v * g[e] - f[e] * k3);
-      } else if (complete) {
-        if (want_ds) {
-          float f[E];
-          grown_value<DT, E>(p, yr, pvr, v, f);
+      for (int c = 0; c < AV; ++c) {
+        if (c < nc) {
+          if (gor) {
+            unpack<DT, E>(graw[c], gv[c]);
+          } else {
 #pragma unroll
-          for (int e = 0; e < E; ++e) acc_v += DT::rnd(g[e] * f[e]);
+            for (int e = 0; e < E; ++e) gv[c][e] = 0.f;
+          }
+          if (need_grown) {
+            acc_row_grown<DT, E, AV>(a, pvr != nullptr, c, f[c]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) f[c][e] = 0.f;
+          }
+          if (lane + c * kWave >= nv) {  // a re-read vector: contributes nothing
+#pragma unroll
+            for (int e = 0; e < E; ++e) gv[c][e] = 0.f;
+          }
+          if (vnorm) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) dot += gv[c][e] * f[c][e];
+          }
         }
-#pragma unroll
-        for (int e = 0; e < E; ++e) g[e] = DT::rnd(g[e] * s);
       }
-      store_vec<DT, E, true>(gyr + v * E, g);
+      const float k3 = vnorm && gor ? inv_v * inv_v * inv_v * (wave_sum(dot) / (float)p.D) : 0.f;
+#pragma unroll
+      for (int c = 0; c < AV; ++c) {
+        const int v = lane + c * kWave;
+        if (c < nc && v < nv) {
+          grown_grad<DT, E>(vnorm && gor, complete, want_ds, s, inv_v, k3, f[c], gv[c], acc_v);
+          store_vec<DT, E, true>(gyr + v * E, gv[c]);
+        }
+      }
+    } else {
+      float dot = 0.f;
+      if (vnorm && gor) {  // rms-norm backward needs <g, x> over the row first
+        for (int v = lane; v < nv; v += kWave) {
+          float f[E], gg[E];
+          grown_value<DT, E>(p, yr, pvr, v, f);
+          load_vec<DT, E, true>(gor + v * E, gg);
+#pragma unroll
+          for (int e = 0; e < E; ++e) dot += gg[e] * f[e];
+        }
+        dot = wave_sum(dot);
+      }
+      const float k3 = inv_v * inv_v * inv_v * (dot / (float)p.D);
+      for (int v = lane; v < nv; v += kWave) {
+        float gg[E], f[E];
+        if (gor) {
+          load_vec<DT, E, true>(gor + v * E, gg);
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) gg[e] = 0.f;
+        }
+        if (need_grown) {
+          grown_value<DT, E>(p, yr, pvr, v, f);
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) f[e] = 0.f;
+        }
+        grown_grad<DT, E>(vnorm && gor, complete, want_ds, s, inv_v, k3, f, gg, acc_v);
+        store_vec<DT, E, true>(gyr + v * E, gg);
+      }
     }
     // ---- key columns
-    const S* gkr = p.gkey ? (const S*)p.gkey + tok * (int64_t)p.R : nullptr;
-    const S* pkr = p.pk ? (const S*)p.pk + tok * (int64_t)p.R : nullptr;
-    float x[kKsJ], g[kKsJ], inv[kKsJ];
-#pragma unroll
-    for (int j = 0; j < kKsJ; ++j) {
-      const int r = lane + j * kWave;
-      x[j] = r < p.R ? DT::load1(yr + p.D + r) : 0.f;
-      g[j] = (gkr && r < p.R) ? DT::load1(gkr + r) : 0.f;
-      inv[j] = (p.key_norm && r < p.R) ? p.inv[tok * p.H + r / p.hd] : 1.f;
-    }
     if (complete && !vnorm && p.scale_key) {
       // key = rnd(grown key * s): the grown key's gradient is rnd(g * s)
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
-        if (want_ds && gkr && r < p.R) {
+        if (key_ds && r < p.R) {
           const float kt = p.key_norm ? DT::rnd(x[j] * inv[j]) : x[j];
-          const float kg = pkr ? DT::rnd(DT::load1(pkr + r) + kt) : kt;
+          const float kg = pkr ? DT::rnd(pkv[j] + kt) : kt;
           acc_k += DT::rnd(g[j] * kg);
         }
         g[j] = DT::rnd(g[j] * s);
@@ -331,12 +513,12 @@ __global__ void __launch_bounds__(256) block_accum_bwd_kernel(const KeySplitPara
       }
     }
     if (p.key_norm) {
-      float gx[kKsJ], kd[kKsJ];
+      float gx[KJ], kd[KJ];
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) gx[j] = g[j] * x[j];
-      head_sums(p, gx, kd);
+      for (int j = 0; j < KJ; ++j) gx[j] = g[j] * x[j];
+      head_sums<KJ>(p, gx, kd);
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         if (r < p.R) {
           const float k3k = inv[j] * inv[j] * inv[j] * (kd[j] / (float)p.hd);
@@ -345,7 +527,7 @@ __global__ void __launch_bounds__(256) block_accum_bwd_kernel(const KeySplitPara
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < kKsJ; ++j) {
+      for (int j = 0; j < KJ; ++j) {
         const int r = lane + j * kWave;
         if (r < p.R) DT::store1(gyr + p.D + r, g[j]);
       }
@@ -368,34 +550,52 @@ __global__ void __launch_bounds__(256) block_accum_bwd_kernel(const KeySplitPara
   }
 }
 
-template <class DT>
+template <class DT, int KJ>
 static hipError_t keyed_split_t(bool bwd, const KeySplitParams& p, const Launch& L, hipStream_t st) {
   constexpr int EV = 16 / sizeof(typename DT::S);
   const dim3 g(L.grid), b(L.teams * kWave);
   if (p.accum) {
-    if (bwd) {
-      if (L.vec) hipLaunchKernelGGL((block_accum_bwd_kernel<DT, EV>), g, b, 0, st, p);
-      else hipLaunchKernelGGL((block_accum_bwd_kernel<DT, 1>), g, b, 0, st, p);
+    // vectors per lane of a value row: up to 2 or 4 (held in registers) or more (a loop)
+    const int nc = (p.D / (L.vec ? EV : 1) + kWave - 1) / kWave;
+    if (bwd && p.accum == 2 && (p.value_norm || p.partials)) {
+      if (L.vec && nc <= 2) hipLaunchKernelGGL((block_accum_bwd_kernel<DT, EV, 2, KJ, true>), g, b, 0, st, p);
+      else if (L.vec) hipLaunchKernelGGL((block_accum_bwd_kernel<DT, EV, 0, KJ, true>), g, b, 0, st, p);
+      else hipLaunchKernelGGL((block_accum_bwd_kernel<DT, 1, 0, KJ, true>), g, b, 0, st, p);
+    } else if (bwd) {
+      if (L.vec && nc <= 2) hipLaunchKernelGGL((block_accum_bwd_kernel<DT, EV, 2, KJ, false>), g, b, 0, st, p);
+      else if (L.vec && nc <= 4) hipLaunchKernelGGL((block_accum_bwd_kernel<DT, EV, 4, KJ, false>), g, b, 0, st, p);
+      else if (L.vec) hipLaunchKernelGGL((block_accum_bwd_kernel<DT, EV, 0, KJ, false>), g, b, 0, st, p);
+      else hipLaunchKernelGGL((block_accum_bwd_kernel<DT, 1, 0, KJ, false>), g, b, 0, st, p);
     } else {
-      if (L.vec) hipLaunchKernelGGL((block_accum_fwd_kernel<DT, EV>), g, b, 0, st, p);
-      else hipLaunchKernelGGL((block_accum_fwd_kernel<DT, 1>), g, b, 0, st, p);
+      if (L.vec && nc <= 2) hipLaunchKernelGGL((block_accum_fwd_kernel<DT, EV, 2, KJ>), g, b, 0, st, p);
+      else if (L.vec && nc <= 4) hipLaunchKernelGGL((block_accum_fwd_kernel<DT, EV, 4, KJ>), g, b, 0, st, p);
+      else if (L.vec) hipLaunchKernelGGL((block_accum_fwd_kernel<DT, EV, 0, KJ>), g, b, 0, st, p);
+      else hipLaunchKernelGGL((block_accum_fwd_kernel<DT, 1, 0, KJ>), g, b, 0, st, p);
     }
   } else if (bwd) {
-    if (L.vec) hipLaunchKernelGGL((keyed_split_bwd_kernel<DT, EV>), g, b, 0, st, p);
-    else hipLaunchKernelGGL((keyed_split_bwd_kernel<DT, 1>), g, b, 0, st, p);
+    if (L.vec) hipLaunchKernelGGL((keyed_split_bwd_kernel<DT, EV, KJ>), g, b, 0, st, p);
+    else hipLaunchKernelGGL((keyed_split_bwd_kernel<DT, 1, KJ>), g, b, 0, st, p);
   } else {
-    if (L.vec) hipLaunchKernelGGL((keyed_split_fwd_kernel<DT, EV>), g, b, 0, st, p);
-    else hipLaunchKernelGGL((keyed_split_fwd_kernel<DT, 1>), g, b, 0, st, p);
+    if (L.vec) hipLaunchKernelGGL((keyed_split_fwd_kernel<DT, EV, KJ>), g, b, 0, st, p);
+    else hipLaunchKernelGGL((keyed_split_fwd_kernel<DT, 1, KJ>), g, b, 0, st, p);
   }
   return hipGetLastError();
 }
 
-static hipError_t keyed_split(int dtype, bool bwd, const KeySplitParams& p, const Launch& L, hipStream_t st) {
+template <int KJ>
+static hipError_t keyed_split_kj(int dtype, bool bwd, const KeySplitParams& p, const Launch& L, hipStream_t st) {
   switch (dtype) {
-    case ATTNRES_DTYPE_F32: return keyed_split_t<F32>(bwd, p, L, st);
-    case ATTNRES_DTYPE_BF16: return keyed_split_t<BF16>(bwd, p, L, st);
-    default: return keyed_split_t<F16>(bwd, p, L, st);
+    case ATTNRES_DTYPE_F32: return keyed_split_t<F32, KJ>(bwd, p, L, st);
+    case ATTNRES_DTYPE_BF16: return keyed_split_t<BF16, KJ>(bwd, p, L, st);
+    default: return keyed_split_t<F16, KJ>(bwd, p, L, st);
   }
+}
+
+static hipError_t keyed_split(int dtype, bool bwd, const KeySplitParams& p, const Launch& L, hipStream_t st) {
+  const int nj = (p.R + kWave - 1) / kWave;  // the host keeps R <= 256
+  if (nj <= 1) return keyed_split_kj<1>(dtype, bwd, p, L, st);
+  if (nj <= 2) return keyed_split_kj<2>(dtype, bwd, p, L, st);
+  return keyed_split_kj<4>(dtype, bwd, p, L, st);
 }
 
 hipError_t launch_keyed_split_forward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st) {
