@@ -81,6 +81,25 @@ __device__ __forceinline__ float bits_to_float(uint32_t u) {
   else return f16_bits_to_f32(u);
 }
 
+// Elements r = lane + stride * j (j < K) of a short row of R elements: loaded
+// as raw bits and converted only after every load of the row's token is issued
+// -- a 16-bit element converted right after its load would make the wave wait
+// for that load (and every earlier one) before it issues the next.  Every
+// lane issues all K loads, unconditionally: indices past R re-read element
+// R - 1 (in bounds, a cache hit) and convert to 0; a load under a branch
+// would be merged with a zero-extension that again waits for it.
+template <class DT, int K>
+__device__ __forceinline__ void row_bits_load(const typename DT::S* row, int R, int lane, int stride,
+                                              uint32_t (&b)[K]) {
+#pragma unroll
+  for (int j = 0; j < K; ++j) b[j] = load_bits1<DT>(row + min(lane + j * stride, R - 1));
+}
+template <class DT, int K>
+__device__ __forceinline__ void row_bits_floats(const uint32_t (&b)[K], int R, int lane, int stride, float (&f)[K]) {
+#pragma unroll
+  for (int j = 0; j < K; ++j) f[j] = lane + j * stride < R ? bits_to_float<DT>(b[j]) : 0.f;
+}
+
 // A block summary's scale: a python number scales in fp32; a scale tensor takes
 // the value dtype first (model.py:985 casts the learned scale; a 0-dim fp32
 // device tensor multiplying a 16-bit tensor is cast to that dtype the same way)

@@ -23,21 +23,16 @@ namespace attnres {
 // 128 or 256), a template parameter so that short keys keep few registers.
 
 // Key rows are short (R <= 256): the lane holds elements r = lane + 64 j for
-// j < nj = ceil(R / 64).  They are loaded as raw bits and converted only after
-// every load of the token has been issued: a 16-bit element converted right
-// after its load makes the wave wait for that load before issuing the next.
-// Lanes past R re-read element R - 1 (in bounds) and convert to 0.
+// j < nj = ceil(R / 64), loaded as raw bits (row_bits_load) and converted after
+// every load of the token is issued.
 template <class DT, int KJ>
 __device__ __forceinline__ void key_load(const typename DT::S* row, int R, int nj, int lane, uint32_t (&b)[KJ]) {
-#pragma unroll
-  for (int j = 0; j < KJ; ++j)
-    if (j < nj) b[j] = load_bits1<DT>(row + min(lane + j * kWave, R - 1));
+  row_bits_load<DT, KJ>(row, R, lane, kWave, b);
 }
 
 template <class DT, int KJ>
 __device__ __forceinline__ void key_floats(const uint32_t (&b)[KJ], int R, int nj, int lane, float (&f)[KJ]) {
-#pragma unroll
-  for (int j = 0; j < KJ; ++j) f[j] = (j < nj && lane + j * kWave < R) ? bits_to_float<DT>(b[j]) : 0.f;
+  row_bits_floats<DT, KJ>(b, R, lane, kWave, f);
 }
 
 // the key heads' 1/rms values of the lane's elements (forward's saved values)

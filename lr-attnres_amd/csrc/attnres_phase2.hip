@@ -69,16 +69,11 @@ __device__ __forceinline__ void p2_load(const Phase2Params& p, int64_t tok, cons
       if (with_grad) load_raw<DT, E, true>(gp + cl.eoff[c], r.g[c]);
     }
   }
-  if (LR) {
-    const S* kp = (const S*)p.pk + tok * p.pk_stride;
-#pragma unroll
-    for (int j = 0; j < kP2KPT; ++j) {
-      const int r_ = tid + j * bd;
-      r.kr[j] = r_ < p.R ? DT::load1(kp + r_) : 0.f;
-    }
-  }
+  uint32_t kb[kP2KPT];
+  if (LR) row_bits_load<DT, kP2KPT>((const S*)p.pk + tok * p.pk_stride, p.R, tid, bd, kb);
   r.lse = p.lse[tok];
   r.logit = p.logit_given ? load_any(p.plogit, tok, p.pl_dt) : 0.f;
+  if (LR) row_bits_floats<DT, kP2KPT>(kb, p.R, tid, bd, r.kr);
 }
 
 template <class DT, int E, int CB, bool LR>
@@ -185,10 +180,13 @@ __global__ void __launch_bounds__(512) phase2_fwd_kernel(const Phase2Params p) {
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[c][e] = 0.f;
   }
+  if (LR && !p.logit_given) {
+    uint32_t qb[kP2KPT];
+    row_bits_load<DT, kP2KPT>((const S*)p.q, p.R, tid, bd, qb);
+    row_bits_floats<DT, kP2KPT>(qb, p.R, tid, bd, qk);
+  } else {
 #pragma unroll
-  for (int j = 0; j < kP2KPT; ++j) {
-    const int r = tid + j * bd;
-    qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
+    for (int j = 0; j < kP2KPT; ++j) qk[j] = 0.f;
   }
 
   P2Raw<DT, E, CB> nxt;
@@ -240,10 +238,13 @@ __global__ void __launch_bounds__(512) phase2_bwd_kernel(const Phase2Params p) {
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[c][e] = 0.f;
   }
+  if (LR && !p.logit_given) {
+    uint32_t qb[kP2KPT];
+    row_bits_load<DT, kP2KPT>((const S*)p.q, p.R, tid, bd, qb);
+    row_bits_floats<DT, kP2KPT>(qb, p.R, tid, bd, qk);
+  } else {
 #pragma unroll
-  for (int j = 0; j < kP2KPT; ++j) {
-    const int r = tid + j * bd;
-    qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
+    for (int j = 0; j < kP2KPT; ++j) qk[j] = 0.f;
   }
   float dq_b[CB][E], dq_l[kP2KPT];
 #pragma unroll
@@ -474,16 +475,11 @@ __device__ __forceinline__ void p2w_token(const Phase2Params& p, int64_t tok, co
       load_raw<DT, E, true>(pvp + cl.eoff[c], st.pv[c]);
       load_raw<DT, E, true>(itp + cl.eoff[c], itr[c]);
     }
-  if (LR) {
-    const S* kp = (const S*)p.pk + tok * p.pk_stride;
-#pragma unroll
-    for (int j = 0; j < kP2KPT; ++j) {
-      const int r = lane + j * kWave;
-      st.kr[j] = r < p.R ? DT::load1(kp + r) : 0.f;
-    }
-  }
+  uint32_t kb[kP2KPT];
+  if (LR) row_bits_load<DT, kP2KPT>((const S*)p.pk + tok * p.pk_stride, p.R, lane, kWave, kb);
   const float lse = p.lse[tok];
   const float given = p.logit_given ? load_any(p.plogit, tok, p.pl_dt) : 0.f;
+  if (LR) row_bits_floats<DT, kP2KPT>(kb, p.R, lane, kWave, st.kr);
 #pragma unroll
   for (int c = 0; c < CB; ++c) {
     float pr[E];
@@ -563,10 +559,13 @@ __device__ __forceinline__ void p2w_queries(const Phase2Params& p, const Cols<CB
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[c][e] = 0.f;
   }
+  if (LR && !p.logit_given) {
+    uint32_t qb[kP2KPT];
+    row_bits_load<DT, kP2KPT>((const S*)p.q, p.R, lane, kWave, qb);
+    row_bits_floats<DT, kP2KPT>(qb, p.R, lane, kWave, qk);
+  } else {
 #pragma unroll
-  for (int j = 0; j < kP2KPT; ++j) {
-    const int r = lane + j * kWave;
-    qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
+    for (int j = 0; j < kP2KPT; ++j) qk[j] = 0.f;
   }
 }
 
@@ -648,10 +647,13 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
 #pragma unroll
       for (int i = 0; i < Vec<DT, E>::kWords; ++i) qr[c].w[i] = 0u;
   }
+  if (LR && !p.logit_given) {
+    uint32_t qb[kP2KPT];
+    row_bits_load<DT, kP2KPT>((const S*)p.q, p.R, lane, kWave, qb);
+    row_bits_floats<DT, kP2KPT>(qb, p.R, lane, kWave, qk);
+  } else {
 #pragma unroll
-  for (int j = 0; j < kP2KPT; ++j) {
-    const int r = lane + j * kWave;
-    qk[j] = (LR && !p.logit_given && r < p.R) ? DT::load1((const S*)p.q + r) : 0.f;
+    for (int j = 0; j < kP2KPT; ++j) qk[j] = 0.f;
   }
 
   float dq_b[CB][E], dq_l[kP2KPT];
@@ -686,16 +688,11 @@ __global__ void __launch_bounds__(256) phase2_wave_bwd_kernel(const Phase2Params
       }
     }
     float kr[kP2KPT], kv[kP2KPT], kl[kP2KPT];
-    if (LR) {
-      const S* kp = (const S*)p.pk + tok * p.pk_stride;
-#pragma unroll
-      for (int j = 0; j < kP2KPT; ++j) {
-        const int r = lane + j * kWave;
-        kr[j] = r < p.R ? DT::load1(kp + r) : 0.f;
-      }
-    }
+    uint32_t kb[kP2KPT];
+    if (LR) row_bits_load<DT, kP2KPT>((const S*)p.pk + tok * p.pk_stride, p.R, lane, kWave, kb);
     const float lse = p.lse[tok];
     const float given = p.logit_given ? load_any(p.plogit, tok, p.pl_dt) : 0.f;
+    if (LR) row_bits_floats<DT, kP2KPT>(kb, p.R, lane, kWave, kr);
 
     // ---- forward recompute: scaled partial (packed), key, logit, sigmoid
 #pragma unroll
