@@ -132,6 +132,13 @@ int attnres_kernel_timing(int enable);
  * a negative error code (timing not enabled, bad buffer, HIP error). */
 int attnres_kernel_times(float* ms, int max_n);
 
+/* Test hook, no counterpart in the reference.  on = 1 makes the phase-2 entry
+ * points run the workgroup-per-token kernels for every shape (process-wide),
+ * so that a test can compare them with the one-wave-per-token kernels the
+ * library otherwise picks from the shape; on = 0 restores that choice.  The
+ * two give the same per-token results.  Returns ATTNRES_OK or ATTNRES_EINVAL. */
+int attnres_test_phase2_block_layout(int on);
+
 /*
  * Forward read.  Writes out [n_tok, dim] (dtype); when `weights` is not NULL
  * also the fp32 softmax weights [n_tok, heads, n_src] (the backward needs

@@ -243,6 +243,8 @@ def load() -> ctypes.CDLL:
                                                  POINTER(c_float), c_void_p, c_size_t, c_void_p]
     lib.attnres_kernel_timing.restype = c_int
     lib.attnres_kernel_timing.argtypes = [c_int]
+    lib.attnres_test_phase2_block_layout.restype = c_int
+    lib.attnres_test_phase2_block_layout.argtypes = [c_int]
     lib.attnres_kernel_times.restype = c_int
     lib.attnres_kernel_times.argtypes = [POINTER(c_float), c_int]
     v = lib.attnres_abi_version()

@@ -5,6 +5,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -25,16 +26,35 @@ thread_local std::string g_last_error;
 constexpr int kTimerPairs = 256;
 struct KernelTimer {
   bool on = false;
+  bool failed = false;  // an event record failed since the last attnres_kernel_times
   int n = 0;
   hipEvent_t ev[2 * kTimerPairs];
 };
 KernelTimer g_timer;
 
-inline void timer_begin(hipStream_t st) {
-  if (g_timer.on && g_timer.n < kTimerPairs) (void)hipEventRecord(g_timer.ev[2 * g_timer.n], st);
+// Test hook (attnres_test_phase2_block_layout): phase 2 on the workgroup-per-token kernels.
+std::atomic<int> g_phase2_block_layout{0};
+
+// Whether a start event was recorded for this call: not while the stream is
+// being captured into a graph (the pair would land in the graph).
+inline bool timer_begin(hipStream_t st) {
+  if (!g_timer.on || g_timer.n >= kTimerPairs) return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  if (hipEventRecord(g_timer.ev[2 * g_timer.n], st) != hipSuccess) {
+    g_timer.failed = true;
+    return false;
+  }
+  return true;
 }
-inline void timer_end(hipStream_t st) {
-  if (g_timer.on && g_timer.n < kTimerPairs) (void)hipEventRecord(g_timer.ev[2 * g_timer.n++ + 1], st);
+// A pair counts only around a kernel that launched and when both records succeeded.
+inline void timer_end(hipStream_t st, bool began, hipError_t launch) {
+  if (!began || launch != hipSuccess) return;
+  if (hipEventRecord(g_timer.ev[2 * g_timer.n + 1], st) != hipSuccess) {
+    g_timer.failed = true;
+    return;
+  }
+  ++g_timer.n;
 }
 
 int fail(int code, const char* fmt, ...) {
@@ -401,10 +421,12 @@ extern "C" int attnres_kernel_timing(int enable) {
       }
     }
     g_timer.on = true;
+    g_timer.failed = false;
     g_timer.n = 0;
   } else if (!enable && g_timer.on) {
     for (int i = 0; i < 2 * kTimerPairs; ++i) (void)hipEventDestroy(g_timer.ev[i]);
     g_timer.on = false;
+    g_timer.failed = false;
     g_timer.n = 0;
   }
   return ATTNRES_OK;
@@ -413,6 +435,11 @@ extern "C" int attnres_kernel_timing(int enable) {
 extern "C" int attnres_kernel_times(float* ms, int max_n) {
   if (!g_timer.on) return fail(ATTNRES_EINVAL, "kernel timing is not enabled");
   if (max_n < 0 || (max_n > 0 && !ms)) return fail(ATTNRES_EINVAL, "bad output buffer");
+  if (g_timer.failed) {
+    g_timer.failed = false;
+    g_timer.n = 0;
+    return fail(ATTNRES_ELAUNCH, "a kernel timing event record failed; the recording is discarded");
+  }
   const int n = g_timer.n < max_n ? g_timer.n : max_n;
   for (int i = 0; i < n; ++i) {
     hipError_t e = hipEventSynchronize(g_timer.ev[2 * i + 1]);
@@ -422,6 +449,12 @@ extern "C" int attnres_kernel_times(float* ms, int max_n) {
   const int recorded = g_timer.n;
   g_timer.n = 0;
   return recorded < max_n ? recorded : max_n;
+}
+
+extern "C" int attnres_test_phase2_block_layout(int on) {
+  if (on != 0 && on != 1) return fail(ATTNRES_EINVAL, "on must be 0 or 1, got %d", on);
+  g_phase2_block_layout.store(on, std::memory_order_relaxed);
+  return ATTNRES_OK;
 }
 
 extern "C" size_t attnres_read_backward_workspace_size(const attnres_read_desc* d) {
@@ -458,7 +491,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
   L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;
-  timer_begin(st);
+  const bool timed = timer_begin(st);
   if (d->mode == ATTNRES_MODE_AVERAGE) {
     L.lds = 32 * sizeof(float);
     err = launch_average_forward(d->dtype, p, L, st);
@@ -500,7 +533,7 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       err = launch_base_forward(d->dtype, p, L, st);
     }
   }
-  timer_end(st);
+  timer_end(st, timed, err);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "forward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
 }
@@ -591,7 +624,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
   int partials_layout = kPartRowMajor;  // fast LR: slot-major; fast base: tiled (slot-major for tiny inputs)
   BaseFastPlan bf;
   hipError_t err;
-  timer_begin(st);
+  const bool timed = timer_begin(st);
   if (d->mode == ATTNRES_MODE_AVERAGE) {
     L.lds = 32 * sizeof(float);
     err = launch_average_backward(d->dtype, bp, L, st);
@@ -661,7 +694,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "base backward needs %zu bytes of LDS", L.lds);
     err = launch_base_backward(d->dtype, bp, L, st);
   }
-  timer_end(st);
+  timer_end(st, timed, err);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "backward launch failed: %s", hipGetErrorString(err));
 
   if (PL.n_part > 0) {
@@ -917,16 +950,14 @@ int phase2_waves(const attnres_phase2_desc* d, const PhasePlan& pl) {
 // lane and the LR key with at most 4: fp32 rows in 16-byte vectors (1-4 per
 // lane), 16-bit rows in 16-byte vectors (1-2 per lane) or, where those would
 // leave lanes idle (D <= 256, 512 < D <= 768), in 8-byte vectors (1 or 3).
-// ATTNRES_PHASE2_LAYOUT=block (read by the host on every call) keeps the
-// workgroup-per-token kernels: the two layouts give the same per-token
-// results, which a test checks with this switch.
+// attnres_test_phase2_block_layout(1) keeps the workgroup-per-token kernels
+// instead: the two layouts give the same per-token results, which a test checks.
 constexpr int kPhase2Teams = 4;  // tokens (waves) per workgroup
 struct P2Wave {
   int vb, cb, ncols;
 };
 bool phase2_wave_plan(const attnres_phase2_desc* d, const PhasePlan& pl, P2Wave* w) {
-  const char* env = getenv("ATTNRES_PHASE2_LAYOUT");
-  if (env && strcmp(env, "block") == 0) return false;
+  if (g_phase2_block_layout.load(std::memory_order_relaxed)) return false;
   if (!pl.vec || d->rank > 4 * kWaveSize) return false;
   const int D = d->dim;
   if (elem_size(d->dtype) == 4) {

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
                             "attnres_keyed_split_forward", "attnres_keyed_split_backward",
                             "attnres_keyed_logits_forward", "attnres_keyed_logits_backward",
                             "attnres_keyed_logits_backward_workspace_size", "attnres_kernel_timing",
-                            "attnres_kernel_times", "attnres_read_backward_noalloc",
+                            "attnres_kernel_times", "attnres_read_backward_noalloc", "attnres_test_phase2_block_layout",
                             "attnres_block_accum_forward", "attnres_block_accum_backward",
                             "attnres_block_accum_backward_workspace_size"])
     for n in names:
@@ -476,3 +476,14 @@ def test_block_accumulate_rejects_bad_calls_on_the_host():
     with pytest.raises(RuntimeError, match="value_norm"):
         ops.lrid_block_accumulate(torch.randn(2, 3, 80), None, None, 64, 16, complete=True, value_norm=True,
                                   scale_key=True)
+
+
+@needs_lib
+def test_phase2_layout_hook_validates_and_kernel_times_need_timing():
+    lib = H.load()
+    assert lib.attnres_test_phase2_block_layout(2) == -1
+    assert b"on must be 0 or 1" in lib.attnres_last_error()
+    assert lib.attnres_test_phase2_block_layout(0) == 0
+    buf = (ctypes.c_float * 4)()
+    assert lib.attnres_kernel_times(buf, 4) == -1
+    assert b"not enabled" in lib.attnres_last_error()

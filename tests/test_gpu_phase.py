@@ -303,10 +303,10 @@ def test_phase2_many_tokens_matches_oracle(variant, dtype):
 
 @pytest.mark.parametrize("variant", ["base", "lrid", "lrid_addcmul", "logit"])
 @pytest.mark.parametrize("D", [512, 1024])
-def test_phase2_wave_layout_matches_block_layout(variant, D, monkeypatch):
+def test_phase2_wave_layout_matches_block_layout(variant, D):
     """For rows one wave covers with 16-byte vectors, phase 2 runs one wave
-    per token; the workgroup-per-token kernels (ATTNRES_PHASE2_LAYOUT=block)
-    sum each row in the same order, so every per-token output and gradient
+    per token; the workgroup-per-token kernels (selected through the test
+    hook attnres_test_phase2_block_layout) sum each row in the same order, so every per-token output and gradient
     is bit-identical in bf16.  Cross-token sums (query, bias) walk tokens in
     another order and are compared at the reduced bound.  (D=768 uses 8-byte
     vectors, whose sums associate differently; it is checked against the
@@ -314,8 +314,12 @@ def test_phase2_wave_layout_matches_block_layout(variant, D, monkeypatch):
     t = _phase2_case(700 + D + len(variant), torch.bfloat16, 4, 4100, D, variant)
     m = dict(variant=variant, key_norm=True, bias=0.4, bias_tensor=True, normalize_output=True, scale=0.125)
     out_w, g_w = _phase2_hip(t, m)
-    monkeypatch.setenv("ATTNRES_PHASE2_LAYOUT", "block")
-    out_b, g_b = _phase2_hip(t, m)
+    lib = H.load()
+    assert lib.attnres_test_phase2_block_layout(1) == 0
+    try:
+        out_b, g_b = _phase2_hip(t, m)
+    finally:
+        assert lib.attnres_test_phase2_block_layout(0) == 0
     assert torch.equal(out_w, out_b)
     for key in g_w:
         if key in ("dquery", "dbias"):
