@@ -393,51 +393,70 @@ def time_api(c, wl, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(c, budget_s):
-    """The eager restatement (oracle/) on the host cores, bounded token sample."""
+    """The eager restatement (oracle/) on the host cores, on a bounded token
+    sample (B=1, T=2048) of the workload: fp32 and bf16, each the median of
+    >= 5 timed iterations after 2 warmups (time.perf_counter), as tokens/s and
+    effective GB/s from the same byte formula as the GPU line.  ``value`` is
+    the workload dtype's median."""
     from oracle import attnres_oracle as O
 
     cores = len(os.sched_getaffinity(0))
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     torch.set_num_threads(cores)
-    g = torch.Generator().manual_seed(1)
-    D, N, R, Hh, dt = c["D"], c["N"], c["R"], c["H"], c["dtype"]
-    T = 2048
-    B = 1
-    mk = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(dt).requires_grad_(True)
-    vals = [mk(B, T, D) for _ in range(N)]
-    keys = [mk(B, T, R) for _ in range(N)] if R else []
-    up = torch.randn(B, T, D, generator=g).to(dt)
-    if c["kind"] == "base":
-        q = mk(D, std=c["qstd"])
-    else:
-        q = mk(Hh, R // Hh, std=c["qstd"])
-    qd = mk(B, T, Hh, R // Hh) if c["kind"] == "lr_gated" else None
-    gt = mk(B, T, Hh) if c["kind"] == "lr_gated" else None
+    D, N, R, Hh = c["D"], c["N"], c["R"], c["H"]
+    T, B = 2048, 1
+    by = {}
+    for name, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        g = torch.Generator().manual_seed(1)
+        mk = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(dt).requires_grad_(True)  # noqa: E731
+        vals = [mk(B, T, D) for _ in range(N)]
+        keys = [mk(B, T, R) for _ in range(N)] if R else []
+        up = torch.randn(B, T, D, generator=g).to(dt)
+        q = mk(D, std=c["qstd"]) if c["kind"] == "base" else mk(Hh, R // Hh, std=c["qstd"])
+        qd = mk(B, T, Hh, R // Hh) if c["kind"] == "lr_gated" else None
+        gt = mk(B, T, Hh) if c["kind"] == "lr_gated" else None
 
-    def step():
-        if c["kind"] == "base":
-            out = O.attention_residual_read_ref(vals, q, True)
-        elif c["kind"] == "lr":
-            out = O.lrid_attention_residual_read_ref(vals, keys, q, Hh, c["scale"], True)
-        else:
-            qq = O.gated_query_ref(q.float(), qd.float(), gt.float(), Hh, "sigmoid")
-            out = O.lrid_attention_residual_read_ref(vals, keys, qq, Hh, c["scale"], True)
-        if not c.get("fwd_only"):
-            out.backward(up)
+        def step():
+            if c["kind"] == "base":
+                out = O.attention_residual_read_ref(vals, q, True)
+            elif c["kind"] == "lr":
+                out = O.lrid_attention_residual_read_ref(vals, keys, q, Hh, c["scale"], True)
+            else:
+                qq = O.gated_query_ref(q.float(), qd.float(), gt.float(), Hh, "sigmoid")
+                out = O.lrid_attention_residual_read_ref(vals, keys, qq, Hh, c["scale"], True)
+            if not c.get("fwd_only"):
+                out.backward(up)
 
-    step()  # warmup
-    t0 = time.perf_counter()
-    step()
-    one = time.perf_counter() - t0
-    iters = max(2, min(2000, int(budget_s / max(one, 1e-4))))
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        step()
-    el = time.perf_counter() - t0
-    return dict(value=B * T * iters / el, unit="tokens/s", cores=cores, kind="port",
+        for _ in range(2):
+            step()
+        times = []
+        t_end = time.perf_counter() + budget_s / 2
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+        med = sorted(times)[len(times) // 2]
+        f_b, b_b = bytes_per_token(dict(c, dtype=dt))
+        by[name] = {"tokens_per_s": round(B * T / med, 1), "gbs": round((f_b + b_b) * B * T / med / 1e9, 2),
+                    "median_s": round(med, 5), "iterations": len(times)}
+    main = "fp32" if c["dtype"] == torch.float32 else "bf16"
+    return dict(value=by[main]["tokens_per_s"], unit="tokens/s", cores=cores, kind="port",
                 sample=f"oracle eager fwd{'' if c.get('fwd_only') else '+bwd'} on B={B} T={T} tokens of the "
-                       f"workload ({dt}), {iters} iterations in {el:.1f} s, torch {torch.__version__}")
+                       f"workload's rows, median of >= 5 iterations after 2 warmups, per dtype; value is {main}; "
+                       f"torch {torch.__version__}",
+                cpu_model=_cpu_model(), by_dtype=by)
 
 
 def copy_calibration(steps, gib=1.0):
