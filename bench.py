@@ -40,7 +40,12 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
 CONFIGS = {
     "c1": dict(kind="base", B=2, T=128, D=128, N=4, R=0, H=1, scale=1.0, dtype=torch.float32, qstd=0.02,
                fwd_only=True),
-    "c2": dict(kind="base", B=8, T=1024, D=768, N=7, R=0, H=1, scale=1.0, dtype=torch.bfloat16, qstd=0.02),
+    # C2's sources as the configuration defines them (the embedding and 6 block
+    # summaries of two sublayer outputs, count**-1); two input sets alternate
+    # step by step, so that the ~200 MB one step touches is not served from the
+    # previous step's copy in the 256 MB MALL
+    "c2": dict(kind="base", B=8, T=1024, D=768, N=7, R=0, H=1, scale=1.0, dtype=torch.bfloat16, qstd=0.02,
+               block_summaries=True, sets=2),
     "c3": dict(kind="lr", B=8, T=2048, D=1024, N=13, R=64, H=4, scale=0.25, dtype=torch.bfloat16, qstd=0.02),
     "c4": dict(kind="lr_gated", B=4, T=4096, D=2048, N=17, R=128, H=8, scale=0.25, dtype=torch.bfloat16,
                qstd=0.02),
@@ -247,7 +252,12 @@ class Workload:
         B, T, D, N, R, Hh, dt = c["B"], c["T"], c["D"], c["N"], c["R"], c["H"], c["dtype"]
         self.n_tok = B * T
         rn = lambda *shape, std=1.0: (torch.randn(shape, generator=g, device=device) * std).to(dt)
-        self.values = [rn(B, T, D) for _ in range(N)]
+        if c.get("block_summaries"):
+            # the embedding, then summaries (a + b) * count**-1 of two N(0, 1) outputs
+            # in the dtype's arithmetic (model.py:990-1001)
+            self.values = [rn(B, T, D)] + [(rn(B, T, D) + rn(B, T, D)) * 0.5 for _ in range(N - 1)]
+        else:
+            self.values = [rn(B, T, D) for _ in range(N)]
         self.keys = [rn(B, T, R) for _ in range(N)] if R else []
         if c["kind"] == "base":
             self.query = rn(D, std=c["qstd"])
@@ -300,6 +310,37 @@ class Workload:
         rc = self.lib.attnres_read_backward(ctypes.byref(self.desc.c), ctypes.byref(self.grads), stream)
         if rc:
             raise RuntimeError(self.lib.attnres_last_error().decode())
+
+
+class Rotation:
+    """Several input sets of one configuration used in turn, one per step
+    (forward and backward of a step on the same set)."""
+
+    def __init__(self, sets):
+        self.sets = sets
+        self.i = 0
+        w = sets[0]
+        self.c, self.lib, self.n_tok, self.fwd_only = w.c, w.lib, w.n_tok, w.fwd_only
+
+    def __getattr__(self, name):  # inputs for the API timing: the first set's
+        return getattr(self.__dict__["sets"][0], name)
+
+    def fwd(self, stream):
+        self.sets[self.i].fwd(stream)
+        if self.fwd_only:
+            self.i = (self.i + 1) % len(self.sets)
+
+    def bwd(self, stream):
+        if self.fwd_only:
+            return
+        self.sets[self.i].bwd(stream)
+        self.i = (self.i + 1) % len(self.sets)
+
+
+def make_workload(c, device):
+    if c.get("sets", 1) > 1:
+        return Rotation([Workload(c, device, seed=i) for i in range(c["sets"])])
+    return Workload(c, device)
 
 
 def time_steps(wl, steps, warmup, stream, sv):
@@ -506,7 +547,7 @@ def main():
         bench_phase(args, dev)
         return
     c = CONFIGS[args.config]
-    wl = Workload(c, dev)
+    wl = make_workload(c, dev)
     stream = torch.cuda.current_stream(dev)
     sv = ctypes.c_void_p(stream.cuda_stream)
 
@@ -525,13 +566,15 @@ def main():
     # HBM bytes per launch of the dominant kernel, measured with rocprofv3
     # FETCH_SIZE / WRITE_SIZE (scaled by a copy of known size) and kept in
     # profiles/traffic_<config>.json; null when no measurement is recorded
-    traffic = None
+    # (only when the record names the kernel family this configuration runs)
+    traffic = traffic_kernel = None
     tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             rec = json.load(f).get("kernels", {}).get("bwd" if bwd_b else "fwd")
-        if rec:
-            traffic = rec["bytes_per_launch"]
+        family = ("lr_" if c["kind"] != "base" else "base_") + ("bwd" if bwd_b else "fwd")
+        if rec and family in rec.get("name", ""):
+            traffic, traffic_kernel = rec["bytes_per_launch"], rec["name"]
 
     res = {
         "metric": "AttnRes fwd+bwd tokens/s (d=1024,N=13,r=64,bf16); HBM GB/s as % of peak",
@@ -550,12 +593,12 @@ def main():
                    + f" read fwd+bwd B{c['B']} T{c['T']} d{c['D']} N{c['N']}"
                    + (f" r{c['R']} H{c['H']}" if c["R"] else "") + (" gated dyn query" if c["kind"] == "lr_gated"
                                                                     else ""),
-                   "tokens": n_tok, "parallelism": "single GPU"},
+                   "tokens": n_tok, "parallelism": "single GPU", "input_sets": c.get("sets", 1)},
         "hbm_gbs_step": round(gbs_step, 1),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
                      "bytes_per_token": dom_bytes, "algorithmic_bytes_per_launch": dom_bytes * n_tok,
-                     "traffic": traffic},
+                     "traffic": traffic, "traffic_kernel": traffic_kernel},
         "kernels": {"forward_ms": round(fk_ms, 5), "forward_gbs": round(fwd_gbs, 1),
                     "backward_ms": round(bk_ms, 5), "backward_gbs": round(bwd_gbs, 1),
                     "forward_call_ms": round(f_ms, 5), "backward_call_ms": round(b_ms, 5),
