@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 5
+#define ATTNRES_ABI_VERSION 6
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -93,6 +93,11 @@ typedef struct attnres_read_desc {
                                       the query (static or per-token) must be in that logit dtype and
                                       its gradient is written in it.  No gate with mixed dtypes.  Base
                                       and average reads ignore it. */
+  const void* static_keys;         /* LR: [n_src, rank] dense in key_dtype, or NULL.  Row s is added to
+                                      every key of source s before it is scored, rounded to the key
+                                      dtype -- the model's static source key (model.py:2046-2049,
+                                      LRIDStaticKey :275-289; config 4's [N, 128] key), fused here
+                                      instead of materialising key + static per source. */
 } attnres_read_desc;
 
 /* Gradient buffers for attnres_read_backward. */
@@ -109,6 +114,9 @@ typedef struct attnres_read_grads {
   float* dbias;              /* [n_src] fp32 or NULL */
   void* workspace;           /* device scratch for deterministic cross-token reductions */
   size_t workspace_bytes;
+  void* dstatic_keys;        /* LR with static_keys: [n_src, rank] key_dtype, the token sums of dkeys
+                                (each rounded to the key dtype once, as the reference's expand
+                                backward sums them), or NULL; needs dkeys */
 } attnres_read_grads;
 
 /* ABI version compiled into the library (ATTNRES_ABI_VERSION). */

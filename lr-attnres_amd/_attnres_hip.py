@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_SOURCES = 64
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -56,6 +56,7 @@ class ReadDesc(ctypes.Structure):
         ("gate_act", c_int32),
         ("logit_bias", POINTER(c_float)),
         ("key_dtype", c_int32),
+        ("static_keys", c_void_p),
     ]
 
 
@@ -75,6 +76,7 @@ class ReadGrads(ctypes.Structure):
         ("dbias", POINTER(c_float)),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("dstatic_keys", c_void_p),
     ]
 
 
@@ -294,12 +296,13 @@ class Desc:
     """Builds the C descriptor for one read; keeps the ctypes arrays alive."""
 
     def __init__(self, values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm,
-                 normalize_output, mode, gate_act, gate_per_token, eps=FLT_EPSILON):
+                 normalize_output, mode, gate_act, gate_per_token, eps=FLT_EPSILON, static_keys=None):
         v0 = values[0]
         B, T, D = v0.shape
         n = len(values)
         # the descriptor holds raw device pointers: keep the tensors alive with it
-        self._tensors = (list(values), list(keys), query, query_dyn, gate, bias)
+        self._tensors = (list(values), list(keys), query, query_dyn, gate, bias, static_keys)
+        self.has_static_keys = static_keys is not None
         self.n_src = n
         self.n_tok = B * T
         self.D = D
@@ -340,6 +343,7 @@ class Desc:
         d.gate_act = gate_act
         d.logit_bias = _fptr(bias)
         d.key_dtype = DTYPE_CODE[self.key_dtype]
+        d.static_keys = static_keys.data_ptr() if static_keys is not None else None
         self.c = d
 
 
@@ -377,8 +381,9 @@ def _row_blocks(count: int, n_tok: int, width: int, device, dtype, batched: bool
 
 def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, want_dquery: bool,
              want_dgate: bool, want_dbias: bool, query_shape, gate_shape, lr: bool, has_query_dyn: bool,
-             batched: bool = False, lead=None):
-    """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias).
+             batched: bool = False, lead=None, want_dstatic: bool = False):
+    """Launch the backward; returns (dvalues list, dkeys list, dquery, dquery_dyn, dgate, dbias,
+    dstatic_keys [N, R] | None).
 
     With ``batched`` the per-source gradients are views of one allocation per
     kind (fewer allocator calls); otherwise each is its own tensor (the
@@ -392,6 +397,7 @@ def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, wan
     dqd = torch.empty((desc.n_tok, desc.R), device=device, dtype=desc.query_dtype) if has_query_dyn else None
     dg = torch.empty(gate_shape, device=device, dtype=dtype) if want_dgate else None
     db = torch.empty((n,), device=device, dtype=torch.float32) if want_dbias else None
+    dsk = torch.empty((n, desc.R), device=device, dtype=desc.key_dtype) if want_dstatic else None
     g = ReadGrads()
     g.grad_out = grad_out.data_ptr()
     g.out_prenorm = prenorm.data_ptr() if prenorm is not None and prenorm.numel() else None
@@ -406,6 +412,7 @@ def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, wan
     g.dquery_dyn = dqd.data_ptr() if dqd is not None else None
     g.dgate = dg.data_ptr() if dg is not None else None
     g.dbias = _fptr(db)
+    g.dstatic_keys = dsk.data_ptr() if dsk is not None else None
     # workspace for the cross-token partial sums of the requested gradients
     ws_bytes = lib.attnres_read_backward_workspace_size(ctypes.byref(desc.c))
     ws = torch.empty((max(int(ws_bytes), 1),), device=device, dtype=torch.uint8)
@@ -413,7 +420,7 @@ def backward(desc: Desc, device, dtype, grad_out, prenorm, inv_rms, weights, wan
     g.workspace_bytes = int(ws_bytes)
     rc = lib.attnres_read_backward(ctypes.byref(desc.c), ctypes.byref(g), _stream(device))
     _check(rc, "backward")
-    return dvals, dkeys, dq, dqd, dg, db
+    return dvals, dkeys, dq, dqd, dg, db, dsk
 
 
 # ---------------------------------------------------------------------------

@@ -211,13 +211,13 @@ def _empty(device):
 
 @torch.library.custom_op("attnres_hip::read", mutates_args=())
 def _read_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], query_dyn: Optional[Tensor],
-             gate: Optional[Tensor], bias: Optional[Tensor], heads: int, logit_scale: float, key_norm: bool,
-             normalize_output: bool, mode: int, gate_act: int, gate_per_token: bool,
-             save_weights: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+             gate: Optional[Tensor], bias: Optional[Tensor], static_keys: Optional[Tensor], heads: int,
+             logit_scale: float, key_norm: bool, normalize_output: bool, mode: int, gate_act: int,
+             gate_per_token: bool, save_weights: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     v0 = values[0]
     B, T, D = v0.shape
     desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
-                     mode, gate_act, gate_per_token)
+                     mode, gate_act, gate_per_token, static_keys=static_keys)
     with torch.cuda.device(v0.device):
         out, w, inv, pre = _hip.forward(desc, v0.device, v0.dtype, save_weights and mode == _hip.MODE_SOFTMAX,
                                         normalize_output, save_weights)
@@ -225,8 +225,8 @@ def _read_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], 
 
 
 @_read_op.register_fake
-def _read_fake(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode,
-               gate_act, gate_per_token, save_weights):
+def _read_fake(values, keys, query, query_dyn, gate, bias, static_keys, heads, logit_scale, key_norm,
+               normalize_output, mode, gate_act, gate_per_token, save_weights):
     v0 = values[0]
     B, T, D = v0.shape
     n_tok = B * T
@@ -240,51 +240,54 @@ def _read_fake(values, keys, query, query_dyn, gate, bias, heads, logit_scale, k
 
 @torch.library.custom_op("attnres_hip::read_backward", mutates_args=())
 def _read_backward_op(values: list[Tensor], keys: list[Tensor], query: Optional[Tensor], query_dyn: Optional[Tensor],
-                      gate: Optional[Tensor], bias: Optional[Tensor], grad_out: Tensor, prenorm: Tensor,
-                      inv_rms: Tensor, weights: Tensor, heads: int, logit_scale: float, key_norm: bool,
-                      normalize_output: bool, mode: int, gate_act: int,
-                      gate_per_token: bool) -> tuple[list[Tensor], list[Tensor], Tensor, Tensor, Tensor, Tensor]:
+                      gate: Optional[Tensor], bias: Optional[Tensor], static_keys: Optional[Tensor],
+                      grad_out: Tensor, prenorm: Tensor, inv_rms: Tensor, weights: Tensor, heads: int,
+                      logit_scale: float, key_norm: bool, normalize_output: bool, mode: int, gate_act: int,
+                      gate_per_token: bool) -> tuple[list[Tensor], list[Tensor], Tensor, Tensor, Tensor, Tensor,
+                                                     Tensor]:
     v0 = values[0]
     B, T, D = v0.shape
     dev = v0.device
     desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
-                     mode, gate_act, gate_per_token)
+                     mode, gate_act, gate_per_token, static_keys=static_keys)
     lr = len(keys) > 0
     with torch.cuda.device(dev):
-        dvals, dkeys, dq, dqd, dg, db = _hip.backward(
+        dvals, dkeys, dq, dqd, dg, db, dsk = _hip.backward(
             desc, dev, v0.dtype, grad_out.contiguous(), prenorm, inv_rms, weights,
             want_dquery=query is not None and mode == _hip.MODE_SOFTMAX,
             want_dgate=gate is not None, want_dbias=bias is not None,
             query_shape=tuple(query.shape) if query is not None else (0,),
             gate_shape=tuple(gate.shape) if gate is not None else (0,), lr=lr,
-            has_query_dyn=query_dyn is not None)
+            has_query_dyn=query_dyn is not None, want_dstatic=static_keys is not None)
     dvals = [t.view(B, T, D) for t in dvals]
     dkeys = [t.view(B, T, keys[0].size(-1)) for t in dkeys]
     # absent gradients are distinct empty tensors (custom-op outputs may not alias)
     return (dvals, dkeys, dq if dq is not None else _empty(dev),
             dqd.view(query_dyn.shape) if dqd is not None else _empty(dev),
-            dg if dg is not None else _empty(dev), db if db is not None else _empty(dev))
+            dg if dg is not None else _empty(dev), db if db is not None else _empty(dev),
+            dsk.view(static_keys.shape) if dsk is not None else _empty(dev))
 
 
 @_read_backward_op.register_fake
-def _read_backward_fake(values, keys, query, query_dyn, gate, bias, grad_out, prenorm, inv_rms, weights, heads,
-                        logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token):
+def _read_backward_fake(values, keys, query, query_dyn, gate, bias, static_keys, grad_out, prenorm, inv_rms, weights,
+                        heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token):
     e = lambda: values[0].new_empty((0,))  # noqa: E731
     return ([v.new_empty(v.shape) for v in values], [k.new_empty(k.shape) for k in keys],
             query.new_empty(query.shape) if query is not None else e(),
             query_dyn.new_empty(query_dyn.shape) if query_dyn is not None else e(),
             gate.new_empty(gate.shape) if gate is not None else e(),
-            bias.new_empty(bias.shape) if bias is not None else e())
+            bias.new_empty(bias.shape) if bias is not None else e(),
+            static_keys.new_empty(static_keys.shape) if static_keys is not None else e())
 
 
 def _read_setup_context(ctx, inputs, output):
-    (values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode, gate_act,
-     gate_per_token, save_weights) = inputs
+    (values, keys, query, query_dyn, gate, bias, static_keys, heads, logit_scale, key_norm, normalize_output, mode,
+     gate_act, gate_per_token, save_weights) = inputs
     out, w, inv, pre = output
     ctx.n_values = len(values)
     ctx.n_keys = len(keys)
-    ctx.has = (query is not None, query_dyn is not None, gate is not None, bias is not None)
-    opt = [t for t in (query, query_dyn, gate, bias) if t is not None]
+    ctx.has = (query is not None, query_dyn is not None, gate is not None, bias is not None, static_keys is not None)
+    opt = [t for t in (query, query_dyn, gate, bias, static_keys) if t is not None]
     ctx.save_for_backward(*values, *keys, *opt, pre, w, inv)
     ctx.flags = (heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token)
 
@@ -297,15 +300,16 @@ def _read_backward(ctx, grad_out, grad_w, grad_inv, grad_pre):
     opt = []
     for present in ctx.has:
         opt.append(rest.pop(0) if present else None)
-    query, query_dyn, gate, bias = opt
+    query, query_dyn, gate, bias, static_keys = opt
     pre, w, inv = rest
     heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token = ctx.flags
-    dvals, dkeys, dq, dqd, dg, db = _read_backward_op(values, keys, query, query_dyn, gate, bias, grad_out, pre,
-                                                      inv, w, heads, logit_scale, key_norm, normalize_output, mode,
-                                                      gate_act, gate_per_token)
+    dvals, dkeys, dq, dqd, dg, db, dsk = _read_backward_op(values, keys, query, query_dyn, gate, bias, static_keys,
+                                                           grad_out, pre, inv, w, heads, logit_scale, key_norm,
+                                                           normalize_output, mode, gate_act, gate_per_token)
     return (dvals, dkeys,
             dq if query is not None else None, dqd if query_dyn is not None else None,
             dg if gate is not None else None, db if bias is not None else None,
+            dsk if static_keys is not None else None,
             None, None, None, None, None, None, None, None)
 
 
@@ -346,11 +350,11 @@ class _ReadFn(torch.autograd.Function):
         n_v, n_k, has, heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token, save = meta
         values = flat[:n_v]
         keys = flat[n_v:n_v + n_k]
-        query, query_dyn, gate, bias = _unflatten_opt(has, flat[n_v + n_k:])
+        query, query_dyn, gate, bias, static_keys = _unflatten_opt(has, flat[n_v + n_k:])
         v0 = values[0]
         B, T, D = v0.shape
         desc = _hip.Desc(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output,
-                         mode, gate_act, gate_per_token)
+                         mode, gate_act, gate_per_token, static_keys=static_keys)
         with _device_ctx(v0.device):
             out, w, inv, pre = _hip.forward(desc, v0.device, v0.dtype, save and mode == _hip.MODE_SOFTMAX,
                                             normalize_output, save)
@@ -366,21 +370,23 @@ class _ReadFn(torch.autograd.Function):
     def backward(ctx, grad_out):
         n_v, n_k, has, heads, logit_scale, key_norm, normalize_output, mode, gate_act, gate_per_token, _ = ctx.meta
         saved = ctx.saved_tensors  # (checks that no input was modified in place)
-        query, query_dyn, gate, bias = _unflatten_opt(has, saved[n_v + n_k:-3])
+        query, query_dyn, gate, bias, static_keys = _unflatten_opt(has, saved[n_v + n_k:-3])
         pre, w, inv = saved[-3:]
         B, T, D = ctx.shape
         dev = saved[0].device
         want = ctx.needs_input_grad
         with _device_ctx(dev):
-            dvals, dkeys, dq, dqd, dg, db = _hip.backward(
+            dvals, dkeys, dq, dqd, dg, db, dsk = _hip.backward(
                 ctx.desc, dev, saved[0].dtype, grad_out.contiguous(), pre, inv, w,
                 want_dquery=query is not None and mode == _hip.MODE_SOFTMAX,
                 want_dgate=gate is not None, want_dbias=bias is not None,
                 query_shape=tuple(query.shape) if query is not None else (0,),
                 gate_shape=tuple(gate.shape) if gate is not None else (0,), lr=n_k > 0,
-                has_query_dyn=query_dyn is not None, batched=True, lead=(B, T))
+                has_query_dyn=query_dyn is not None, batched=True, lead=(B, T),
+                want_dstatic=static_keys is not None)
         grads = [None, *dvals, *dkeys]
-        for present, g in zip(has, (dq, dqd.view(query_dyn.shape) if dqd is not None else None, dg, db)):
+        for present, g in zip(has, (dq, dqd.view(query_dyn.shape) if dqd is not None else None, dg, db,
+                                    dsk.view(static_keys.shape) if dsk is not None else None)):
             if present:
                 grads.append(g)
         # inputs that do not need a gradient get None (the kernels write all of them in one pass)
@@ -388,12 +394,12 @@ class _ReadFn(torch.autograd.Function):
 
 
 def _run(values, keys, query, query_dyn, gate, bias, heads, logit_scale, key_norm, normalize_output, mode,
-         gate_act=_hip.GATE_NONE, gate_per_token=False):
-    opt = (query, query_dyn, gate, bias)
+         gate_act=_hip.GATE_NONE, gate_per_token=False, static_keys=None):
+    opt = (query, query_dyn, gate, bias, static_keys)
     save = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (*values, *keys, *opt))
     if _compiling():
-        out, _, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, int(heads), float(logit_scale),
-                                bool(key_norm), bool(normalize_output), int(mode), int(gate_act),
+        out, _, _, _ = _read_op(values, keys, query, query_dyn, gate, bias, static_keys, int(heads),
+                                float(logit_scale), bool(key_norm), bool(normalize_output), int(mode), int(gate_act),
                                 bool(gate_per_token), bool(save))
         return out
     meta = (len(values), len(keys), tuple(t is not None for t in opt), int(heads), float(logit_scale),
@@ -475,21 +481,37 @@ def _lr_common(values, keys, num_heads, what):
     return _promote(vs), _promote(ks), H, D, R, ks[0].dtype
 
 
+def _static_keys(static_keys, n: int, R: int, dtype, what: str) -> Tensor:
+    """A static key per source as one [N, R] tensor in the key dtype: the
+    model's ``key + static_key.to(key.dtype)`` (model.py:2046-2049, :286-288)."""
+    sk = torch.stack(list(static_keys)) if isinstance(static_keys, (list, tuple)) else static_keys
+    if sk.numel() != n * R:
+        raise RuntimeError(f"{what}: static_keys must be [{n}, {R}] (one rank-{R} key per source), "
+                           f"got {tuple(sk.shape)}")
+    return sk.to(dtype).reshape(n, R).contiguous()
+
+
 def lrid_attention_residual_read(values, keys, query: Tensor, num_heads: int, logit_scale: float, key_norm: bool,
                                  force_triton: bool = False, normalize_output: bool = False, source_counts=None,
-                                 source_logit_biases=None) -> Tensor:
+                                 source_logit_biases=None, static_keys=None) -> Tensor:
     """LR AttnRes read (reference: attnres_ops.py:4852-5003).
 
     values: N x [B,T,D] (list or stacked); keys: N x [B,T,R]; query [H, R/H]
     (static, per read site) or [B,T,H,R/H] (input dependent).  The query is
     cast to the key dtype first, as in the reference.  The optional output
-    rms-norm is fused for any number of heads.
+    rms-norm is fused for any number of heads.  Extra (not in the reference's
+    op): ``static_keys`` [N, R] (or N tensors [R]) adds source s's static key to
+    every key of source s inside the kernel, as the model adds it eagerly
+    before the read (model.py:2046-2049); its gradient is the token sum of the
+    key gradient.
     """
     vs, ks, H, D, R, k0_dtype = _lr_common(values, keys, num_heads, "lrid_attention_residual_read")
     query = query.to(k0_dtype)
     if len(vs) == 1:
         return _norm(vs[0]) if normalize_output else vs[0]
-    dev = _check_gpu(vs + ks + [query], "lrid_attention_residual_read")
+    sk = None if static_keys is None else _static_keys(static_keys, len(vs), R, ks[0].dtype,
+                                                        "lrid_attention_residual_read")
+    dev = _check_gpu(vs + ks + [query] + ([sk] if sk is not None else []), "lrid_attention_residual_read")
     # Keys of another dtype than the values stay in their dtype: the eager read
     # norms them in fp32 and rounds them to the value dtype (attnres_ops.py:4179-4180),
     # so the logits are a value-dtype contraction with key_norm and a key-dtype
@@ -504,18 +526,19 @@ def lrid_attention_residual_read(values, keys, query: Tensor, num_heads: int, lo
             raise RuntimeError(f"lrid_attention_residual_read: per-token query must be {(B, T, H, R // H)}, "
                                f"got {tuple(query.shape)}")
         qd = _hip.as_rows(query.reshape(B, T, R))
-        return _run(vs, ks, None, qd, None, bias, H, logit_scale, key_norm, normalize_output, _hip.MODE_SOFTMAX)
+        return _run(vs, ks, None, qd, None, bias, H, logit_scale, key_norm, normalize_output, _hip.MODE_SOFTMAX,
+                    static_keys=sk)
     if query.numel() != R:
         raise RuntimeError(f"lrid_attention_residual_read: static query must have {R} elements "
                            f"([{H}, {R // H}]), got {tuple(query.shape)}")
     return _run(vs, ks, query.reshape(H, R // H).contiguous(), None, None, bias, H, logit_scale, key_norm,
-                normalize_output, _hip.MODE_SOFTMAX)
+                normalize_output, _hip.MODE_SOFTMAX, static_keys=sk)
 
 
 def lrid_attention_residual_read_gated(values, keys, static_query: Optional[Tensor], dynamic_query: Tensor,
                                        gate: Optional[Tensor], num_heads: int, logit_scale: float, key_norm: bool,
                                        gate_activation: str = "sigmoid", normalize_output: bool = False,
-                                       source_counts=None, source_logit_biases=None) -> Tensor:
+                                       source_counts=None, source_logit_biases=None, static_keys=None) -> Tensor:
     """LR read with the query composed inside the kernel: ``q = q_static + act(gate) * q_dyn``.
 
     ``gate_activation="linear"`` with a per-site ``gate[H]`` is the model's
@@ -524,7 +547,8 @@ def lrid_attention_residual_read_gated(values, keys, static_query: Optional[Tens
     [B,T,H,R/H]; ``static_query`` is [H,R/H] or None.  Gradients flow to all
     three (the per-site gate and static query are reduced over tokens
     deterministically).  Not present in the reference, which composes the query
-    eagerly and then reads with an input-dependent query.
+    eagerly and then reads with an input-dependent query.  ``static_keys`` as
+    in ``lrid_attention_residual_read`` (config 4's [N, 128] static source key).
     """
     vs, ks, H, D, R, _ = _lr_common(values, keys, num_heads, "lrid_attention_residual_read_gated")
     dtype = vs[0].dtype
@@ -556,10 +580,14 @@ def lrid_attention_residual_read_gated(values, keys, static_query: Optional[Tens
     if len(vs) == 1:
         return _norm(vs[0]) if normalize_output else vs[0]
     bias = _source_logit_bias(source_counts, source_logit_biases, len(vs), dev)
+    sk = None if static_keys is None else _static_keys(static_keys, len(vs), R, dtype,
+                                                        "lrid_attention_residual_read_gated")
+    if sk is not None:
+        _check_gpu([sk], "lrid_attention_residual_read_gated")
     vs = [_hip.as_rows(t) for t in vs]
     ks = [_hip.as_rows(t) for t in ks]
     return _run(vs, ks, qs, qd, g, bias, H, logit_scale, key_norm, normalize_output, _hip.MODE_SOFTMAX,
-                act if g is not None else _hip.GATE_NONE, per_token)
+                act if g is not None else _hip.GATE_NONE, per_token, static_keys=sk)
 
 
 def lrid_attention_residual_read_torch(values, keys, query: Tensor, num_heads: int, logit_scale: float,

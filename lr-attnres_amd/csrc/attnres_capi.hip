@@ -111,6 +111,8 @@ int check_desc(const attnres_read_desc* d) {
       return fail(ATTNRES_EINVAL, "value_row_stride[%d]=%lld must be in [dim, 2^31)", s,
                   (long long)d->value_row_stride[s]);
   }
+  if (d->static_keys && (d->mode != ATTNRES_MODE_SOFTMAX || d->rank == 0))
+    return fail(ATTNRES_EINVAL, "static_keys apply to LR reads only");
   if (d->mode == ATTNRES_MODE_AVERAGE) return ATTNRES_OK;
   if (d->heads < 1) return fail(ATTNRES_EINVAL, "heads=%d < 1", d->heads);
   if (d->rank == 0) {
@@ -196,6 +198,7 @@ int make_plan(const attnres_read_desc* d, const void* const* extra, int n_extra,
     bool kv = rh % EV == 0;
     for (int s = 0; kv && s < d->n_src; ++s) kv = aligned16(d->keys[s]) && ((d->key_row_stride[s] * es) % 16 == 0);
     if (kv && d->query) kv = aligned16(d->query);
+    if (kv && d->static_keys) kv = aligned16(d->static_keys) && ((d->rank * es) % 16 == 0);
     if (kv && d->query_dyn) kv = aligned16(d->query_dyn) && ((d->query_dyn_row_stride * es) % 16 == 0);
     pl->key_vec = kv ? 1 : 0;
   }
@@ -237,6 +240,23 @@ void fill_params(const attnres_read_desc* d, const Plan& pl, ReadParams* p) {
   p->eps = d->norm_eps;
   p->kdt = pl.lr ? d->key_dtype : d->dtype;
   p->ldt = logit_dtype(d);
+  p->skey = pl.lr ? d->static_keys : nullptr;
+}
+
+// The static keys' gradient: per-source token sums of dkeys, partial sums
+// per token chunk in the workspace after the cross-token partial rows.
+// LDS bytes of the static keys in the fast LR kernels ([n_src, rank] in the dtype)
+size_t static_keys_lds(const attnres_read_desc* d) {
+  return d->static_keys ? (size_t)d->n_src * d->rank * elem_size(d->dtype) : 0;
+}
+
+int colsum_chunks(int64_t n_tok) {
+  const int64_t c = (n_tok + kColsumTokens - 1) / kColsumTokens;
+  return (int)(c < 1 ? 1 : c < kColsumMaxChunks ? c : kColsumMaxChunks);
+}
+size_t colsum_bytes(const attnres_read_desc* d) {
+  if (!d->static_keys || d->rank <= 0 || d->n_tok == 0) return 0;
+  return (size_t)d->n_src * colsum_chunks(d->n_tok) * d->rank * sizeof(float);
 }
 
 struct PartLayout {
@@ -382,12 +402,13 @@ bool base_fast_plan(const attnres_read_desc* d, const Plan& pl, BaseFastPlan* f)
   return true;
 }
 
-// Optional code the fast LR kernels must carry for a read: 0 (static query,
-// no output norm), 1 (per-token query / gate) or 3 (everything); these are
-// the instantiated sets (the kFeat* bits of attnres_lr_fast.h).
+// Optional code the fast LR kernels must carry for a read, rounded up to an
+// instantiated set: 0 (static query, no output norm), kFeatDyn (per-token query
+// / gate), kFeatDyn | kFeatStatic (and static source keys) or kFeatAll.
 int lr_fast_features(const attnres_read_desc* d) {
-  if (d->normalize_output) return 3;
-  return (d->query_dyn || d->gate) ? 1 : 0;
+  if (d->normalize_output) return kFeatAll;
+  if (d->static_keys) return kFeatDyn | kFeatStatic;
+  return (d->query_dyn || d->gate) ? kFeatDyn : 0;
 }
 
 // token teams per LR-backward workgroup: four independent one-wave teams when a
@@ -457,11 +478,21 @@ extern "C" int attnres_test_phase2_block_layout(int on) {
   return ATTNRES_OK;
 }
 
-extern "C" size_t attnres_read_backward_workspace_size(const attnres_read_desc* d) {
-  if (check_desc(d) != ATTNRES_OK) return 0;
+// bytes of the cross-token partial rows (the largest layout), padded so that
+// the static keys' column sums start on a 256-byte boundary after them
+size_t partial_rows_bytes(const attnres_read_desc* d) {
   const PartLayout L = part_layout(d, true, true, true);
   if (L.n_part == 0 || d->n_tok == 0) return 0;
-  return (size_t)bwd_groups(d->n_tok) * L.n_part * sizeof(float);
+  return ((size_t)bwd_groups(d->n_tok) * L.n_part * sizeof(float) + 255) / 256 * 256;
+}
+
+extern "C" size_t attnres_read_backward_workspace_size(const attnres_read_desc* d) {
+  if (check_desc(d) != ATTNRES_OK) return 0;
+  const size_t cs = colsum_bytes(d);
+  const PartLayout L = part_layout(d, true, true, true);
+  if (d->n_tok == 0) return 0;
+  if (cs == 0) return L.n_part == 0 ? 0 : (size_t)bwd_groups(d->n_tok) * L.n_part * sizeof(float);
+  return partial_rows_bytes(d) + cs;
 }
 
 extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void* out_prenorm, float* weights,
@@ -510,7 +541,8 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       L.teams = f.rhc;
       L.feat = lr_fast_features(d);
       L.grid = (int)((f.n_items * (int64_t)p.streams + 3) / 4);
-      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float);
+      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float) + static_keys_lds(d);
+      if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR forward needs %zu bytes of LDS", L.lds);
       err = launch_lr_fast_forward(d->dtype, p, L, st);
     } else {
       L.lds = (2 * (size_t)d->heads * d->n_src + 32) * sizeof(float);
@@ -557,6 +589,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       for (int s = 0; s < d->n_src; ++s)
         if (!g->dkeys[s]) return fail(ATTNRES_EINVAL, "dkeys[%d] is NULL", s);
       if (d->query_dyn && !g->dquery_dyn) return fail(ATTNRES_EINVAL, "per-token query needs dquery_dyn");
+      if (g->dstatic_keys && !d->static_keys) return fail(ATTNRES_EINVAL, "dstatic_keys without static_keys");
       if (d->gate && d->gate_per_token && !g->dgate) return fail(ATTNRES_EINVAL, "per-token gate needs dgate");
     }
   }
@@ -568,6 +601,8 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       zero_async(g->dquery, (size_t)(lr ? d->rank : d->dim) * elem_size(logit_dtype(d)), st);
     if (softmax && g->dgate && d->gate && !d->gate_per_token) zero_async(g->dgate, (size_t)d->heads * es, st);
     if (softmax && g->dbias && d->logit_bias) zero_async(g->dbias, (size_t)d->n_src * 4, st);
+    if (lr && g->dstatic_keys && d->static_keys)
+      zero_async(g->dstatic_keys, (size_t)d->n_src * d->rank * elem_size(d->key_dtype), st);
     return ATTNRES_OK;
   }
   Plan pl;
@@ -637,7 +672,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       // instantiations with all optional code (fewer waves per SIMD) stream
       // best with 2048 workgroups, the leaner ones with twice as many
       // (measured at C3 and C4)
-      const int64_t cap = feat != 3 ? groups : (groups < kFullBwdGroups ? groups : kFullBwdGroups);
+      const int64_t cap = feat != kFeatAll ? groups : (groups < kFullBwdGroups ? groups : kFullBwdGroups);
       streams = 4 * cap / f.n_items;
       if (streams > d->n_tok) streams = d->n_tok;
     }
@@ -654,8 +689,10 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
       L.feat = feat;
       L.grid = (int)((f.n_items * streams + 3) / 4);
       L.lds = lr_fast_table_bytes() +
-              ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads + 1)) + 4 * (size_t)PL.n_part) *
-                  sizeof(float);
+              ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads + 1)) +
+               (4 * (size_t)PL.n_part + 3) / 4 * 4) *
+                  sizeof(float) +
+              static_keys_lds(d);
       if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS", L.lds);
       // slot-major partials (R + few slots: one reduction workgroup per slot
       // beats 16-slot tiles here, measured at C3 and C4)
@@ -718,6 +755,24 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     rp.dextra = nullptr;
     err = launch_reduce_partials(logit_dtype(d), rp, st);  // the query gradient is in the logit dtype
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
+  }
+  if (lr && g->dstatic_keys) {
+    const size_t need = partial_rows_bytes(d) + colsum_bytes(d);
+    if (!g->workspace || g->workspace_bytes < need)
+      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
+                  g->workspace ? g->workspace_bytes : (size_t)0);
+    ColsumParams cp;
+    memset(&cp, 0, sizeof(cp));
+    for (int s = 0; s < d->n_src; ++s) cp.dk[s] = g->dkeys[s];
+    cp.partials = (float*)((char*)g->workspace + partial_rows_bytes(d));
+    cp.out = g->dstatic_keys;
+    cp.n_tok = d->n_tok;
+    cp.n_src = d->n_src;
+    cp.R = d->rank;
+    cp.chunks = colsum_chunks(d->n_tok);
+    cp.kdt = d->key_dtype;
+    err = launch_key_colsum(cp, st);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "static-key gradient launch failed: %s", hipGetErrorString(err));
   }
   return ATTNRES_OK;
 }

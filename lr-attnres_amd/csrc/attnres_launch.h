@@ -26,6 +26,7 @@ hipError_t launch_base_backward(int dtype, const ReadBwdParams& p, const Launch&
 hipError_t launch_average_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_average_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_reduce_partials(int dtype, const ReduceParams& p, hipStream_t st);
+hipError_t launch_key_colsum(const ColsumParams& p, hipStream_t st);
 // LR fast path (head-aligned one-wave work items): L.wpt = columns per item,
 // L.nmax = source slots (8/16/32), L.teams = key chunks per head slot (2/8)
 hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);

@@ -69,14 +69,24 @@ __device__ __forceinline__ const char* key_slice(const ReadParams& p, int s, int
   return (const char*)p.key[s] + (tok * (int64_t)p.kstride[s] + (int64_t)h * p.rh) * dtype_bytes(p.kdt);
 }
 
+// Key element j of (source s, head h) as the read scores it: the key plus the
+// source's static key, rounded to the key dtype as the eager add is, when there
+// is one.
+__device__ __forceinline__ float key_at(const ReadParams& p, const char* kp, int s, int h, int j) {
+  const float k = load_any(kp, j, p.kdt);
+  if (!p.skey) return k;
+  return round_any(k + load_any(p.skey, (int64_t)s * p.R + h * p.rh + j, p.kdt), p.kdt);
+}
+
 // Sum of squares of one key slice (rh elements): 16-byte loads when the keys
-// have the value dtype and are aligned for them, else one element at a time.
+// have the value dtype and are aligned for them (and no static key is added),
+// else one element at a time.
 template <class DT>
-__device__ __forceinline__ float key_sumsq(const ReadParams& p, const char* kp) {
+__device__ __forceinline__ float key_sumsq(const ReadParams& p, const char* kp, int s, int h) {
   constexpr int KV = 16 / (int)sizeof(typename DT::S);
   const int rh = p.rh;
   float ss = 0.f;
-  if (p.key_vec) {
+  if (p.key_vec && !p.skey) {
     for (int j = 0; j < rh; j += KV) {
       float k[KV];
       load_vec<DT, KV>((const typename DT::S*)kp + j, k);
@@ -85,7 +95,7 @@ __device__ __forceinline__ float key_sumsq(const ReadParams& p, const char* kp) 
     }
   } else {
     for (int j = 0; j < rh; ++j) {
-      const float k = load_any(kp, j, p.kdt);
+      const float k = key_at(p, kp, s, h, j);
       ss += k * k;
     }
   }
@@ -101,9 +111,9 @@ __device__ float lr_logit(const ReadParams& p, int64_t tok, int h, int s) {
   const char* kp = key_slice(p, s, tok, h);
   const QueryView<DT> q = query_view<DT>(p, tok, h);
   float inv = 1.f;
-  if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(p, kp) / (float)rh + p.eps);
+  if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(p, kp, s, h) / (float)rh + p.eps);
   float dot = 0.f;
-  if (p.key_vec) {
+  if (p.key_vec && !p.skey) {
     for (int j = 0; j < rh; j += KV) {
       float k[KV];
       load_vec<DT, KV>((const S*)kp + j, k);
@@ -115,7 +125,7 @@ __device__ float lr_logit(const ReadParams& p, int64_t tok, int h, int s) {
     }
   } else {
     for (int j = 0; j < rh; ++j) {
-      float k = load_any(kp, j, p.kdt);
+      const float k = key_at(p, kp, s, h, j);
       const float kh = p.key_norm ? round_any(k * inv, ldt) : k;
       dot += kh * q.at(j);
     }
@@ -419,10 +429,10 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
       const char* kp = key_slice(p, s, tok, h);
       const QueryView<DT> q = query_view<DT>(p, tok, h);
       float inv = 1.f;
-      if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(p, kp) / (float)rh + p.eps);
+      if (p.key_norm) inv = 1.0f / sqrtf(key_sumsq<DT>(p, kp, s, h) / (float)rh + p.eps);
       float m = 0.f;
       for (int j = 0; j < rh; ++j) {
-        const float k = load_any(kp, j, p.kdt);
+        const float k = key_at(p, kp, s, h, j);
         const float kh = p.key_norm ? round_any(k * inv, ldt) : k;
         s_kh[s * R + h * rh + j] = kh;
         if (p.key_norm) m += round_any(ge * q.at(j), ldt) * (k * inv);
@@ -435,7 +445,7 @@ __global__ void __launch_bounds__(1024) lr_bwd_kernel(const ReadBwdParams bp) {
         const float dkh = round_any(ge * q.at(j), ldt);
         float dk = dkh;
         if (p.key_norm) {
-          const float yk = load_any(kp, j, p.kdt) * inv;
+          const float yk = key_at(p, kp, s, h, j) * inv;
           dk = inv * (dkh - yk * mr);
         }
         store_any(dkp, j, p.kdt, dk);
@@ -518,6 +528,63 @@ static hipError_t lr_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t
   const int threads = L.wpt * kWave * L.teams;
   if (L.vec) return launch_lr_bwd_t<DT, 16 / sizeof(typename DT::S), 2>(p, threads, L.grid, L.lds, st);
   return launch_lr_bwd_t<DT, 1, 4>(p, threads, L.grid, L.lds, st);
+}
+
+// ---------------------------------------------------------------- static-key gradient
+// d static_s = rnd(sum over tokens of dk_s): the reference's `key + static`
+// expands the static key over (B, T), whose backward sums the key-dtype
+// gradient rows with fp32 accumulation and rounds once.  Pass 1: workgroup
+// (chunk, source) sums its chunk of tokens for every column -- 256 / R token
+// phases of R threads for R <= 256 (coalesced row reads), phases folded in a
+// fixed order; pass 2: thread (source, column) adds the chunks in order.
+__global__ void __launch_bounds__(256) key_colsum_kernel(const ColsumParams p) {
+  __shared__ float s_part[256];
+  const int c = blockIdx.x, s = blockIdx.y, R = p.R;
+  const int64_t tpc = (p.n_tok + p.chunks - 1) / p.chunks;
+  const int64_t t0 = (int64_t)c * tpc;
+  const int64_t t1 = t0 + tpc < p.n_tok ? t0 + tpc : p.n_tok;
+  const int P = R <= 256 ? 256 / R : 1;  // token phases
+  const int tid = threadIdx.x;
+  const void* dk = p.dk[s];
+  float* out = p.partials + ((int64_t)s * p.chunks + c) * R;
+  if (R <= 256) {
+    const int ph = tid / R, r = tid - (tid / R) * R;
+    float a = 0.f;
+    if (ph < P)
+      for (int64_t t = t0 + ph; t < t1; t += P) a += load_any(dk, t * R + r, p.kdt);
+    s_part[tid] = a;
+    __syncthreads();
+    if (tid < R) {
+      float sum = 0.f;
+      for (int k = 0; k < P; ++k) sum += s_part[k * R + tid];
+      out[tid] = sum;
+    }
+  } else {
+    for (int r = tid; r < R; r += 256) {
+      float a = 0.f;
+      for (int64_t t = t0; t < t1; ++t) a += load_any(dk, t * R + r, p.kdt);
+      out[r] = a;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) key_colsum_finish_kernel(const ColsumParams p) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)p.n_src * p.R) return;
+  const int s = (int)(i / p.R), r = (int)(i - (int64_t)s * p.R);
+  const float* row = p.partials + (int64_t)s * p.chunks * p.R + r;
+  float a = 0.f;
+  for (int c = 0; c < p.chunks; ++c) a += row[(int64_t)c * p.R];
+  store_any(p.out, i, p.kdt, a);
+}
+
+hipError_t launch_key_colsum(const ColsumParams& p, hipStream_t st) {
+  hipLaunchKernelGGL(key_colsum_kernel, dim3(p.chunks, p.n_src), dim3(256), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t n = (int64_t)p.n_src * p.R;
+  hipLaunchKernelGGL(key_colsum_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
+  return hipGetLastError();
 }
 
 hipError_t launch_lr_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st) {

@@ -38,11 +38,12 @@ namespace attnres {
 constexpr int kFastWaves = 4;  // waves per workgroup (independent token streams)
 
 // FEAT selects at compile time which optional code an instantiation carries:
-// kFeatDyn = per-token query and gate, kFeatNorm = output norm.  The host picks
-// the smallest set a read needs (0, kFeatDyn, or all): without them the
-// static-query backward fits 4 waves per SIMD instead of 3, and the gated one
-// 3 instead of 2.
-constexpr int kFeatDyn = 1, kFeatNorm = 2, kFeatAll = 3;
+// kFeatDyn = per-token query and gate, kFeatNorm = output norm, kFeatStatic =
+// a static key per source added to every key.  The host picks the smallest
+// instantiated set a read needs (0, kFeatDyn, kFeatDyn | kFeatStatic, or all):
+// without them the static-query backward fits 4 waves per SIMD instead of 3,
+// and the gated one 3 instead of 2.
+// (the kFeat* constants are in attnres_params.h, shared with the host)
 
 // per-source tables in LDS
 struct SrcTab {
@@ -60,6 +61,45 @@ struct KeySlice {
   static constexpr int KV = 16 / (int)sizeof(typename DT::S);
   Raw<DT, KV> r[RHC];
 };
+
+// Static source keys (kFeatStatic): the [n_src, R] table is copied to LDS once
+// per workgroup (16-byte chunks; the host checks R * elem is a multiple of 16),
+// and every token's key slice gets its source's slice added from there,
+// rounded to the dtype as the eager `key + static` is -- token-invariant data
+// kept out of the loop-carried registers.
+template <class DT>
+__device__ __forceinline__ void static_keys_to_lds(const ReadParams& p, typename DT::S* dst) {
+  using S = typename DT::S;
+  const int n16 = p.n_src * p.R * (int)sizeof(S) / 16;
+  const u32x4* src = (const u32x4*)p.skey;
+  for (int i = threadIdx.x; i < n16; i += blockDim.x) ((u32x4*)dst)[i] = src[i];
+}
+
+template <class DT, int RHC>
+__device__ __forceinline__ void add_static_key(const typename DT::S* sk, int kch, KeySlice<DT, RHC>& kr) {
+#pragma unroll
+  for (int j = 0; j < RHC; ++j) {
+    if (j < kch) {
+      const u32x4 w = *(const u32x4*)(sk + j * KeySlice<DT, RHC>::KV);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      // word by word (two 16-bit elements, or one fp32), so few values are live at once
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(typename DT::S) == 2) {
+          Raw<DT, 2> a, b;
+          a.w[0] = kr.r[j].w[i];
+          b.w[0] = ww[i];
+          float x[2], y[2];
+          unpack<DT, 2>(a, x);
+          unpack<DT, 2>(b, y);
+          kr.r[j].w[i] = pack2<DT>(x[0] + y[0], x[1] + y[1]);  // packing rounds to the dtype
+        } else {
+          kr.r[j].w[i] = __float_as_uint(__uint_as_float(kr.r[j].w[i]) + __uint_as_float(ww[i]));
+        }
+      }
+    }
+  }
+}
 
 // byte address of a row: base + tok * stride, one 32 x 32 -> 64-bit
 // multiply-add (tok and the byte stride fit 32 bits on this path)
@@ -180,8 +220,10 @@ __device__ __forceinline__ float key_query_dot(const KeySlice<DT, RHC>& kr, cons
 }
 
 // ============================================================== forward
+// (the static-key instantiations with 20+ slots would cross 168 VGPRs by one
+// register: they ask for 3 waves per SIMD, which the compiler meets without spills)
 template <class DT, int VB, int CB, int NB, int RHC, int FEAT>
-__global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
+__global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1) lr_fwd_fast_kernel(const ReadParams p) {
   using S = typename DT::S;
   constexpr int E = VB / (int)sizeof(S);        // value elements per lane vector
   constexpr int KV = 16 / (int)sizeof(S);       // key elements per 16-byte chunk
@@ -209,6 +251,10 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
   }
   if (p.q_static)
     for (int i = threadIdx.x; i < R; i += blockDim.x) s_q[i] = DT::load1((const S*)p.q_static + i);
+  // static keys after the per-wave weight words
+  S* s_sk = (S*)(s_q + R + nwaves * 64);
+  const bool skey = (FEAT & kFeatStatic) && p.skey != nullptr;
+  if (skey) static_keys_to_lds<DT>(p, s_sk);
   __syncthreads();
 
   const int wv = blockIdx.x * nwaves + wslot;
@@ -279,6 +325,7 @@ __global__ void __launch_bounds__(256) lr_fwd_fast_kernel(const ReadParams p) {
     // ---- logits of this wave's (head, source) pairs
     float logit = -INFINITY;
     if (has_pair) {
+      if (skey) add_static_key<DT, RHC>(s_sk + ps * R + ph * rh, kch, kr);
       const float gf = (dyn && p.gate) ? gate_value(DT::load1(&graw), p.gate_act) : 1.f;
       const float inv = p.key_norm ? key_inv_rms<DT, RHC>(kr, kch, rh, p.eps) : 1.f;
       QSlice<DT, RHC> q;
@@ -408,6 +455,10 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   }
   if (p.q_static)
     for (int i = threadIdx.x; i < R; i += blockDim.x) s_q[i] = DT::load1((const S*)p.q_static + i);
+  // static keys after the fold rows, on a 16-byte boundary
+  S* s_sk = (S*)(s_fold + (nwaves * bp.n_part + 3) / 4 * 4);
+  const bool skey = (FEAT & kFeatStatic) && p.skey != nullptr;
+  if (skey) static_keys_to_lds<DT>(p, s_sk);
   __syncthreads();
 
   const int wv = blockIdx.x * nwaves + wslot;
@@ -580,6 +631,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
       const float dl = pr * (dwr - pdot);
       s_dl[lane] = dl;
       ge = DT::rnd(DT::rnd(dl) * p.scale);
+      if (skey) add_static_key<DT, RHC>(s_sk + ps * R + ph * rh, kch, kr);  // the scored key; dk is its gradient
       if (p.key_norm) kinv = key_inv_rms<DT, RHC>(kr, kch, rh, p.eps);
       float m = 0.f;
 #pragma unroll

@@ -18,6 +18,9 @@ static hipError_t fast_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream
   if (L.feat == kFeatDyn) {
     ATTNRES_FAST_SWITCH(fast_bwd_t, p, kFeatDyn)
   }
+  if (L.feat == (kFeatDyn | kFeatStatic)) {
+    ATTNRES_FAST_SWITCH(fast_bwd_t, p, kFeatDyn | kFeatStatic)
+  }
   ATTNRES_FAST_SWITCH(fast_bwd_t, p, kFeatAll)
 }
 

@@ -18,6 +18,9 @@ static hipError_t fast_fwd_dt(const ReadParams& p, const Launch& L, hipStream_t 
   if (L.feat == kFeatDyn) {
     ATTNRES_FAST_SWITCH(fast_fwd_t, p, kFeatDyn)
   }
+  if (L.feat == (kFeatDyn | kFeatStatic)) {
+    ATTNRES_FAST_SWITCH(fast_fwd_t, p, kFeatDyn | kFeatStatic)
+  }
   ATTNRES_FAST_SWITCH(fast_fwd_t, p, kFeatAll)
 }
 

@@ -29,6 +29,10 @@ __host__ __device__ constexpr int lr_fast_slot_floor(int cb, int rhc, int nb) {
   return nb <= 8 ? 1 : nb <= 16 ? 9 : 17;
 }
 
+// Optional code sets of the fast LR kernels (FEAT template parameter): per-token
+// query and gate, output norm, per-source static key.
+constexpr int kFeatDyn = 1, kFeatNorm = 2, kFeatStatic = 4, kFeatAll = 7;
+
 struct ReadParams {
   const void* val[kMaxSources];
   const void* key[kMaxSources];
@@ -58,6 +62,7 @@ struct ReadParams {
   int32_t np;  // lanes per head in the (head, source) pair layout: next power of two >= n_src
   int32_t kdt;  // dtype code of the LR keys and their gradients (the value dtype unless the desc says otherwise)
   int32_t ldt;  // dtype code of the LR logit path: query, rounded keys, logits, their gradients
+  const void* skey;  // LR static source keys [n_src, R] (key dtype) added to every key, or null
 };
 
 struct ReadBwdParams {
@@ -88,6 +93,18 @@ __host__ __device__ inline int64_t part_index(int layout, int64_t w, int i, int 
 }
 // slots per workgroup row in the workspace (tiled rows are padded to whole tiles)
 __host__ __device__ inline int part_stride(int n_part) { return (n_part + kPartTile - 1) / kPartTile * kPartTile; }
+
+// Token sums of the LR key gradients per source (the static keys' gradient):
+// partial sums per (source, token chunk), then a fixed-order sum over chunks.
+constexpr int kColsumMaxChunks = 128;
+constexpr int kColsumTokens = 256;  // tokens per chunk at least
+struct ColsumParams {
+  const void* dk[kMaxSources];  // [n_tok, R] dense, key dtype
+  float* partials;              // [n_src][chunks][R]
+  void* out;                    // [n_src, R] key dtype
+  int64_t n_tok;
+  int32_t n_src, R, chunks, kdt;
+};
 
 struct ReduceParams {
   const float* partials;      // layout: kPart*

@@ -40,6 +40,9 @@ gated_query_ref                           closed form (zero gate -> static)
 block_* helpers                           the reference tests' known answers
 lrid_fused_projection_split_ref           the reference model itself: whole-model
                                           golden vectors (tests/golden/model_*)
+static_key_add_ref                        the model's broadcast add itself (one line);
+                                          the static-key reads are checked against
+                                          the pinned LR read of the summed keys
 lrid_block_accumulate_ref                 composition of the pinned split and
                                           block_* helpers; the decoder built on
                                           it reproduces the reference-model
@@ -420,6 +423,13 @@ def lrid_fused_projection_split_ref(projected: Tensor, output_dim: int, rank: in
     return out, key
 
 
+def static_key_add_ref(keys, static_keys):
+    """Keys with each source's static key added: ``key + static.to(key.dtype)``
+    broadcast over (B, T) (``_add_static_lrid_source_key`` model.py:2046-2049,
+    ``LRIDStaticKey.forward`` :286-288)."""
+    return [k + static_keys[i].to(k.dtype) for i, k in enumerate(keys)]
+
+
 def lrid_block_accumulate_ref(projected: Tensor, partial_value, partial_key, output_dim: int, rank: int,
                               num_heads: int = 1, key_norm: bool = True, complete: bool = False,
                               partial_scale=1.0, value_norm: bool = False, scale_key: bool = False):
@@ -488,6 +498,7 @@ __all__ = [
     "block_count_logit_bias",
     "phase1_from_logits_ref",
     "lrid_block_accumulate_ref",
+    "static_key_add_ref",
     "attention_residual_phase1_ref",
     "attention_residual_phase2_ref",
     "lrid_attention_residual_phase2_ref",

@@ -52,7 +52,7 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 5
+    assert lib.attnres_abi_version() == 6
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()
@@ -133,6 +133,7 @@ def test_host_validation_rejects_bad_descriptions_without_launching():
         (dict(key_dtype=9), -1, b"key dtype"),
         (dict(key_dtype=0, gate=0x5000, query_dyn=0x6000, query_dyn_row_stride=16, gate_act=2), -2,
          b"gated query needs keys in the value dtype"),
+        (dict(rank=0, heads=1, static_keys=0x7000), -1, b"static_keys apply to LR reads only"),
     ]
     for kw, code, msg in cases:
         n_src = kw.pop("n_src", 3)
@@ -158,6 +159,35 @@ def test_workspace_size_is_a_host_computation():
     assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 5 * (64 + 13) * 4
     d.n_tok = 0
     assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 0
+    # static keys: their column sums follow the partial rows (on a 256-byte
+    # boundary), one fp32 row of rank per source and chunk of >= 256 tokens (<= 128 chunks)
+    d = _desc(n_src=17, n_tok=16384, dim=2048, rank=128, heads=8, static_keys=0x7000)
+    rows = 4096 * 128 * 4
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == rows + 17 * 64 * 128 * 4
+    d.n_tok = 100000
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == rows + 17 * 128 * 128 * 4
+    d.n_tok = 3
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == (3 * 128 * 4 + 255) // 256 * 256 + 17 * 128 * 4
+
+
+@needs_lib
+def test_static_key_gradient_needs_static_keys():
+    lib = H.load()
+    d = _desc()
+    g = H.ReadGrads()
+    dv = (ctypes.c_void_p * 3)(*([0x8000] * 3))
+    g.grad_out, g.weights, g.dvalues, g.dkeys = 0x9000, ctypes.cast(ctypes.c_void_p(0xa000), ctypes.POINTER(ctypes.c_float)), dv, dv
+    g.dstatic_keys = 0xb000
+    assert lib.attnres_read_backward(ctypes.byref(d), ctypes.byref(g), None) == -1
+    assert b"dstatic_keys without static_keys" in lib.attnres_last_error()
+
+
+def test_static_keys_shape_is_checked_on_the_host():
+    vs = [torch.randn(1, 2, 8) for _ in range(3)]
+    ks = [torch.randn(1, 2, 4) for _ in range(3)]
+    with pytest.raises(RuntimeError, match="static_keys must be"):
+        ops.lrid_attention_residual_read(vs, ks, torch.zeros(1, 4), 1, 1.0, True, static_keys=torch.zeros(3, 5))
+    assert ops._static_keys([torch.ones(4)] * 3, 3, 4, torch.bfloat16, "x").shape == (3, 4)
 
 
 def test_product_path_fails_loudly_on_cpu_tensors():

@@ -55,6 +55,22 @@ def test_compiled_lr_read_matches_eager():
     _compare(fn, [*vals, *keys, q], up)
 
 
+def test_compiled_lr_read_with_static_keys_matches_eager():
+    g = gen(53)
+    B, T, D, S, R, H = 2, 24, 512, 5, 32, 2
+    vals = [randn(g, (B, T, D), torch.bfloat16).to(DEV).requires_grad_(True) for _ in range(S)]
+    keys = [randn(g, (B, T, R), torch.bfloat16).to(DEV).requires_grad_(True) for _ in range(S)]
+    sk = randn(g, (S, R), torch.float32, 0.1).to(DEV).requires_grad_(True)
+    q = randn(g, (H, R // H), torch.float32, 0.5).to(DEV).requires_grad_(True)
+    up = randn(g, (B, T, D), torch.bfloat16).to(DEV)
+
+    def fn(*t):
+        return ops.lrid_attention_residual_read(list(t[:S]), list(t[S:2 * S]), t[-1], H, 0.25, False,
+                                                static_keys=t[-2])
+
+    _compare(fn, [*vals, *keys, sk, q], up)
+
+
 def test_compiled_phase_schedule_matches_eager():
     g = gen(52)
     B, T, D, S = 2, 16, 256, 3
