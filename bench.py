@@ -47,8 +47,11 @@ CONFIGS = {
     "c2": dict(kind="base", B=8, T=1024, D=768, N=7, R=0, H=1, scale=1.0, dtype=torch.bfloat16, qstd=0.02,
                block_summaries=True, sets=2),
     "c3": dict(kind="lr", B=8, T=2048, D=1024, N=13, R=64, H=4, scale=0.25, dtype=torch.bfloat16, qstd=0.02),
+    # C4 by its full definition: keys rms_norm(v_s) @ W_k (W_k ~ N(0, 0.02); produced
+    # outside the timed step, as the model projects them once per source) plus a
+    # static source key [N, 128] ~ N(0, 0.02) added inside the read
     "c4": dict(kind="lr_gated", B=4, T=4096, D=2048, N=17, R=128, H=8, scale=0.25, dtype=torch.bfloat16,
-               qstd=0.02),
+               qstd=0.02, value_keys=True, static_keys=True),
 }
 
 
@@ -258,7 +261,13 @@ class Workload:
             self.values = [rn(B, T, D)] + [(rn(B, T, D) + rn(B, T, D)) * 0.5 for _ in range(N - 1)]
         else:
             self.values = [rn(B, T, D) for _ in range(N)]
-        self.keys = [rn(B, T, R) for _ in range(N)] if R else []
+        if c.get("value_keys"):
+            import attnres_ops as ops
+            with torch.no_grad():
+                self.keys = ops.lrid_value_key_projection(self.values, rn(R, D, std=0.02))
+        else:
+            self.keys = [rn(B, T, R) for _ in range(N)] if R else []
+        self.static = rn(N, R, std=0.02) if c.get("static_keys") else None
         if c["kind"] == "base":
             self.query = rn(D, std=c["qstd"])
         else:
@@ -268,7 +277,7 @@ class Workload:
         self.grad_out = rn(B, T, D)
         gate_act = H.GATE_SIGMOID if self.gate is not None else H.GATE_NONE
         self.desc = H.Desc(self.values, self.keys, self.query, self.query_dyn, self.gate, None, Hh, c["scale"], True,
-                           False, H.MODE_SOFTMAX, gate_act, self.gate is not None)
+                           False, H.MODE_SOFTMAX, gate_act, self.gate is not None, static_keys=self.static)
         self.out = torch.empty((self.n_tok, D), device=device, dtype=dt)
         self.weights = torch.empty((self.n_tok, Hh, N), device=device, dtype=torch.float32)
         self.dvals = [torch.empty((self.n_tok, D), device=device, dtype=dt) for _ in range(N)]
@@ -293,6 +302,8 @@ class Workload:
         gr.dgate = self.dg.data_ptr() if self.dg is not None else None
         gr.workspace = self.ws.data_ptr()
         gr.workspace_bytes = ws
+        self.dstatic = torch.empty_like(self.static) if self.static is not None else None
+        gr.dstatic_keys = self.dstatic.data_ptr() if self.dstatic is not None else None
         self.grads = gr
         self.wptr = ctypes.cast(ctypes.c_void_p(self.weights.data_ptr()), ctypes.POINTER(ctypes.c_float))
         self.outptr = ctypes.c_void_p(self.out.data_ptr())
@@ -592,7 +603,9 @@ def main():
         "config": {"workload": f"{args.config}: " + ("LR" if c["kind"] != "base" else "base")
                    + f" read fwd+bwd B{c['B']} T{c['T']} d{c['D']} N{c['N']}"
                    + (f" r{c['R']} H{c['H']}" if c["R"] else "") + (" gated dyn query" if c["kind"] == "lr_gated"
-                                                                    else ""),
+                                                                    else "")
+                   + (" keys rms_norm(v)W_k" if c.get("value_keys") else "")
+                   + (" + static source keys" if c.get("static_keys") else ""),
                    "tokens": n_tok, "parallelism": "single GPU", "input_sets": c.get("sets", 1)},
         "hbm_gbs_step": round(gbs_step, 1),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,

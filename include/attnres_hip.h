@@ -460,6 +460,34 @@ int attnres_block_accum_backward(const attnres_block_accum_desc* desc, const voi
                                  const float* value_inv_rms, void* grad_projected, void* grad_partial_key,
                                  float* grad_value_scale, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Value-derived LR keys (config 4's key producer): the rms-norm on either side
+ * of LRIDSourceKeyProjection's projection GEMM (model.py:391-428 with
+ * lrid_key_from_value and lrid_key_value_norm):  key_s = rms_norm(v_s) @ W^T.
+ * The GEMM itself is the caller's (a library GEMM over all sources at once,
+ * [n_src * n_tok, dim] x [dim, rank]); these entry points produce its input and
+ * take its input gradient back to the values.
+ */
+typedef struct attnres_value_key_desc {
+  int32_t n_src;                   /* 1..ATTNRES_MAX_SOURCES */
+  int32_t dtype;                   /* ATTNRES_DTYPE_* of the values (and the normed rows) */
+  int64_t n_tok;                   /* rows per source */
+  int32_t dim;                     /* D: <= 4096 (16-bit) / 2048 (fp32) on aligned rows, else <= 512 */
+  float norm_eps;                  /* torch's default: FLT_EPSILON */
+  const void* const* values;       /* [n_src] device pointers */
+  const int64_t* value_row_stride; /* [n_src] elements */
+} attnres_value_key_desc;
+
+/* normed [n_src, n_tok, dim] dense (dtype): rms_norm(v) rounded once;
+ * inv_rms [n_src, n_tok] fp32 (for the backward). */
+int attnres_value_norm_forward(const attnres_value_key_desc* desc, void* normed, float* inv_rms, void* stream);
+
+/* grad_normed [n_src, n_tok, dim] dense: the GEMM's input gradient;
+ * grad_values [n_src] device pointers, each [n_tok, dim] dense (written, not
+ * accumulated): the rms-norm backward, rounded once. */
+int attnres_value_norm_backward(const attnres_value_key_desc* desc, const void* grad_normed, const float* inv_rms,
+                                void* const* grad_values, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

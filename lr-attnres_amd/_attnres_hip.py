@@ -188,6 +188,12 @@ class BlockAccumDesc(ctypes.Structure):
                 ("value_scale", c_float), ("value_scale_dev", POINTER(c_float))]
 
 
+class ValueKeyDesc(ctypes.Structure):
+    """attnres_value_key_desc (include/attnres_hip.h)."""
+    _fields_ = [("n_src", c_int32), ("dtype", c_int32), ("n_tok", c_int64), ("dim", c_int32),
+                ("norm_eps", c_float), ("values", POINTER(c_void_p)), ("value_row_stride", POINTER(c_int64))]
+
+
 def load() -> ctypes.CDLL:
     """Load the HIP library once; raise with a build hint if it is missing."""
     global _lib
@@ -243,6 +249,11 @@ def load() -> ctypes.CDLL:
     lib.attnres_block_accum_backward.argtypes = [POINTER(BlockAccumDesc), c_void_p, c_int64, c_void_p,
                                                  POINTER(c_float), POINTER(c_float), c_void_p, c_void_p,
                                                  POINTER(c_float), c_void_p, c_size_t, c_void_p]
+    lib.attnres_value_norm_forward.restype = c_int
+    lib.attnres_value_norm_forward.argtypes = [POINTER(ValueKeyDesc), c_void_p, POINTER(c_float), c_void_p]
+    lib.attnres_value_norm_backward.restype = c_int
+    lib.attnres_value_norm_backward.argtypes = [POINTER(ValueKeyDesc), c_void_p, POINTER(c_float),
+                                                POINTER(c_void_p), c_void_p]
     lib.attnres_kernel_timing.restype = c_int
     lib.attnres_kernel_timing.argtypes = [c_int]
     lib.attnres_test_phase2_block_layout.restype = c_int
@@ -727,3 +738,51 @@ def block_accum_backward(d: BlockAccumDesc, device, dtype, grad_value, grad_key,
         _ptr(gy), _ptr(dpk), _fptr(ds), _ptr(ws), ws_bytes, _stream(device))
     _check(rc, "block accumulation backward")
     return gy, dpk, ds
+
+
+# ---------------------------------------------------------------------------
+# value-derived keys (rms-norm around the key projection GEMM)
+# ---------------------------------------------------------------------------
+
+class ValueKey:
+    """Descriptor of the rms-norm of N value sources [B, T, D] (last dim contiguous)."""
+
+    def __init__(self, values, eps=FLT_EPSILON):
+        n = len(values)
+        v0 = values[0]
+        self._tensors = list(values)
+        self.n_src = n
+        self.n_tok = v0.size(0) * v0.size(1)
+        self.D = v0.size(-1)
+        self._vals = (c_void_p * n)(*[t.data_ptr() for t in values])
+        self._vstr = (c_int64 * n)(*[t.stride(1) for t in values])
+        d = ValueKeyDesc()
+        d.n_src = n
+        d.dtype = DTYPE_CODE[v0.dtype]
+        d.n_tok = self.n_tok
+        d.dim = self.D
+        d.norm_eps = float(eps)
+        d.values = self._vals
+        d.value_row_stride = self._vstr
+        self.c = d
+
+
+def value_norm_forward(d: ValueKey, device, dtype):
+    """(normed [N * n_tok, D] dense, inv_rms [N, n_tok] fp32)."""
+    lib = load()
+    normed = torch.empty((d.n_src * d.n_tok, d.D), device=device, dtype=dtype)
+    inv = torch.empty((d.n_src, d.n_tok), device=device, dtype=torch.float32)
+    rc = lib.attnres_value_norm_forward(ctypes.byref(d.c), _ptr(normed), _fptr(inv), _stream(device))
+    _check(rc, "value norm forward")
+    return normed, inv
+
+
+def value_norm_backward(d: ValueKey, device, dtype, grad_normed, inv, lead):
+    """The values' gradients (N tensors lead + (D,)) from the normed rows' gradient [N * n_tok, D]."""
+    lib = load()
+    dvals = _row_blocks(d.n_src, d.n_tok, d.D, device, dtype, True, lead)
+    arr = (c_void_p * d.n_src)(*[t.data_ptr() for t in dvals])
+    rc = lib.attnres_value_norm_backward(ctypes.byref(d.c), _ptr(grad_normed.contiguous()), _fptr(inv), arr,
+                                         _stream(device))
+    _check(rc, "value norm backward")
+    return dvals

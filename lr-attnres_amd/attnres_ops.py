@@ -1151,6 +1151,81 @@ def lrid_fused_projection_split(projected: Tensor, output_dim: int, rank: int, n
     return out.view(*lead, output_dim), key.view(*lead, rank)
 
 
+# ------------------------------------------------------------------ value-derived keys
+
+class _ValueKeyFn(torch.autograd.Function):
+    """Eager autograd of the value-derived keys: inputs (meta, W [R, D], *values);
+    outputs N keys [B, T, R]."""
+
+    @staticmethod
+    def forward(ctx, meta, weight, *values):
+        value_norm, = meta
+        v0 = values[0]
+        B, T, D = v0.shape
+        n = len(values)
+        R = weight.size(0)
+        ctx.set_materialize_grads(False)
+        if value_norm:
+            d = _hip.ValueKey(values)
+            with _device_ctx(v0.device):
+                x, inv = _hip.value_norm_forward(d, v0.device, v0.dtype)
+            ctx.desc, ctx.inv = d, inv
+        else:
+            x = torch.stack([v.reshape(B * T, D) for v in values]).reshape(n * B * T, D)
+            ctx.desc = None
+        # one library GEMM over every source's rows: [N * n_tok, D] x [D, R]
+        keys = torch.mm(x, weight.t())
+        ctx.save_for_backward(weight, x, *values)
+        ctx.shape = (n, B, T, D, R)
+        return tuple(keys.view(n, B, T, R).unbind(0))
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grad_keys):
+        weight, x, *values = ctx.saved_tensors
+        n, B, T, D, R = ctx.shape
+        if all(g is None for g in grad_keys):
+            return (None, None) + (None,) * n
+        gk = torch.stack([g.reshape(B * T, R) if g is not None else x.new_zeros((B * T, R)) for g in grad_keys])
+        gk = gk.reshape(n * B * T, R)
+        want = ctx.needs_input_grad  # (meta, weight, *values)
+        dw = torch.mm(gk.t(), x) if want[1] else None
+        dvals = [None] * n
+        if any(want[2:]):
+            gx = torch.mm(gk, weight)
+            if ctx.desc is not None:
+                with _device_ctx(x.device):
+                    dvals = _hip.value_norm_backward(ctx.desc, x.device, x.dtype, gx, ctx.inv, (B, T))
+            else:
+                dvals = list(gx.view(n, B, T, D).unbind(0))
+        return (None, dw) + tuple(dv if want[2 + i] else None for i, dv in enumerate(dvals))
+
+
+def lrid_value_key_projection(values, weight: Tensor, value_norm: bool = True):
+    """LR keys projected from the sources' values: ``rms_norm(v_s) @ W^T``.
+
+    Not in the reference's op module: the reference's
+    ``LRIDSourceKeyProjection.forward`` (model.py:420-428, with
+    ``lrid_key_from_value`` and ``lrid_key_value_norm``) does this per source as
+    ``self.proj(norm(x))`` -- config 4's key producer.  Here one HIP pass
+    rms-norms every source (fp32, one rounding to the dtype) into one block, a
+    single library GEMM projects all of them, and the backward runs the GEMMs
+    for the weight and input gradients and one HIP pass of the rms-norm
+    backward.  ``values``: N x [B, T, D] (or [N, B, T, D]); ``weight`` [R, D]
+    (``nn.Linear(D, R).weight``).  Returns N keys [B, T, R] in the values' dtype.
+    """
+    vs = _sources(values)
+    _check_sources(vs, "lrid_value_key_projection")
+    _check_gpu(vs + [weight], "lrid_value_key_projection")
+    vs = _promote(vs)
+    D = vs[0].size(-1)
+    if weight.dim() != 2 or weight.size(1) != D:
+        raise RuntimeError(f"lrid_value_key_projection: weight must be [rank, {D}], got {tuple(weight.shape)}")
+    vs = [_hip.as_rows(t) for t in vs]
+    w = weight.to(vs[0].dtype)
+    return list(_ValueKeyFn.apply((bool(value_norm),), w, *vs))
+
+
 # ------------------------------------------------------------------ block-summary accumulation
 
 class _BlockAccumFn(torch.autograd.Function):

@@ -113,6 +113,8 @@ int check_desc(const attnres_read_desc* d) {
   }
   if (d->static_keys && (d->mode != ATTNRES_MODE_SOFTMAX || d->rank == 0))
     return fail(ATTNRES_EINVAL, "static_keys apply to LR reads only");
+  if (d->static_keys && d->rank > 256)
+    return fail(ATTNRES_EUNSUPPORTED, "static_keys need rank <= 256, got %d", d->rank);
   if (d->mode == ATTNRES_MODE_AVERAGE) return ATTNRES_OK;
   if (d->heads < 1) return fail(ATTNRES_EINVAL, "heads=%d < 1", d->heads);
   if (d->rank == 0) {
@@ -1637,5 +1639,93 @@ extern "C" int attnres_block_accum_backward(const attnres_block_accum_desc* d, c
     err = launch_reduce_partials(sd->dtype, rp, st);
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
   }
+  return ATTNRES_OK;
+}
+
+// ---------------------------------------------------------------- value-derived keys
+namespace {
+
+int check_value_key(const attnres_value_key_desc* d, bool* vec) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->n_src < 1 || d->n_src > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_src=%d outside [1, %d]", d->n_src, ATTNRES_MAX_SOURCES);
+  if (d->dtype != ATTNRES_DTYPE_F32 && d->dtype != ATTNRES_DTYPE_BF16 && d->dtype != ATTNRES_DTYPE_F16)
+    return fail(ATTNRES_EINVAL, "unknown dtype %d", d->dtype);
+  if (d->n_tok < 0) return fail(ATTNRES_EINVAL, "n_tok=%lld < 0", (long long)d->n_tok);
+  if (d->dim < 1) return fail(ATTNRES_EINVAL, "dim=%d < 1", d->dim);
+  if (!d->values || !d->value_row_stride) return fail(ATTNRES_EINVAL, "values / value_row_stride is NULL");
+  const int es = elem_size(d->dtype);
+  bool v = (d->dim * es) % 16 == 0;
+  for (int s = 0; s < d->n_src; ++s) {
+    if (d->n_tok > 0 && !d->values[s]) return fail(ATTNRES_EINVAL, "values[%d] is NULL", s);
+    if (d->value_row_stride[s] < d->dim || d->value_row_stride[s] > INT32_MAX)
+      return fail(ATTNRES_EINVAL, "value_row_stride[%d]=%lld must be in [dim, 2^31)", s,
+                  (long long)d->value_row_stride[s]);
+    v = v && aligned16(d->values[s]) && (d->value_row_stride[s] * es) % 16 == 0;
+  }
+  // a row is held in registers: 8 vectors per lane of 64
+  const int max_dim = 64 * 8 * (v ? 16 / es : 1);
+  if (d->dim > max_dim)
+    return fail(ATTNRES_EUNSUPPORTED, "dim=%d exceeds %d on the %s path", d->dim, max_dim, v ? "vector" : "unaligned");
+  *vec = v;
+  return ATTNRES_OK;
+}
+
+void fill_value_norm(const attnres_value_key_desc* d, ValueNormParams* p) {
+  memset(p, 0, sizeof(*p));
+  for (int s = 0; s < d->n_src; ++s) {
+    p->val[s] = d->values[s];
+    p->vstride[s] = (int32_t)d->value_row_stride[s];
+  }
+  p->n_tok = d->n_tok;
+  p->n_src = d->n_src;
+  p->D = d->dim;
+  p->eps = d->norm_eps;
+}
+
+int value_norm_grid(const attnres_value_key_desc* d) {
+  const int64_t rows = (int64_t)d->n_src * d->n_tok;
+  const int64_t wgs = (rows + 3) / 4;
+  return (int)(wgs < kMaxFwdGroups ? wgs : kMaxFwdGroups);
+}
+
+}  // namespace
+
+extern "C" int attnres_value_norm_forward(const attnres_value_key_desc* d, void* normed, float* inv_rms,
+                                          void* stream) {
+  bool vec = false;
+  int rc = check_value_key(d, &vec);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!normed || !inv_rms) return fail(ATTNRES_EINVAL, "normed / inv_rms is NULL");
+  vec = vec && aligned16(normed);
+  ValueNormParams p;
+  fill_value_norm(d, &p);
+  p.normed = normed;
+  p.inv = inv_rms;
+  hipError_t err = launch_value_norm(d->dtype, false, p, value_norm_grid(d), vec, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "value norm forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_value_norm_backward(const attnres_value_key_desc* d, const void* grad_normed,
+                                           const float* inv_rms, void* const* grad_values, void* stream) {
+  bool vec = false;
+  int rc = check_value_key(d, &vec);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!grad_normed || !inv_rms || !grad_values) return fail(ATTNRES_EINVAL, "grad_normed / inv_rms / grad_values is NULL");
+  vec = vec && aligned16(grad_normed);
+  ValueNormParams p;
+  fill_value_norm(d, &p);
+  for (int s = 0; s < d->n_src; ++s) {
+    if (!grad_values[s]) return fail(ATTNRES_EINVAL, "grad_values[%d] is NULL", s);
+    vec = vec && aligned16(grad_values[s]);
+    p.dval[s] = grad_values[s];
+  }
+  p.gnormed = grad_normed;
+  p.inv = const_cast<float*>(inv_rms);
+  hipError_t err = launch_value_norm(d->dtype, true, p, value_norm_grid(d), vec, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "value norm backward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
 }

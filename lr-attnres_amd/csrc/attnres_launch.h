@@ -27,6 +27,7 @@ hipError_t launch_average_forward(int dtype, const ReadParams& p, const Launch& 
 hipError_t launch_average_backward(int dtype, const ReadBwdParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_reduce_partials(int dtype, const ReduceParams& p, hipStream_t st);
 hipError_t launch_key_colsum(const ColsumParams& p, hipStream_t st);
+hipError_t launch_value_norm(int dtype, bool bwd, const ValueNormParams& p, int grid, bool vec, hipStream_t st);
 // LR fast path (head-aligned one-wave work items): L.wpt = columns per item,
 // L.nmax = source slots (8/16/32), L.teams = key chunks per head slot (2/8)
 hipError_t launch_lr_fast_forward(int dtype, const ReadParams& p, const Launch& L, hipStream_t st);

@@ -30,7 +30,7 @@ constexpr int kSrcGroup = 8;
 // (p.ldt).  Both equal the value dtype unless keys of another dtype are read
 // (the reference norms such keys in fp32 and rounds them to the value dtype:
 // attnres_ops.py:4179-4186); the fast kernels handle only equal dtypes.
-__device__ __forceinline__ int dtype_bytes(int code) { return code == 0 ? 4 : 2; }
+__host__ __device__ __forceinline__ int dtype_bytes(int code) { return code == 0 ? 4 : 2; }
 
 // query element j of head h for token tok (fp32 of a logit-dtype value;
 // composed queries are rounded to that dtype, as the reference casts the
@@ -534,37 +534,44 @@ static hipError_t lr_bwd_dt(const ReadBwdParams& p, const Launch& L, hipStream_t
 // d static_s = rnd(sum over tokens of dk_s): the reference's `key + static`
 // expands the static key over (B, T), whose backward sums the key-dtype
 // gradient rows with fp32 accumulation and rounds once.  Pass 1: workgroup
-// (chunk, source) sums its chunk of tokens for every column -- 256 / R token
-// phases of R threads for R <= 256 (coalesced row reads), phases folded in a
-// fixed order; pass 2: thread (source, column) adds the chunks in order.
+// (chunk, source) sums its chunk of tokens: a thread owns V consecutive
+// columns (one 16-byte load per row when the rows allow it) and one of P
+// token phases; the phases are folded in a fixed order through LDS.  Pass 2:
+// thread (source, column) adds the chunks in order and rounds.
+template <class DT, int V>
 __global__ void __launch_bounds__(256) key_colsum_kernel(const ColsumParams p) {
-  __shared__ float s_part[256];
+  using S = typename DT::S;
+  __shared__ float s_part[256 * V];
   const int c = blockIdx.x, s = blockIdx.y, R = p.R;
   const int64_t tpc = (p.n_tok + p.chunks - 1) / p.chunks;
   const int64_t t0 = (int64_t)c * tpc;
   const int64_t t1 = t0 + tpc < p.n_tok ? t0 + tpc : p.n_tok;
-  const int P = R <= 256 ? 256 / R : 1;  // token phases
+  const int cg = R / V;               // column groups (the host keeps cg <= 256)
+  const int P = 256 / cg;             // token phases
   const int tid = threadIdx.x;
-  const void* dk = p.dk[s];
+  const int ph = tid / cg, col = tid - (tid / cg) * cg;
+  const S* dk = (const S*)p.dk[s] + col * V;
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0.f;
+  if (ph < P) {
+#pragma unroll 8
+    for (int64_t t = t0 + ph; t < t1; t += P) {
+      float x[V];
+      load_vec<DT, V, true>(dk + t * R, x);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[v] += x[v];
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) s_part[tid * V + v] = acc[v];
+  __syncthreads();
   float* out = p.partials + ((int64_t)s * p.chunks + c) * R;
-  if (R <= 256) {
-    const int ph = tid / R, r = tid - (tid / R) * R;
-    float a = 0.f;
-    if (ph < P)
-      for (int64_t t = t0 + ph; t < t1; t += P) a += load_any(dk, t * R + r, p.kdt);
-    s_part[tid] = a;
-    __syncthreads();
-    if (tid < R) {
-      float sum = 0.f;
-      for (int k = 0; k < P; ++k) sum += s_part[k * R + tid];
-      out[tid] = sum;
-    }
-  } else {
-    for (int r = tid; r < R; r += 256) {
-      float a = 0.f;
-      for (int64_t t = t0; t < t1; ++t) a += load_any(dk, t * R + r, p.kdt);
-      out[r] = a;
-    }
+  for (int r = tid; r < R; r += 256) {
+    const int g = r / V, v = r - (r / V) * V;
+    float sum = 0.f;
+    for (int k = 0; k < P; ++k) sum += s_part[(k * cg + g) * V + v];
+    out[r] = sum;
   }
 }
 
@@ -573,13 +580,39 @@ __global__ void __launch_bounds__(256) key_colsum_finish_kernel(const ColsumPara
   if (i >= (int64_t)p.n_src * p.R) return;
   const int s = (int)(i / p.R), r = (int)(i - (int64_t)s * p.R);
   const float* row = p.partials + (int64_t)s * p.chunks * p.R + r;
+  // in chunk order; 16 loads in flight per batch
   float a = 0.f;
-  for (int c = 0; c < p.chunks; ++c) a += row[(int64_t)c * p.R];
+  for (int c0 = 0; c0 < p.chunks; c0 += 16) {
+    float t[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t[k] = c0 + k < p.chunks ? row[(int64_t)(c0 + k) * p.R] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a += t[k];
+  }
   store_any(p.out, i, p.kdt, a);
 }
 
+template <class DT>
+static void key_colsum_t(const ColsumParams& p, bool vec, hipStream_t st) {
+  constexpr int EV = 16 / sizeof(typename DT::S);
+  const dim3 g(p.chunks, p.n_src), b(256);
+  if (vec) hipLaunchKernelGGL((key_colsum_kernel<DT, EV>), g, b, 0, st, p);
+  else hipLaunchKernelGGL((key_colsum_kernel<DT, 1>), g, b, 0, st, p);
+}
+
 hipError_t launch_key_colsum(const ColsumParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(key_colsum_kernel, dim3(p.chunks, p.n_src), dim3(256), 0, st, p);
+  // 16-byte rows when every source's dk rows are aligned for them; column
+  // groups must fit the 256 threads (rank <= 256 scalar, <= 2048 / 1024 vector)
+  const int es = dtype_bytes(p.kdt);
+  bool vec = (p.R * es) % 16 == 0;
+  for (int s = 0; vec && s < p.n_src; ++s) vec = ((uintptr_t)p.dk[s] & 15u) == 0;
+  const int cg = vec ? p.R * es / 16 : p.R;
+  if (cg > 256) return hipErrorInvalidValue;
+  switch (p.kdt) {
+    case ATTNRES_DTYPE_F32: key_colsum_t<F32>(p, vec, st); break;
+    case ATTNRES_DTYPE_BF16: key_colsum_t<BF16>(p, vec, st); break;
+    default: key_colsum_t<F16>(p, vec, st); break;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t n = (int64_t)p.n_src * p.R;

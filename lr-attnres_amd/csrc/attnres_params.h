@@ -97,13 +97,26 @@ __host__ __device__ inline int part_stride(int n_part) { return (n_part + kPartT
 // Token sums of the LR key gradients per source (the static keys' gradient):
 // partial sums per (source, token chunk), then a fixed-order sum over chunks.
 constexpr int kColsumMaxChunks = 128;
-constexpr int kColsumTokens = 256;  // tokens per chunk at least
+constexpr int kColsumTokens = 128;  // tokens per chunk at least
 struct ColsumParams {
   const void* dk[kMaxSources];  // [n_tok, R] dense, key dtype
   float* partials;              // [n_src][chunks][R]
   void* out;                    // [n_src, R] key dtype
   int64_t n_tok;
   int32_t n_src, R, chunks, kdt;
+};
+
+// Value-derived keys: rms-norm of every source row into one dense block
+struct ValueNormParams {
+  const void* val[kMaxSources];
+  int32_t vstride[kMaxSources];  // row strides in elements
+  void* dval[kMaxSources];       // backward: [n_tok, D] dense
+  void* normed;                  // [n_src, n_tok, D] dense
+  const void* gnormed;           // backward: its gradient, same layout
+  float* inv;                    // [n_src, n_tok]
+  int64_t n_tok;
+  int32_t n_src, D;
+  float eps;
 };
 
 struct ReduceParams {

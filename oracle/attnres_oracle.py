@@ -40,6 +40,8 @@ gated_query_ref                           closed form (zero gate -> static)
 block_* helpers                           the reference tests' known answers
 lrid_fused_projection_split_ref           the reference model itself: whole-model
                                           golden vectors (tests/golden/model_*)
+lrid_value_key_projection_ref             the model's norm + Linear (two library ops);
+                                          norm pinned with the read's rms-norm
 static_key_add_ref                        the model's broadcast add itself (one line);
                                           the static-key reads are checked against
                                           the pinned LR read of the summed keys
@@ -423,6 +425,15 @@ def lrid_fused_projection_split_ref(projected: Tensor, output_dim: int, rank: in
     return out, key
 
 
+def lrid_value_key_projection_ref(values, weight: Tensor, value_norm: bool = True):
+    """Keys projected from the values: ``LRIDSourceKeyProjection.forward``
+    (model.py:420-428) with ``lrid_key_from_value`` -- ``norm(x)`` when
+    ``lrid_key_value_norm``, then the rank-R ``nn.Linear`` without bias (no key
+    norm on this path: ``use_key_norm`` is off with ``lrid_key_from_value``,
+    :418)."""
+    return [F.linear(norm(v) if value_norm else v, weight.to(v.dtype)) for v in values]
+
+
 def static_key_add_ref(keys, static_keys):
     """Keys with each source's static key added: ``key + static.to(key.dtype)``
     broadcast over (B, T) (``_add_static_lrid_source_key`` model.py:2046-2049,
@@ -499,6 +510,7 @@ __all__ = [
     "phase1_from_logits_ref",
     "lrid_block_accumulate_ref",
     "static_key_add_ref",
+    "lrid_value_key_projection_ref",
     "attention_residual_phase1_ref",
     "attention_residual_phase2_ref",
     "lrid_attention_residual_phase2_ref",

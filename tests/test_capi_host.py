@@ -40,6 +40,7 @@ def test_library_exports_every_declared_symbol():
                             "attnres_keyed_logits_forward", "attnres_keyed_logits_backward",
                             "attnres_keyed_logits_backward_workspace_size", "attnres_kernel_timing",
                             "attnres_kernel_times", "attnres_read_backward_noalloc", "attnres_test_phase2_block_layout",
+                            "attnres_value_norm_forward", "attnres_value_norm_backward",
                             "attnres_block_accum_forward", "attnres_block_accum_backward",
                             "attnres_block_accum_backward_workspace_size"])
     for n in names:
@@ -66,7 +67,7 @@ def test_abi_version_and_error_reporting():
 STRUCTS = ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads"),
            (H.Phase1Desc, "attnres_phase1_desc"), (H.Phase2Desc, "attnres_phase2_desc"),
            (H.Phase2Grads, "attnres_phase2_grads"), (H.KeyedSplitDesc, "attnres_keyed_split_desc"),
-           (H.BlockAccumDesc, "attnres_block_accum_desc"))
+           (H.BlockAccumDesc, "attnres_block_accum_desc"), (H.ValueKeyDesc, "attnres_value_key_desc"))
 
 
 def _c_layout():
@@ -160,12 +161,12 @@ def test_workspace_size_is_a_host_computation():
     d.n_tok = 0
     assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 0
     # static keys: their column sums follow the partial rows (on a 256-byte
-    # boundary), one fp32 row of rank per source and chunk of >= 256 tokens (<= 128 chunks)
+    # boundary), one fp32 row of rank per source and chunk of >= 128 tokens (<= 128 chunks)
     d = _desc(n_src=17, n_tok=16384, dim=2048, rank=128, heads=8, static_keys=0x7000)
     rows = 4096 * 128 * 4
-    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == rows + 17 * 64 * 128 * 4
-    d.n_tok = 100000
     assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == rows + 17 * 128 * 128 * 4
+    d.n_tok = 1000
+    assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == 1000 * 128 * 4 + 17 * 8 * 128 * 4
     d.n_tok = 3
     assert lib.attnres_read_backward_workspace_size(ctypes.byref(d)) == (3 * 128 * 4 + 255) // 256 * 256 + 17 * 128 * 4
 
@@ -517,3 +518,33 @@ def test_phase2_layout_hook_validates_and_kernel_times_need_timing():
     buf = (ctypes.c_float * 4)()
     assert lib.attnres_kernel_times(buf, 4) == -1
     assert b"not enabled" in lib.attnres_last_error()
+
+
+@needs_lib
+def test_value_norm_host_validation():
+    lib = H.load()
+    vals = (ctypes.c_void_p * 2)(0x1000, 0x1000)
+    vstr = (ctypes.c_int64 * 2)(2048, 2048)
+    d = H.ValueKeyDesc()
+    d.n_src, d.dtype, d.n_tok, d.dim, d.norm_eps = 2, 1, 8, 2048, H.FLT_EPSILON
+    d.values, d.value_row_stride = vals, vstr
+    inv = ctypes.cast(ctypes.c_void_p(0x3000), ctypes.POINTER(ctypes.c_float))
+    assert lib.attnres_value_norm_forward(ctypes.byref(d), None, inv, None) == -1
+    assert b"normed" in lib.attnres_last_error()
+    d.dim = 4104
+    vstr[0] = vstr[1] = 4104
+    assert lib.attnres_value_norm_forward(ctypes.byref(d), ctypes.c_void_p(0x2000), inv, None) == -2
+    assert b"exceeds 4096" in lib.attnres_last_error()
+    d.dim = 600  # unaligned rows are held at one element per lane vector: 512 at most
+    vstr[0] = vstr[1] = 601
+    assert lib.attnres_value_norm_forward(ctypes.byref(d), ctypes.c_void_p(0x2000), inv, None) == -2
+    assert b"unaligned" in lib.attnres_last_error()
+    d.dim, d.n_src = 64, 0
+    assert lib.attnres_value_norm_forward(ctypes.byref(d), ctypes.c_void_p(0x2000), inv, None) == -2
+    d.n_src, d.n_tok = 2, 0
+    assert lib.attnres_value_norm_backward(ctypes.byref(d), None, None, None, None) == 0
+
+
+def test_value_key_projection_fails_loudly_on_cpu_tensors():
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lrid_value_key_projection([torch.randn(1, 2, 8)] * 2, torch.randn(4, 8))
