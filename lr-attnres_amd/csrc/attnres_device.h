@@ -350,6 +350,27 @@ __device__ __forceinline__ void wave_sums(const float (&x)[V], float (&z)[V / 4]
     z[k] = t;
   }
 }
+// Many sums over the two 32-lane halves of a wave at once (V even): one
+// v_permlane16_swap and one add fold two values over lane distance 16 (the
+// first value's halves in rows 0 and 2, the second's in rows 1 and 3), and a
+// DPP all-reduce inside each row completes them.  Register j then holds, in
+// every lane of row r, value 2 j + (r & 1) summed over half r >> 1.  Fixed
+// order (deterministic results).
+template <int V>
+__device__ __forceinline__ void half_sums(const float (&x)[V], float (&z)[V / 2]) {
+  static_assert(V % 2 == 0, "half_sums folds pairs of values");
+#pragma unroll
+  for (int j = 0; j < V / 2; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[2 * j]), __float_as_uint(x[2 * j + 1]), false,
+                                                    false);
+    float t = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    t += dpp_f32<kDppXor1>(t);
+    t += dpp_f32<kDppXor2>(t);
+    t += dpp_f32<kDppHalfMirror>(t);
+    t += dpp_f32<kDppMirror>(t);
+    z[j] = t;
+  }
+}
 // value m of wave_sums' result (wave-uniform): row {0, 2, 1, 3}[m % 4] of z[m / 4]
 template <int V>
 __device__ __forceinline__ float wave_sums_get(const float (&z)[V / 4], int m) {

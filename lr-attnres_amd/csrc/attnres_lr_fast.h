@@ -385,17 +385,16 @@ __global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1)
         }
       }
     }
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < CB; ++c)
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        acc[c][e] = DT::rnd(acc[c][e]);
-        if (ok[c]) ss += acc[c][e] * acc[c][e];
-      }
-
-    // ---- stores
+    // ---- stores (each store's packing rounds the mix to the dtype)
     if ((FEAT & kFeatNorm) && p.norm_out) {  // one item covers the whole row here
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          acc[c][e] = DT::rnd(acc[c][e]);
+          if (ok[c]) ss += acc[c][e] * acc[c][e];
+        }
       if (p.out_prenorm) {
         S* xp = global_ptr<S>((uint64_t)p.out_prenorm) + tok * (int64_t)D;
 #pragma unroll
@@ -406,7 +405,7 @@ __global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1)
 #pragma unroll
       for (int c = 0; c < CB; ++c)
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[c][e] = DT::rnd(acc[c][e] * inv);
+        for (int e = 0; e < E; ++e) acc[c][e] = acc[c][e] * inv;
       if (lane == 0 && p.out_inv_rms) p.out_inv_rms[tok] = inv;
     }
     S* op = global_ptr<S>((uint64_t)p.out) + tok * (int64_t)D;
@@ -588,29 +587,60 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
         for (int i = 0; i < E / 2; ++i) gpk[c][i] = bits16<DT>(g[c][2 * i]) | (bits16<DT>(g[c][2 * i + 1]) << 16);
     }
+    // this lane's share of <g, v_s> over the wave's columns (one head's lanes
+    // of a column, or a head spanning both columns)
+    auto dw_part = [&](int s) {
+      float part = 0.f;
 #pragma unroll
-    for (int s = 0; s < NB; ++s) {
-      if (s < N) {
-        float part[CB];
+      for (int c = 0; c < CB; ++c) {
+        float pc = 0.f;
+        if constexpr (sizeof(S) == 2) {
 #pragma unroll
-        for (int c = 0; c < CB; ++c) {
-          part[c] = 0.f;
-          if constexpr (sizeof(S) == 2) {
-#pragma unroll
-            for (int i = 0; i < E / 2; ++i) part[c] = dot2<DT>(gpk[c][i], vr[s][c].w[i], part[c]);
-          } else {
-            float v[E];
-            unpack<DT, E>(vr[s][c], v);
-#pragma unroll
-            for (int e = 0; e < E; ++e) part[c] += g[c][e] * v[e];
-          }
-        }
-        if (CB == 2) {
-          const float t = wave_sum(part[0] + part[1]);  // one head spans both columns
-          if (lane == 0) s_dw[s] = t;
+          for (int i = 0; i < E / 2; ++i) pc = dot2<DT>(gpk[c][i], vr[s][c].w[i], pc);
         } else {
-          const float t = group_sum(part[0], gl);
-          if (ok[0] && (lane & (gl - 1)) == 0) s_dw[hd[0] * np + s] = t;
+          float v[E];
+          unpack<DT, E>(vr[s][c], v);
+#pragma unroll
+          for (int e = 0; e < E; ++e) pc += g[c][e] * v[e];
+        }
+        part = c == 0 ? pc : part + pc;
+      }
+      return part;
+    };
+    // Sources two at a time.  Two heads per wave (32-lane groups): one
+    // v_permlane16_swap fold and one DPP all-reduce give both sums, and lane
+    // 16 r writes (head r / 2, source 2 j + r % 2); otherwise a butterfly per
+    // source over the head's lane group.
+    const int r16 = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < (NB + 1) / 2; ++j) {
+      if (2 * j < N) {
+        float x[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int s = 2 * j + i;
+          x[i] = 0.f;
+          if (s < NB && s < N) x[i] = dw_part(s);
+        }
+        if (CB == 1 && gl == 32) {
+          float z[1];
+          half_sums<2>(x, z);
+          const int src = 2 * j + (r16 & 1), head = r16 >> 1;
+          if ((lane & 15) == 0 && src < N && head < nh) s_dw[head * np + src] = z[0];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int s = 2 * j + i;
+            if (s < NB && s < N) {
+              if (CB == 2) {
+                const float t = wave_sum(x[i]);  // one head spans both columns
+                if (lane == 0) s_dw[s] = t;
+              } else {
+                const float t = group_sum(x[i], gl);
+                if (ok[0] && (lane & (gl - 1)) == 0) s_dw[hd[0] * np + s] = t;
+              }
+            }
+          }
         }
       }
     }
@@ -685,6 +715,21 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     }
 
     // ---- stores: dv = w * g, dk, per-token dq
+    // 16-bit types: g again from its packed (dtype-exact) words, unpacked once
+    // here, so the unpacked row is not held through the dW loop
+    float gv[CB][E];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      if constexpr (sizeof(S) == 2) {
+        Raw<DT, E> r;
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) r.w[i] = gpk[c][i];
+        unpack<DT, E>(r, gv[c]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) gv[c][e] = g[c][e];
+      }
+    }
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
       if (s < N) {
@@ -693,21 +738,10 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
         for (int c = 0; c < CB; ++c) {
           if (ok[c]) {
             const float w = DT::rnd(s_p[hd[c] * np + s]);
-            // 16-bit types: g again from its packed (dtype-exact) words, so
-            // the unpacked row is not held through the dW loop
-            float gv[E];
-            if constexpr (sizeof(S) == 2) {
-              Raw<DT, E> r;
-#pragma unroll
-              for (int i = 0; i < E / 2; ++i) r.w[i] = gpk[c][i];
-              unpack<DT, E>(r, gv);
-            } else {
-#pragma unroll
-              for (int e = 0; e < E; ++e) gv[e] = g[c][e];
-            }
+            // the store's packing is the one rounding of w * g to the dtype
             float dv[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) dv[e] = DT::rnd(w * gv[e]);
+            for (int e = 0; e < E; ++e) dv[e] = w * gv[c][e];
             store_vec<DT, E, true>(dvp + eoff[c], dv);
           }
         }
@@ -724,7 +758,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
           for (int i = 0; i < KV; ++i) {
             const float dkh = DT::rnd(ge * q.get(j * KV + i));
-            t[i] = p.key_norm ? DT::rnd(kinv * (dkh - k[i] * kinv * mr)) : dkh;
+            t[i] = p.key_norm ? kinv * (dkh - k[i] * kinv * mr) : dkh;  // rounded by the store
           }
           store_vec<DT, KV>(dkp + j * KV, t);
         }
