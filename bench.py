@@ -24,6 +24,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -60,6 +61,10 @@ CONFIGS = {
 # a step is phase 1 once + phase 2 at each of the Q sites, forward and backward
 PHASE_CONFIGS = {
     "p5": dict(B=16, T=1024, D=768, S=6, Q=4, R=64, dtype=torch.bfloat16),
+    # the block LR decoder's form (C5): phase 2 with the partial block's LR key
+    # (r=64, key norm, logit scale 1/8), the lerp merge and the next sublayer's
+    # fused pre-norm
+    "p5lr": dict(B=16, T=1024, D=768, S=6, Q=4, R=64, dtype=torch.bfloat16, lr=True),
 }
 
 
@@ -71,6 +76,9 @@ def phase_bytes_per_token(c):
     p1b = Q * D * s + Q * 4 + S * D * s + Q * S * 4 + S * D * s + Q * S * 4
     p2f = 2 * D * s + 4 + D * s
     p2b = 3 * D * s + 4 + 2 * D * s + 4
+    if c.get("lr"):  # the partial key read (and its gradient written)
+        p2f += c["R"] * s
+        p2b += 2 * c["R"] * s
     # block accumulation, averaged over the Q sublayers of a block (the first has no
     # partial block to read): fwd reads y[:, :D+R] (+ partial value and key) and writes
     # value, key and the key's 1/rms; bwd reads both gradients, the raw key and 1/rms
@@ -107,15 +115,24 @@ class PhaseWorkload:
         self._dv = (ctypes.c_void_p * S)(*[t.data_ptr() for t in self.dvals])
         self.dlog = torch.empty((Q, S, n), device=device, dtype=torch.float32)
         self.partial = rn(n, D)
-        self.query = rn(D, std=0.02)
-        self.p2 = [H.Phase2(self.partial, None, self.query, None, self.out[q], self.lse[q], H.MERGE_ADDCMUL, True,
-                            False, 1.0, 0.693, None, 0.5, None, False) for q in range(Q)]
+        self.lr = bool(c.get("lr"))
+        if self.lr:
+            R = c["R"]
+            self.pkey = rn(n, R)
+            self.query = rn(R, std=0.02)
+            self.dpk = torch.empty((n, R), device=device, dtype=dt)
+            self.p2 = [H.Phase2(self.partial, self.pkey, self.query, None, self.out[q], self.lse[q], H.MERGE_LERP,
+                                True, True, 1.0 / math.sqrt(R), 0.693, None, 0.5, None, False) for q in range(Q)]
+        else:
+            self.query = rn(D, std=0.02)
+            self.p2 = [H.Phase2(self.partial, None, self.query, None, self.out[q], self.lse[q], H.MERGE_ADDCMUL,
+                                True, False, 1.0, 0.693, None, 0.5, None, False) for q in range(Q)]
         self.out2 = torch.empty((n, D), device=device, dtype=dt)
         self.g2 = rn(n, D)
         self.dp = torch.empty((n, D), device=device, dtype=dt)
         self.di = torch.empty((n, D), device=device, dtype=dt)
         self.dl = torch.empty((n,), device=device, dtype=torch.float32)
-        self.dq = torch.empty((D,), device=device, dtype=dt)
+        self.dq = torch.empty_like(self.query)
         ws = lib.attnres_phase2_backward_workspace_size(ctypes.byref(self.p2[0].c))
         self.ws = torch.empty((max(1, ws),), device=device, dtype=torch.uint8)
         gr = H.Phase2Grads()
@@ -123,6 +140,8 @@ class PhaseWorkload:
         gr.dpartial_value = self.dp.data_ptr()
         gr.dquery = self.dq.data_ptr()
         gr.dinterblock_output = self.di.data_ptr()
+        if self.lr:
+            gr.dpartial_key = self.dpk.data_ptr()
         gr.dinterblock_lse = ctypes.cast(ctypes.c_void_p(self.dl.data_ptr()), ctypes.POINTER(ctypes.c_float))
         gr.workspace = self.ws.data_ptr()
         gr.workspace_bytes = ws
@@ -220,8 +239,10 @@ def bench_phase(args, dev):
         "value": round(wl.n_tok / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q']} x phase2 (base, key_norm) "
-                               f"+ {c['Q']} x block accumulation (r{c['R']}, key_norm, the last completing "
+        "config": {"workload": f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q']} x phase2 "
+                               + (f"(LR key r{c['R']}, key_norm, lerp, output norm) " if c.get("lr")
+                                  else "(base, key_norm) ")
+                               + f"+ {c['Q']} x block accumulation (r{c['R']}, key_norm, the last completing "
                                f"the block) B{c['B']} T{c['T']} d{c['D']}", "tokens": wl.n_tok,
                    "phase_ms": round(sum(kern[k]["ms"] for k in parts if k.startswith("phase")), 5)},
         "kernels": kern}))

@@ -1036,13 +1036,15 @@ bool phase2_wave_plan(const attnres_phase2_desc* d, const PhasePlan& pl, P2Wave*
   return true;
 }
 
-// Base-key phase 2 with the addcmul merge on 16-bit rows one wave covers
-// exactly (D = 256, 512, 768, 1024), without the output norm: the
-// packed-arithmetic kernels of attnres_phase2_fast.hip.
+// The packed-arithmetic kernels of attnres_phase2_fast.hip, on 16-bit rows one
+// wave covers exactly (D = 256, 512, 768, 1024): base keys with the addcmul
+// merge and no output norm, or LR keys (r <= 256) with either merge and the
+// optional output norm.
 bool phase2_fast(const attnres_phase2_desc* d, const P2Wave& w) {
-  if (elem_size(d->dtype) != 2 || d->rank != 0 || d->logit_given || d->normalize_output) return false;
-  if (d->merge != ATTNRES_MERGE_ADDCMUL) return false;
-  return d->dim == kWaveSize * (w.vb / 2) * w.cb;
+  if (elem_size(d->dtype) != 2 || d->logit_given) return false;
+  if (d->dim != kWaveSize * (w.vb / 2) * w.cb) return false;
+  if (d->rank > 0) return d->rank <= 4 * kWaveSize;
+  return !d->normalize_output && d->merge == ATTNRES_MERGE_ADDCMUL;
 }
 
 // Phase 1 with one wave per token and packed arithmetic
@@ -1189,10 +1191,15 @@ extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, v
     L.teams = kPhase2Teams;
     L.vb = wv.vb;
     L.wpt = wv.cb;
+    // one resident round of the fast kernels' waves (8 per SIMD), each walking
+    // tokens with that stride: the per-wave setup (query, scale, bias) is paid
+    // once per few tokens (measured at p5lr: 16.4 -> 15.3 us per LR merge,
+    // 17.1 us with four tokens per wave)
     const int64_t wgs = (d->n_tok + kPhase2Teams - 1) / kPhase2Teams;
-    L.grid = (int)(wgs < kMaxFwdGroups ? wgs : kMaxFwdGroups);
+    const int64_t cap = phase2_fast(d, wv) ? 2 * base_fast_streams() / kPhase2Teams : kMaxFwdGroups;
+    L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = 0;
-    L.feat = d->key_norm ? 1 : 0;
+    L.feat = (d->key_norm ? 1 : 0) | (d->merge == ATTNRES_MERGE_LERP ? 2 : 0);
   } else {
     L.wpt = phase2_waves(d, pl);
     L.grid = (int)(d->n_tok < kMaxFwdGroups ? d->n_tok : kMaxFwdGroups);
@@ -1266,7 +1273,7 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     if (cap > base_fast_streams() / kPhase2Teams) cap = base_fast_streams() / kPhase2Teams;
     L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
-    L.feat = d->key_norm ? 1 : 0;
+    L.feat = (d->key_norm ? 1 : 0) | (d->merge == ATTNRES_MERGE_LERP ? 2 : 0);
   } else {
     L.wpt = phase2_waves(d, pl);
     L.grid = (int)(groups < kFullBwdGroups ? groups : kFullBwdGroups);
