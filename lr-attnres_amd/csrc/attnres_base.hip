@@ -329,35 +329,45 @@ __global__ void __launch_bounds__(1024) avg_bwd_kernel(const ReadBwdParams bp) {
 }
 
 // ============================================================== partial-sum reduction
-// A workgroup of 1024 threads owns SPB consecutive slots; thread (rl, sl) sums
-// rows rl, rl + RL, ... of slot sl (RL = 1024 / SPB row lanes, reading SPB-wide
-// coalesced row segments), and the RL row sums of each slot are added by a
-// fixed tree.  The order is fixed, so the result is bit-reproducible run to
-// run.  Few slots (the LR static query: R floats) use narrow, deep workgroups
-// so that enough of them share the rows.
+// A workgroup of 1024 threads (16 waves) owns SPB consecutive slots; thread
+// (rl, sl) sums rows rl, rl + RL, ... of slot sl (RL = 1024 / SPB row lanes,
+// reading SPB-wide coalesced row segments; the loads are issued ahead of the
+// adds).  The row sums of a slot are then added inside each wave (lane
+// shuffles across the wave's row lanes) and the 16 wave sums in wave order by
+// one thread: one workgroup barrier.  The order is fixed, so the result is
+// bit-reproducible run to run.  Few slots (the LR static query: R floats) use
+// narrow, deep workgroups so that enough of them share the rows.
 template <class DT, int SPB>
 __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParams rp) {
+  static_assert(SPB >= 1 && SPB <= kWave && kWave % SPB == 0, "slots per workgroup divide the wave");
   constexpr int RL = 1024 / SPB;
-  const int tid = threadIdx.x;
+  constexpr int kWaves = 1024 / kWave;
+  constexpr int kExtraChunk = 4;
+  __shared__ float sh[kWaves][kWave];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
   const int n_slot_blocks = (rp.n_part + SPB - 1) / SPB;
   if ((int)blockIdx.x < n_slot_blocks) {
-    __shared__ float sh[RL][SPB + 1];
     const int sl = tid % SPB, rl = tid / SPB;
     const int slot = (int)blockIdx.x * SPB + sl;
     const bool regular = slot < rp.n_part && !(slot >= rp.part_extra && slot < rp.part_extra + rp.n_extra);
     float a = 0.f;
     if (regular) {
-#pragma unroll 8
+#pragma unroll 16
       for (int w = rl; w < rp.n_groups; w += RL) a += rp.partials[part_index(rp.layout, w, slot, rp.n_groups, rp.n_part)];
     }
-    sh[rl][sl] = a;
-    __syncthreads();
-    for (int o = RL / 2; o > 0; o >>= 1) {
-      if (rl < o) sh[rl][sl] += sh[rl + o][sl];
-      __syncthreads();
+    // the wave's row lanes of slot sl are the lanes congruent to sl mod SPB
+    if constexpr (SPB == 1) {
+      a = wave_sum(a);
+    } else {
+#pragma unroll
+      for (int o = SPB; o < kWave; o <<= 1) a += __shfl_xor(a, o, kWave);
     }
-    if (rl == 0 && regular) {
-      const float t = sh[0][sl];
+    if (lane < SPB) sh[wv][lane] = a;
+    __syncthreads();
+    if (tid < SPB && regular) {
+      float t = 0.f;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) t += sh[v][tid];
       if (slot >= rp.part_q && slot < rp.part_q + rp.n_q) {
         if (rp.dquery) DT::store1((typename DT::S*)rp.dquery + (slot - rp.part_q), t);
       } else if (slot >= rp.part_gate && slot < rp.part_gate + rp.n_gate) {
@@ -371,21 +381,32 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
   // the last workgroup: extra slots are the summands of one gradient, each
   // summed over the rows and rounded to the dtype on its own (separate autograd
   // edges reduced in the dtype), then accumulated in slot order with a rounding
-  // after each add (autograd's accumulation of gradients in the dtype)
-  __shared__ float tree[1024];
+  // after each add (autograd's accumulation of gradients in the dtype); up to
+  // four slots are read in one pass over the rows
   float tot = 0.f;
-  for (int k = 0; k < rp.n_extra; ++k) {
-    float b = 0.f;
+  for (int k0 = 0; k0 < rp.n_extra; k0 += kExtraChunk) {
+    float b[kExtraChunk];
+#pragma unroll
+    for (int k = 0; k < kExtraChunk; ++k) b[k] = 0.f;
     for (int w = tid; w < rp.n_groups; w += 1024) {
-      b += rp.partials[part_index(rp.layout, w, rp.part_extra + k, rp.n_groups, rp.n_part)];
+#pragma unroll
+      for (int k = 0; k < kExtraChunk; ++k)
+        if (k0 + k < rp.n_extra) b[k] += rp.partials[part_index(rp.layout, w, rp.part_extra + k0 + k, rp.n_groups, rp.n_part)];
     }
-    tree[tid] = b;
+#pragma unroll
+    for (int k = 0; k < kExtraChunk; ++k) {
+      b[k] = wave_sum(b[k]);
+      if (lane == 0) sh[wv][k] = b[k];
+    }
     __syncthreads();
-    for (int o = 512; o > 0; o >>= 1) {
-      if (tid < o) tree[tid] += tree[tid + o];
-      __syncthreads();
+    if (tid == 0) {
+      for (int k = 0; k < kExtraChunk && k0 + k < rp.n_extra; ++k) {
+        float t = 0.f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) t += sh[v][k];
+        tot = DT::rnd(tot + DT::rnd(t));
+      }
     }
-    tot = DT::rnd(tot + DT::rnd(tree[0]));
     __syncthreads();
   }
   if (tid == 0 && rp.dextra) rp.dextra[0] = tot;

@@ -277,7 +277,25 @@ def test_phase2_one_wave_rows(dtype, D, key_norm, bias_tensor):
     _check_phase2(out, grads, ref_out, ref_grads, dtype)
 
 
-@pytest.mark.parametrize("R", [16, 64, 128, 1024])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,R,variant,key_norm,norm", [
+    (256, 64, "lrid", True, True), (256, 32, "lrid_addcmul", False, False),
+    (512, 128, "lrid", True, False), (512, 100, "lrid_addcmul", True, True),
+    (768, 64, "lrid", True, True), (768, 256, "lrid_addcmul", True, False),
+    (1024, 64, "lrid", False, True), (1024, 200, "lrid", True, True)])
+def test_lrid_phase2_one_wave_rows(dtype, D, R, variant, key_norm, norm):
+    """LR keys on 16-bit rows one wave covers exactly: the packed-arithmetic
+    phase-2 kernels (every column layout, 1, 2 and 4 key elements per lane,
+    both merges, with and without key norm and the fused output norm); 111
+    tokens leave part of the last workgroup idle."""
+    t = _phase2_case(6000 + D + R, dtype, 3, 37, D, variant, R=R)
+    m = dict(variant=variant, key_norm=key_norm, bias=0.3, bias_tensor=True, normalize_output=norm, scale=0.25)
+    out, grads = _phase2_hip(t, m)
+    ref_out, ref_grads = _phase2_oracle(t, m)
+    _check_phase2(out, grads, ref_out, ref_grads, dtype)
+
+
+@pytest.mark.parametrize("R", [16, 64, 128, 200, 256, 1024])
 def test_lrid_phase2_key_widths(R):
     t = _phase2_case(40 + R, torch.bfloat16, 1, 6, 512, "lrid", R=R)
     m = dict(variant="lrid", key_norm=True, bias=0.3, bias_tensor=False, normalize_output=False, scale=0.25)
