@@ -12,7 +12,9 @@ MLP 4d, vocab 100277, block LR-AttnRes with rank 64 over 6 blocks (7 sources
 at the last read), B=16, T=1024, bf16 weights and activations (the model is
 cast with ``.to(bf16)``, as ``bench_attnres.py:180-181`` does), SDPA token
 attention, LM cross-entropy loss and an SGD update, random init and uniform
-random token ids.  Eager mode: no ``torch.compile``.
+random token ids.  Eager by default (no ``torch.compile``); ``--graph true``
+replays everything after the embedding lookup from HIP graphs, the
+counterpart of the reference's CUDA-graph runs (``FUSED_ATTNRES.md:317-345``).
 
     python lr-attnres_amd/bench_attnres.py [--batch_sizes 16] [--phase train] [--loss lm] ...
 
@@ -82,6 +84,9 @@ def parse_args(argv=None):
     p.add_argument("--nonzero_attnres_queries", type=_bool, default=True)
     p.add_argument("--profile_iters", type=int, default=2,
                    help="extra steps under torch.profiler for the kernel share (0 = skip)")
+    p.add_argument("--graph", type=_bool, default=False,
+                   help="train steps with everything after the embedding lookup replayed from HIP graphs "
+                        "(torch.cuda.make_graphed_callables); the lookup, its backward and the update stay eager")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args(argv)
 
@@ -121,6 +126,71 @@ def train_step(args, model, idx, targets):
                 if p.grad is not None:
                     p.add_(p.grad, alpha=-args.lr)
     return loss
+
+
+class _Body(torch.nn.Module):
+    """The decoder between its embedding lookup and its head: ``x -> hidden``.
+
+    The lookup's backward (a scatter whose sort / unique step has data-dependent
+    sizes) cannot be replayed from a graph captured at other token ids, so a
+    graphed step keeps the lookup eager; the head and the loss stay eager too
+    (a few launches), which keeps large single-tensor reductions -- whose
+    multi-workgroup form clears its counters with a memset node -- out of the
+    graph."""
+
+    def __init__(self, model):
+        super().__init__()
+        self.model = model
+
+    def forward(self, x):
+        m = self.model
+        return m._forward_block_lrid(x) if m.config.use_attnres else m._forward_baseline(x)
+
+
+def _loss_from_hidden(args, model, h, targets):
+    if args.loss == "hidden_mse":
+        return h.float().square().mean()
+    logits = F.linear(h, model.transformer.wte.weight, None) if model.config.weight_tying else model.lm_head(h)
+    return F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.view(-1))
+
+
+def graphed_train_step(args, model, idx, targets):
+    """A train step whose decoder body (everything between the embedding
+    lookup and the head, forward and backward) replays HIP graphs; returns
+    (step, check) where check(n) runs n graphed and n eager steps from the same
+    weights and returns the largest relative difference of their losses (graph
+    replays must match eager execution before their timing means anything)."""
+    x0 = model.transformer.wte(idx).detach().requires_grad_(True)
+    graphed = torch.cuda.make_graphed_callables(_Body(model), (x0,), allow_unused_input=True)
+    params = [p for p in model.parameters()]
+
+    def step():
+        for p in params:
+            p.grad = None
+        h = graphed(model.transformer.wte(idx))
+        loss = _loss_from_hidden(args, model, h, targets)
+        loss.backward()
+        if args.optimizer_step:
+            with torch.no_grad():
+                live = [p for p in params if p.grad is not None]
+                torch._foreach_add_(live, [p.grad for p in live], alpha=-args.lr)
+        return loss
+
+    def check(n):
+        start = [p.detach().clone() for p in params]
+        losses = []
+        for fn in (step, lambda: train_step(args, model, idx, targets)):
+            with torch.no_grad():
+                for p, s0 in zip(params, start):
+                    p.copy_(s0)
+            torch.cuda.synchronize()
+            losses.append([float(fn().detach()) for _ in range(n)])
+        with torch.no_grad():
+            for p, s0 in zip(params, start):
+                p.copy_(s0)
+        return max(abs(a - b) / max(abs(b), 1e-6) for a, b in zip(*losses)), losses
+
+    return step, check
 
 
 def _device_time_us(event):
@@ -166,10 +236,17 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
     idx = torch.randint(0, args.vocab_size, (batch, args.block_size), device=device, generator=gen)
     targets = torch.randint(0, args.vocab_size, (batch, args.block_size), device=device, generator=gen)
 
+    graph_check = None
     if args.phase == "forward":
         def step():
             with torch.inference_mode():
                 model(idx, return_hidden=True)
+    elif args.graph:
+        step, check = graphed_train_step(args, model, idx, targets)
+        rel, losses = check(6)
+        graph_check = {"max_rel_loss_diff": rel, "graph_losses": losses[0], "eager_losses": losses[1]}
+        if rel > 1e-2:
+            raise RuntimeError(f"graph replays do not match eager steps: {graph_check}")
     else:
         def step():
             train_step(args, model, idx, targets)
@@ -203,6 +280,8 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
         "attnres_kernel_ms": None if attn_us is None else attn_us / 1000.0,
         "device_kernel_ms": None if total_us is None else total_us / 1000.0,
         "params": n_params,
+        "graph": bool(args.graph and args.phase == "train"),
+        "graph_check": graph_check,
     }
 
 
@@ -226,6 +305,7 @@ def main(argv=None):
     print(f"dtype={args.dtype} phase={args.phase} loss={args.loss} optimizer_step={args.optimizer_step} "
           f"n_layer={args.n_layer} n_embd={args.n_embd} n_head={args.n_head} vocab={args.vocab_size} "
           f"T={args.block_size} blocks={args.attnres_num_blocks} fold_block_summary={args.fold_block_summary} "
+          f"graph={args.graph} "
           f"torch={torch.__version__} device={torch.cuda.get_device_name(0)}", flush=True)
     print("case,batch,rank,latency_ms,overhead_vs_baseline_pct,tokens_per_s,attnres_kernel_ms,"
           "attnres_kernel_share_pct", flush=True)
@@ -254,6 +334,7 @@ def main(argv=None):
         "workload": "c5" if (args.n_layer, args.n_embd, args.n_head, args.vocab_size, args.block_size,
                              args.attnres_num_blocks) == (12, 768, 12, 100277, 1024, 6) else "custom",
         "phase": args.phase, "loss": args.loss, "optimizer_step": args.optimizer_step, "dtype": args.dtype,
+        "graph": bool(args.graph and args.phase == "train"),
         "data": "synthetic (uniform random token ids, random init)",
         "cases": summary,
     }), flush=True)

@@ -247,9 +247,10 @@ void fill_params(const attnres_read_desc* d, const Plan& pl, ReadParams* p) {
 
 // The static keys' gradient: per-source token sums of dkeys, partial sums
 // per token chunk in the workspace after the cross-token partial rows.
-// LDS bytes of the static keys in the fast LR kernels ([n_src, rank] in the dtype)
+// LDS bytes of the static keys in the fast LR kernels ([n_src, rank] in the
+// dtype, rows one 16-byte chunk apart more than rank)
 size_t static_keys_lds(const attnres_read_desc* d) {
-  return d->static_keys ? (size_t)d->n_src * d->rank * elem_size(d->dtype) : 0;
+  return d->static_keys ? (size_t)d->n_src * ((size_t)d->rank * elem_size(d->dtype) + 16) : 0;
 }
 
 int colsum_chunks(int64_t n_tok) {

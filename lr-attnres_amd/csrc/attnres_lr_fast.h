@@ -66,13 +66,24 @@ struct KeySlice {
 // per workgroup (16-byte chunks; the host checks R * elem is a multiple of 16),
 // and every token's key slice gets its source's slice added from there,
 // rounded to the dtype as the eager `key + static` is -- token-invariant data
-// kept out of the loop-carried registers.
+// kept out of the loop-carried registers.  Rows sit one 16-byte chunk more
+// than R apart: the pair lanes of one head read the same offset in every
+// source's row, which with a row stride of a multiple of 256 bytes would all
+// fall in the same LDS banks.
+template <class DT>
+__device__ __forceinline__ int static_key_row(int R) {
+  return R + 16 / (int)sizeof(typename DT::S);  // elements
+}
 template <class DT>
 __device__ __forceinline__ void static_keys_to_lds(const ReadParams& p, typename DT::S* dst) {
   using S = typename DT::S;
-  const int n16 = p.n_src * p.R * (int)sizeof(S) / 16;
+  const int row16 = p.R * (int)sizeof(S) / 16;  // chunks per row
+  const int n16 = p.n_src * row16;
   const u32x4* src = (const u32x4*)p.skey;
-  for (int i = threadIdx.x; i < n16; i += blockDim.x) ((u32x4*)dst)[i] = src[i];
+  for (int i = threadIdx.x; i < n16; i += blockDim.x) {
+    const int s = i / row16;
+    ((u32x4*)dst)[i + s] = src[i];  // row s starts s chunks further on
+  }
 }
 
 template <class DT, int RHC>
@@ -325,7 +336,7 @@ __global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1)
     // ---- logits of this wave's (head, source) pairs
     float logit = -INFINITY;
     if (has_pair) {
-      if (skey) add_static_key<DT, RHC>(s_sk + ps * R + ph * rh, kch, kr);
+      if (skey) add_static_key<DT, RHC>(s_sk + ps * static_key_row<DT>(R) + ph * rh, kch, kr);
       const float gf = (dyn && p.gate) ? gate_value(DT::load1(&graw), p.gate_act) : 1.f;
       const float inv = p.key_norm ? key_inv_rms<DT, RHC>(kr, kch, rh, p.eps) : 1.f;
       QSlice<DT, RHC> q;
@@ -661,7 +672,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
       const float dl = pr * (dwr - pdot);
       s_dl[lane] = dl;
       ge = DT::rnd(DT::rnd(dl) * p.scale);
-      if (skey) add_static_key<DT, RHC>(s_sk + ps * R + ph * rh, kch, kr);  // the scored key; dk is its gradient
+      if (skey) add_static_key<DT, RHC>(s_sk + ps * static_key_row<DT>(R) + ph * rh, kch, kr);  // the scored key; dk is its gradient
       if (p.key_norm) kinv = key_inv_rms<DT, RHC>(kr, kch, rh, p.eps);
       float m = 0.f;
 #pragma unroll
