@@ -95,9 +95,16 @@ typedef struct attnres_read_desc {
                                       and average reads ignore it. */
   const void* static_keys;         /* LR: [n_src, rank] dense in key_dtype, or NULL.  Row s is added to
                                       every key of source s before it is scored, rounded to the key
-                                      dtype -- the model's static source key (model.py:2046-2049,
-                                      LRIDStaticKey :275-289; config 4's [N, 128] key), fused here
-                                      instead of materialising key + static per source. */
+                                      dtype, fused here instead of materialising key + static per
+                                      source.  Config 4 defines one [N, 128] key per source.  The
+                                      reference model has ONE shared [rank] parameter
+                                      (LRIDStaticKey, model.py:275-289, fp32) that
+                                      _add_static_lrid_source_key (:2046-2049) adds to every source
+                                      key except the embedding's (:2062-2063, 2070-2078): express it
+                                      as row 0 = zero and rows 1..n_src-1 = the parameter cast to
+                                      key_dtype.  dstatic_keys then holds one gradient per row; the
+                                      parameter's gradient is the fp32 sum of rows 1..n_src-1, as
+                                      the model's autograd adds one cast per source. */
 } attnres_read_desc;
 
 /* Gradient buffers for attnres_read_backward. */
@@ -114,7 +121,7 @@ typedef struct attnres_read_grads {
   float* dbias;              /* [n_src] fp32 or NULL */
   void* workspace;           /* device scratch for deterministic cross-token reductions */
   size_t workspace_bytes;
-  void* dstatic_keys;        /* LR with static_keys: [n_src, rank] key_dtype, the token sums of dkeys
+  void* dstatic_keys;        /* LR with static_keys: [n_src, rank] key_dtype, per row (see static_keys), the token sums of dkeys
                                 (each rounded to the key dtype once, as the reference's expand
                                 backward sums them), or NULL; needs dkeys */
 } attnres_read_grads;

@@ -503,7 +503,11 @@ def lrid_attention_residual_read(values, keys, query: Tensor, num_heads: int, lo
     op): ``static_keys`` [N, R] (or N tensors [R]) adds source s's static key to
     every key of source s inside the kernel, as the model adds it eagerly
     before the read (model.py:2046-2049); its gradient is the token sum of the
-    key gradient.
+    key gradient.  The model's one shared ``[R]`` parameter (LRIDStaticKey,
+    model.py:275-289), which it adds to every source but the embedding
+    (model.py:2062-2063, 2070-2078), is the table with a zero row 0 and the
+    parameter cast to the key dtype in every other row; autograd then sums the
+    rows' gradients back into the parameter.
     """
     vs, ks, H, D, R, k0_dtype = _lr_common(values, keys, num_heads, "lrid_attention_residual_read")
     query = query.to(k0_dtype)

@@ -636,6 +636,15 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
                   g->workspace ? g->workspace_bytes : (size_t)0);
     bp.partials = (float*)g->workspace;
   }
+  // the static keys' column sums follow the partial rows in the workspace:
+  // checked here, before anything is launched, so a too-small workspace leaves
+  // every output untouched
+  if (lr && g->dstatic_keys) {
+    const size_t need = partial_rows_bytes(d) + colsum_bytes(d);
+    if (!g->workspace || g->workspace_bytes < need)
+      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
+                  g->workspace ? g->workspace_bytes : (size_t)0);
+  }
   bp.n_part = PL.n_part;
   bp.part_q = PL.part_q;
   bp.part_gate = PL.part_gate;
@@ -759,11 +768,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     err = launch_reduce_partials(logit_dtype(d), rp, st);  // the query gradient is in the logit dtype
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
   }
-  if (lr && g->dstatic_keys) {
-    const size_t need = partial_rows_bytes(d) + colsum_bytes(d);
-    if (!g->workspace || g->workspace_bytes < need)
-      return fail(ATTNRES_EWORKSPACE, "workspace of %zu bytes needed, got %zu", need,
-                  g->workspace ? g->workspace_bytes : (size_t)0);
+  if (lr && g->dstatic_keys) {  // (workspace size checked above)
     ColsumParams cp;
     memset(&cp, 0, sizeof(cp));
     for (int s = 0; s < d->n_src; ++s) cp.dk[s] = g->dkeys[s];

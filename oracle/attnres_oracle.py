@@ -40,11 +40,17 @@ gated_query_ref                           closed form (zero gate -> static)
 block_* helpers                           the reference tests' known answers
 lrid_fused_projection_split_ref           the reference model itself: whole-model
                                           golden vectors (tests/golden/model_*)
-lrid_value_key_projection_ref             the model's norm + Linear (two library ops);
-                                          norm pinned with the read's rms-norm
-static_key_add_ref                        the model's broadcast add itself (one line);
-                                          the static-key reads are checked against
-                                          the pinned LR read of the summed keys
+lrid_value_key_projection_ref             golden vectors written by the reference's
+                                          LRIDSourceKeyProjection (lrid_key_from_value,
+                                          value norm on and off; fp32 and bf16; keys,
+                                          value and weight gradients), bit for bit
+                                          (tests/test_oracle_producers.py)
+static_key_add_ref,                       golden vectors written by the reference's
+shared_static_key_table_ref               LRIDStaticKey + OBPM._add_static_lrid_source_key
+                                          followed by its eager LR read (keys with the
+                                          static key, output, value / key / query
+                                          gradients and the fp32 parameter's gradient)
+                                          (tests/test_oracle_producers.py)
 lrid_block_accumulate_ref                 composition of the pinned split and
                                           block_* helpers; the decoder built on
                                           it reproduces the reference-model
@@ -441,6 +447,19 @@ def static_key_add_ref(keys, static_keys):
     return [k + static_keys[i].to(k.dtype) for i, k in enumerate(keys)]
 
 
+def shared_static_key_table_ref(static_key: Tensor, n_src: int, dtype) -> Tensor:
+    """The reference model's static source key as a per-source ``[n_src, R]``
+    table: one shared ``[R]`` parameter (``LRIDStaticKey``, model.py:275-289)
+    added to every source key except the embedding's (``_lrid_source`` with
+    ``add_static_key=True``, model.py:2062-2063; the embedding source, :2070-2078,
+    does not add it).  Row 0 is zero and every other row is the parameter cast
+    to the key dtype, one cast per source as the model casts it once per call
+    (:286-288), so autograd sums the per-source gradients into the parameter in
+    its own dtype as the model's graph does."""
+    zero = torch.zeros_like(static_key, dtype=dtype)
+    return torch.stack([zero] + [static_key.to(dtype) for _ in range(n_src - 1)])
+
+
 def lrid_block_accumulate_ref(projected: Tensor, partial_value, partial_key, output_dim: int, rank: int,
                               num_heads: int = 1, key_norm: bool = True, complete: bool = False,
                               partial_scale=1.0, value_norm: bool = False, scale_key: bool = False):
@@ -510,6 +529,7 @@ __all__ = [
     "phase1_from_logits_ref",
     "lrid_block_accumulate_ref",
     "static_key_add_ref",
+    "shared_static_key_table_ref",
     "lrid_value_key_projection_ref",
     "attention_residual_phase1_ref",
     "attention_residual_phase2_ref",

@@ -183,6 +183,25 @@ def test_static_key_gradient_needs_static_keys():
     assert b"dstatic_keys without static_keys" in lib.attnres_last_error()
 
 
+@needs_lib
+def test_static_key_workspace_is_checked_before_any_launch():
+    """A workspace sized without the static keys' column sums is refused on the
+    host, before the backward launches anything (every output untouched)."""
+    lib = H.load()
+    d = _desc(n_src=13, n_tok=16384, dim=1024, rank=64, heads=4, static_keys=0x7000)
+    need = lib.attnres_read_backward_workspace_size(ctypes.byref(d))
+    rows = 4096 * 64 * 4
+    assert need > rows
+    g = H.ReadGrads()
+    dv = (ctypes.c_void_p * 13)(*([0x8000] * 13))
+    g.grad_out, g.weights, g.dvalues, g.dkeys = 0x9000, ctypes.cast(ctypes.c_void_p(0xa000), ctypes.POINTER(ctypes.c_float)), dv, dv
+    g.dquery = 0xc000
+    g.dstatic_keys = 0xb000
+    g.workspace, g.workspace_bytes = 0xd000, rows  # the partial rows only
+    assert lib.attnres_read_backward(ctypes.byref(d), ctypes.byref(g), None) == -4
+    assert f"workspace of {need} bytes needed, got {rows}".encode() in lib.attnres_last_error()
+
+
 def test_static_keys_shape_is_checked_on_the_host():
     vs = [torch.randn(1, 2, 8) for _ in range(3)]
     ks = [torch.randn(1, 2, 4) for _ in range(3)]
