@@ -544,7 +544,8 @@ extern "C" int attnres_read_forward(const attnres_read_desc* d, void* out, void*
       L.teams = f.rhc;
       L.feat = lr_fast_features(d);
       L.grid = (int)((f.n_items * (int64_t)p.streams + 3) / 4);
-      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float) + static_keys_lds(d);
+      L.lds = lr_fast_table_bytes() + ((size_t)d->rank + 4 * 64) * sizeof(float) + static_keys_lds(d) +
+              4 * (size_t)lr_fast_staged_rows(f.cb, f.rhc, f.nb, elem_size(d->dtype), lr_fast_features(d)) * 1024;
       if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR forward needs %zu bytes of LDS", L.lds);
       err = launch_lr_fast_forward(d->dtype, p, L, st);
     } else {
@@ -704,7 +705,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
               ((size_t)d->rank + 4 * (192 + (size_t)f.np * f.nh * (d->rank / d->heads + 1)) +
                (4 * (size_t)PL.n_part + 3) / 4 * 4) *
                   sizeof(float) +
-              static_keys_lds(d);
+              static_keys_lds(d) + 4 * (size_t)lr_fast_staged_rows(f.cb, f.rhc, f.nb, elem_size(d->dtype), lr_fast_features(d)) * 1024;
       if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "LR backward needs %zu bytes of LDS", L.lds);
       // slot-major partials (R + few slots: one reduction workgroup per slot
       // beats 16-slot tiles here, measured at C3 and C4)

@@ -406,6 +406,18 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Staged rows: one 16-byte lane vector loaded straight into LDS
+// (global_load_lds_dwordx4; lane i's 16 bytes land at lds_row + 16 i, checked
+// on the box), no VGPR held while the load is in flight.  `lds_row` must be
+// wave-uniform.  The compiler does not order LDS reads after these loads:
+// read the row back only after wait_staged() (vmcnt(0): every vector-memory
+// operation of the wave has completed, these loads included).
+__device__ __forceinline__ void stage16(const void* src, void* lds_row) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_row, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_staged() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // a wave-uniform 64-bit value, moved to scalar registers
 __device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);

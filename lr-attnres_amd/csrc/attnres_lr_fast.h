@@ -16,6 +16,13 @@
 // cannot be waited on without draining that store -- keeping stores at the end
 // removes those round trips from the token's critical path.
 //
+// Staged rows: with one 16-bit column per wave, the first SL value rows of a
+// token (lr_fast_staged_rows) go straight into a per-wave LDS area
+// (global_load_lds_dwordx4), issued after the register rows; the mix (and the
+// backward's dW) takes the register rows first, then waits for everything and
+// reads the staged rows back.  They hold no VGPRs in flight (85 / 95 instead
+// of 109 / 111 at C3) and stream faster than register loads.
+//
 // Addressing: the per-source pointer / stride tables are copied to LDS once
 // and read back as wave-uniform scalars inside the token loop, so row
 // addresses are scalar (SGPR base + one VGPR lane offset) and the tables do
@@ -109,6 +116,21 @@ __device__ __forceinline__ void add_static_key(const typename DT::S* sk, int kch
         }
       }
     }
+  }
+}
+
+// the staged rows of this lane back from LDS into the register rows' array
+// (after every load of the token has completed)
+template <int SL, class DT, int E, int NB, int CB>
+__device__ __forceinline__ void read_staged_rows(const char* stage, int lane, Raw<DT, E> (&vr)[NB][CB]) {
+  wait_staged();
+#pragma unroll
+  for (int r = 0; r < SL; ++r) {
+    const u32x4 w = *(const u32x4*)(stage + r * 1024 + lane * 16);
+    vr[r][0].w[0] = w.x;
+    vr[r][0].w[1] = w.y;
+    vr[r][0].w[2] = w.z;
+    vr[r][0].w[3] = w.w;
   }
 }
 
@@ -239,15 +261,18 @@ __global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1)
   constexpr int E = VB / (int)sizeof(S);        // value elements per lane vector
   constexpr int KV = 16 / (int)sizeof(S);       // key elements per 16-byte chunk
   constexpr int colw = kWave * E;
-  extern __shared__ float smem[];
+  extern __shared__ float lds_base[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wslot = uniform_i32(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
   __builtin_assume(N >= lr_fast_slot_floor(CB, RHC, NB));
-  // LDS: source tables | static query [R] | per wave: the softmax weights, 64
-  // words (16-bit types: the rounded weights of lanes 2i and 2i + 1 packed in
-  // word i; fp32: one word per lane)
+  constexpr int SL = lr_fast_staged_rows(CB, RHC, NB, (int)sizeof(S), FEAT);
+  // LDS: per wave SL staged rows of 1 KB | source tables | static query [R] |
+  // per wave: the softmax weights, 64 words (16-bit types: the rounded
+  // weights of lanes 2i and 2i + 1 packed in word i; fp32: one word per lane)
+  char* stage = (char*)lds_base + wslot * SL * 1024;
+  float* smem = lds_base + nwaves * SL * 256;
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
   uint32_t* s_w = (uint32_t*)(s_q + R) + wslot * 64;
@@ -324,11 +349,14 @@ __global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1)
 #pragma unroll
     for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, t);
 #pragma unroll
-    for (int s = 0; s < NB; ++s) {
+    for (int s = SL; s < NB; ++s) {
       const S* vp = global_ptr<const S>(base[s]);
 #pragma unroll
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + eoff[c], vr[s][c]);
     }
+    // the first SL rows straight into LDS, issued last (CB == 1 here)
+#pragma unroll
+    for (int s = 0; s < SL; ++s) stage16(global_ptr<const S>(base[s]) + eoff[0], stage + s * 1024);
   };
 
   for (int64_t tok = t0; tok < p.n_tok; tok += p.streams) {
@@ -367,8 +395,11 @@ __global__ void __launch_bounds__(256, (FEAT & kFeatStatic) && NB >= 20 ? 3 : 1)
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[c][e] = 0.f;
     if constexpr (sizeof(S) == 2) {
+      // register rows first (as they arrive), then the staged rows
 #pragma unroll
-      for (int s = 0; s < NB; s += 2) {
+      for (int s0 = SL; s0 < NB + SL; s0 += 2) {
+        const int s = s0 < NB ? s0 : s0 - NB;
+        if (s0 == NB) read_staged_rows<SL>(stage, lane, vr);
         if (s < N) {
 #pragma unroll
           for (int c = 0; c < CB; ++c) {
@@ -436,14 +467,18 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
   constexpr int KV = 16 / (int)sizeof(S);
   constexpr int colw = kWave * E;
   const ReadParams& p = bp.f;
-  extern __shared__ float smem[];
+  extern __shared__ float lds_base[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wslot = uniform_i32(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
   const int N = p.n_src, H = p.H, rh = p.rh, dh = p.dh, D = p.D, R = p.R;
   __builtin_assume(N >= lr_fast_slot_floor(CB, RHC, NB));
-  // LDS: source tables | static query [R] | per wave: p [64], dW [64], dl [64],
-  // contributions [nh*np][rh] | fold [nwaves][n_part]
+  constexpr int SL = lr_fast_staged_rows(CB, RHC, NB, (int)sizeof(S), FEAT);
+  // LDS: per wave SL staged rows of 1 KB | source tables | static query [R] |
+  // per wave: p [64], dW [64], dl [64], contributions [nh*np][rh] | fold
+  // [nwaves][n_part]
+  char* stage = (char*)lds_base + wslot * SL * 1024;
+  float* smem = lds_base + nwaves * SL * 256;
   SrcTab* tab = (SrcTab*)smem;
   float* s_q = smem + kSrcTabFloats;
   const int wave_floats = 3 * 64 + p.np * p.nh * (rh + 1);
@@ -551,11 +586,14 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 #pragma unroll
       for (int s = 0; s < NB; ++s) base[s] = row_base(tab, s, tok);
 #pragma unroll
-      for (int s = 0; s < NB; ++s) {
+      for (int s = SL; s < NB; ++s) {
         const S* vp = global_ptr<const S>(base[s]);
 #pragma unroll
         for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + eoff[c], vr[s][c]);
       }
+      // the first SL rows straight into LDS, issued last (CB == 1 here)
+#pragma unroll
+      for (int s = 0; s < SL; ++s) stage16(global_ptr<const S>(base[s]) + eoff[0], stage + s * 1024);
     }
     float g[CB][E];
 #pragma unroll
@@ -623,8 +661,12 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     // 16 r writes (head r / 2, source 2 j + r % 2); otherwise a butterfly per
     // source over the head's lane group.
     const int r16 = lane >> 4;
+    // register rows first (as they arrive), then the staged rows
+    constexpr int NJ = (NB + 1) / 2;
 #pragma unroll
-    for (int j = 0; j < (NB + 1) / 2; ++j) {
+    for (int j0 = SL / 2; j0 < NJ + SL / 2; ++j0) {
+      const int j = j0 < NJ ? j0 : j0 - NJ;
+      if (SL > 0 && j0 == NJ) read_staged_rows<SL>(stage, lane, vr);
       if (2 * j < N) {
         float x[2];
 #pragma unroll

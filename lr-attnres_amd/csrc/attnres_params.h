@@ -33,6 +33,25 @@ __host__ __device__ constexpr int lr_fast_slot_floor(int cb, int rhc, int nb) {
 // query and gate, output norm, per-source static key.
 constexpr int kFeatDyn = 1, kFeatNorm = 2, kFeatStatic = 4, kFeatAll = 7;
 
+// Value rows per token that the one-column 16-bit fast LR kernels load straight
+// into LDS (global_load_lds_dwordx4) instead of VGPRs.  Rows loaded that way
+// hold no registers while in flight and, measured at C3, stream faster than
+// register loads (forward 87.6 -> 74.9 us, backward 183.5 -> 165.8 us with 6
+// rows).  At most the slot floor (so every staged row is a real source), even
+// (the mix and dW loops take source pairs), and 6 at most: each row costs
+// 4 KB of LDS per workgroup, and at 8 the backward drops from 4 to 3
+// workgroups per CU (188 us).  Only the static-query sets (no per-token query,
+// no static keys): while a direct-to-LDS load is pending the compiler turns
+// every wait on the vector-memory counter into a wait for all of them, and the
+// per-token query chain then runs after the whole token has arrived (C4 with
+// staging: forward 226 -> 243 us, backward 468 -> 507 us).
+__host__ __device__ constexpr int lr_fast_staged_rows(int cb, int rhc, int nb, int elem_bytes, int feat) {
+  if (cb != 1 || elem_bytes != 2 || (feat & (kFeatDyn | kFeatStatic)) != 0) return 0;
+  const int f = lr_fast_slot_floor(cb, rhc, nb) & ~1;
+  return f < 6 ? f : 6;
+}
+
+
 struct ReadParams {
   const void* val[kMaxSources];
   const void* key[kMaxSources];
