@@ -64,6 +64,9 @@ def parse_args(argv=None):
     p.add_argument("--attnres_num_blocks", type=int, default=6)
     p.add_argument("--batch_sizes", type=str, default="16")
     p.add_argument("--lrid_ranks", type=str, default="64")
+    p.add_argument("--lrid_projection_rank", type=int, default=None,
+                   help="physical width of the key part of each fused projection (>= rank; the extra columns are "
+                        "padding the read ignores), as the reference's flag (bench_attnres.py:37)")
     p.add_argument("--attnres_block_average", type=_bool, default=True)
     p.add_argument("--attnres_block_average_mode", choices=("count", "sqrt"), default="count")
     p.add_argument("--attnres_block_count_prior", type=_bool, default=True)
@@ -103,7 +106,8 @@ def make_config(args, use_attnres, rank):
         attnres_block_average_mode=args.attnres_block_average_mode,
         attnres_block_count_prior=args.attnres_block_count_prior, attnres_key_norm=args.attnres_key_norm,
         attnres_training_torch_phase2=args.attnres_training_torch_phase2,
-        attnres_fuse_read_norm=args.attnres_fuse_read_norm, lrid_rank=rank or 64, lrid_num_heads=1,
+        attnres_fuse_read_norm=args.attnres_fuse_read_norm, lrid_rank=rank or 64,
+        lrid_projection_rank=args.lrid_projection_rank if use_attnres else None, lrid_num_heads=1,
         lrid_use_logit_scale=True, fold_block_summary=args.fold_block_summary,
         fuse_block_accumulation=args.fuse_block_accumulation)
 
@@ -200,25 +204,56 @@ def _device_time_us(event):
     return 0.0
 
 
+# Device-time categories of the step's kernels (first match wins), so that the
+# AttnRes model's extra device time can be attributed beyond this library's
+# own kernels: the GEMMs of the wider fused projections, the eager glue that
+# builds logits and queries, etc.
+KERNEL_CATEGORIES = (
+    ("attnres", ("attnres::",)),
+    ("gemm", ("cijk_", "gemm", "hipblaslt", "matmul", "wvsplitk", "mfma")),
+    ("attention", ("attn", "fmha", "flash", "sdpa", "aotriton")),
+    ("embedding_index", ("embedding", "index", "gather", "scatter", "partition", "radix", "sort", "unique",
+                         "segment")),
+    ("norm", ("norm",)),
+    ("loss", ("softmax", "nll", "cross_entropy", "log_softmax")),
+    ("reduce", ("reduce",)),
+    ("elementwise", ("elementwise", "vectorized", "copy", "fill", "cat", "where", "pointwise")),
+)
+
+
+def kernel_category(name):
+    n = name.lower()
+    for cat, keys in KERNEL_CATEGORIES:
+        if any(k in n for k in keys):
+            return cat
+    return "other"
+
+
 def kernel_share(step, iters):
-    """(attnres kernel µs per step, all kernels µs per step) from torch.profiler, or (None, None)."""
+    """(attnres kernel µs per step, all kernels µs per step, µs per step by
+    KERNEL_CATEGORIES) from torch.profiler, or (None, None, None)."""
     try:
         from torch.profiler import ProfilerActivity, profile
     except ImportError:
-        return None, None
+        return None, None, None
     with profile(activities=[ProfilerActivity.CUDA]) as prof:
         for _ in range(iters):
             step()
         torch.cuda.synchronize()
     total = attn = 0.0
+    cats = {}
     for ev in prof.key_averages():
         t = _device_time_us(ev)
+        if t == 0.0:
+            continue
         total += t
         if ATTNRES_KERNEL_PREFIX in ev.key:
             attn += t
+        c = kernel_category(ev.key)
+        cats[c] = cats.get(c, 0.0) + t
     if total == 0.0:
-        return None, None
-    return attn / iters, total / iters
+        return None, None, None
+    return attn / iters, total / iters, {k: v / iters for k, v in sorted(cats.items())}
 
 
 def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
@@ -263,9 +298,9 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
         end.record()
         torch.cuda.synchronize()
         latency_ms = start.elapsed_time(end) / args.iters
-        attn_us = total_us = None
+        attn_us = total_us = cats_us = None
         if args.profile_iters > 0:
-            attn_us, total_us = kernel_share(step, args.profile_iters)
+            attn_us, total_us, cats_us = kernel_share(step, args.profile_iters)
         n_params = model.get_num_params()
     finally:
         del model, idx, targets
@@ -275,10 +310,12 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
         "label": label,
         "batch": batch,
         "rank": rank or "",
+        "projection_rank": cfg.lrid_projection_rank if use_attnres else "",
         "latency_ms": latency_ms,
         "tokens_per_s": batch * args.block_size / (latency_ms * 1e-3),
         "attnres_kernel_ms": None if attn_us is None else attn_us / 1000.0,
         "device_kernel_ms": None if total_us is None else total_us / 1000.0,
+        "device_ms_by_category": None if cats_us is None else {k: v / 1000.0 for k, v in cats_us.items()},
         "params": n_params,
         "graph": bool(args.graph and args.phase == "train"),
         "graph_check": graph_check,
@@ -324,6 +361,12 @@ def main(argv=None):
                                                100.0 * (row["latency_ms"] / base["latency_ms"] - 1.0))
             row["attnres_kernel_share_pct"] = (None if row["attnres_kernel_ms"] is None else
                                                100.0 * row["attnres_kernel_ms"] / row["latency_ms"])
+            # where the extra device time goes, by kernel category (ms per step)
+            bc = None if base is None else base.get("device_ms_by_category")
+            rc = row.get("device_ms_by_category")
+            row["device_ms_delta_by_category"] = (None if bc is None or rc is None else
+                                                  {k: rc.get(k, 0.0) - bc.get(k, 0.0)
+                                                   for k in sorted(set(bc) | set(rc))})
             print(f"{row['label']},{row['batch']},{row['rank']},{row['latency_ms']:.3f},"
                   f"{_fmt(row['overhead_vs_baseline_pct'], '.2f')},{row['tokens_per_s']:.0f},"
                   f"{_fmt(row['attnres_kernel_ms'], '.3f')},{_fmt(row['attnres_kernel_share_pct'], '.2f')}",

@@ -418,6 +418,17 @@ __device__ __forceinline__ void stage16(const void* src, void* lds_row) {
 }
 __device__ __forceinline__ void wait_staged() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Workgroups are dispatched round-robin over the GPU's 8 XCDs (workgroup b on
+// XCD b % 8), each XCD with its own L2.  xcd_block gives every XCD a contiguous
+// range of logical workgroup indices, so that the tokens of neighbouring
+// workgroups are handled in one XCD.  A bijection on [0, grid).
+__device__ __forceinline__ int xcd_block(int b, int grid) {
+  constexpr int kXcd = 8;
+  const int per = grid / kXcd, rem = grid - (grid / kXcd) * kXcd;
+  const int x = b - (b / kXcd) * kXcd, i = b / kXcd;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
 // a wave-uniform 64-bit value, moved to scalar registers
 __device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);

@@ -575,21 +575,20 @@ __global__ void __launch_bounds__(256) key_colsum_kernel(const ColsumParams p) {
   }
 }
 
+// Pass 2: one wave per (source, column): lane l adds chunks l and l + 64 (the
+// host keeps chunks <= 128), then a fixed-order wave sum (deterministic), one
+// rounding to the key dtype.  One memory round trip per output instead of a
+// thread walking every chunk.
 __global__ void __launch_bounds__(256) key_colsum_finish_kernel(const ColsumParams p) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)p.n_src * p.R) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t i = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (i >= (int64_t)p.n_src * p.R) return;  // wave-uniform
   const int s = (int)(i / p.R), r = (int)(i - (int64_t)s * p.R);
   const float* row = p.partials + (int64_t)s * p.chunks * p.R + r;
-  // in chunk order; 16 loads in flight per batch
-  float a = 0.f;
-  for (int c0 = 0; c0 < p.chunks; c0 += 16) {
-    float t[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) t[k] = c0 + k < p.chunks ? row[(int64_t)(c0 + k) * p.R] : 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) a += t[k];
-  }
-  store_any(p.out, i, p.kdt, a);
+  float a = lane < p.chunks ? row[(int64_t)lane * p.R] : 0.f;
+  if (lane + kWave < p.chunks) a += row[(int64_t)(lane + kWave) * p.R];
+  a = wave_sum(a);
+  if (lane == 0) store_any(p.out, i, p.kdt, a);
 }
 
 template <class DT>
@@ -615,8 +614,9 @@ hipError_t launch_key_colsum(const ColsumParams& p, hipStream_t st) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t n = (int64_t)p.n_src * p.R;
-  hipLaunchKernelGGL(key_colsum_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
+  const int64_t n = (int64_t)p.n_src * p.R;  // one wave per output, four per workgroup
+  if (p.chunks > 2 * kWaveSize) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(key_colsum_finish_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

@@ -115,7 +115,8 @@ __host__ __device__ inline int part_stride(int n_part) { return (n_part + kPartT
 
 // Token sums of the LR key gradients per source (the static keys' gradient):
 // partial sums per (source, token chunk), then a fixed-order sum over chunks.
-constexpr int kColsumMaxChunks = 128;
+constexpr int kColsumMaxChunks = 128;  // <= 2 x 64: the finish pass gives each lane two chunks
+static_assert(kColsumMaxChunks <= 2 * kWaveSize, "static-key finish pass: two chunks per lane");
 constexpr int kColsumTokens = 128;  // tokens per chunk at least
 struct ColsumParams {
   const void* dk[kMaxSources];  // [n_tok, R] dense, key dtype
