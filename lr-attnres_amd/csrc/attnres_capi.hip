@@ -1068,6 +1068,24 @@ bool phase1_fast(const attnres_phase1_desc* d, const PhasePlan& pl, Launch* L) {
   return true;
 }
 
+// Phase 1 split over D / 256 waves per token (attnres_phase1_fast.hip, column
+// split): 16-bit rows of a multiple of 256 elements up to 2048, no output norm,
+// n_q * np <= 64 -- the reference model's block widths (up to 16 read sites)
+// that the one-wave kernels do not cover.  Sets the lane count np (>= 2) and
+// the launch geometry.
+bool phase1_split(const attnres_phase1_desc* d, const PhasePlan& pl, Phase1Params* p, Launch* L) {
+  if (!pl.vec || elem_size(d->dtype) != 2 || d->normalize_output) return false;
+  if (d->dim % 256 || d->dim / 256 > 8) return false;
+  int np = 2;
+  while (np < d->n_src) np <<= 1;
+  if (np > 16 || d->n_q * np > 64) return false;
+  p->np = np;
+  L->wpt = d->dim / 256;
+  L->nmax = np;
+  L->grid = (int)(d->n_tok < kPhase1SplitGroups ? d->n_tok : kPhase1SplitGroups);
+  return true;
+}
+
 }  // namespace
 
 extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, void* out_prenorm, float* lse,
@@ -1098,6 +1116,11 @@ extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, v
   memset(&L, 0, sizeof(L));
   if (phase1_fast(d, pl, &L)) {
     hipError_t err = launch_phase1_fast_forward(d->dtype, p, L, (hipStream_t)stream);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 forward launch failed: %s", hipGetErrorString(err));
+    return ATTNRES_OK;
+  }
+  if (phase1_split(d, pl, &p, &L)) {
+    hipError_t err = launch_phase1_split_forward(d->dtype, p, L, (hipStream_t)stream);
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 forward launch failed: %s", hipGetErrorString(err));
     return ATTNRES_OK;
   }
@@ -1151,6 +1174,11 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   memset(&L, 0, sizeof(L));
   if (phase1_fast(d, pl, &L)) {
     hipError_t err = launch_phase1_fast_backward(d->dtype, p, L, (hipStream_t)stream);
+    if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 backward launch failed: %s", hipGetErrorString(err));
+    return ATTNRES_OK;
+  }
+  if (phase1_split(d, pl, &p, &L)) {
+    hipError_t err = launch_phase1_split_backward(d->dtype, p, L, (hipStream_t)stream);
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 backward launch failed: %s", hipGetErrorString(err));
     return ATTNRES_OK;
   }

@@ -47,6 +47,10 @@ hipError_t launch_phase1_backward(int dtype, const Phase1Params& p, const Launch
 // L.nmax = source slots (4/8); four token streams per workgroup
 hipError_t launch_phase1_fast_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase1_fast_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
+// phase 1 split over L.wpt = D / 256 waves per token (one workgroup per token),
+// 16-bit rows, no output norm, n_q * np <= 64: L.nmax = np (2/4/8/16)
+hipError_t launch_phase1_split_forward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
+hipError_t launch_phase1_split_backward(int dtype, const Phase1Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_forward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 hipError_t launch_phase2_backward(int dtype, const Phase2Params& p, const Launch& L, hipStream_t st);
 // phase 2 with base keys, 16-bit rows of 256 / 512 / 768 / 1024, no output norm:

@@ -18,6 +18,7 @@ constexpr int kWaveSize = 64;  // CDNA wavefront
 constexpr int kMaxBwdGroups = 4096;
 constexpr int kFullBwdGroups = 2048;
 constexpr int kMaxFwdGroups = 65536;
+constexpr int kPhase1SplitGroups = 65536;  // phase-1 split kernels: at most this many workgroups (one token each per step; one token per workgroup measured best)
 
 // Smallest source count for which the host launches a fast LR kernel with nb
 // value slots (it picks the smallest instantiated slot count that holds N:

@@ -119,6 +119,37 @@ def test_phase1_one_wave_rows_backward(dtype, S, Q, D, ldt, T):
     assert_close(dl, e_dl, dtype, "dlogits", reduced=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,Q,D,ldt,T", [
+    (4, 12, 1024, torch.float32, 9),     # the reference's published block (24 layers, 4 blocks)
+    (8, 6, 1024, torch.bfloat16, 9),     # 24 layers, 8 blocks
+    (16, 4, 768, torch.float32, 9),      # 16 sources
+    (2, 16, 512, torch.float16, 9),      # 16 sites, two lanes per softmax row
+    (5, 8, 256, torch.float32, 9),       # one wave per token
+    (3, 16, 1536, torch.float32, 9),     # six waves per token
+    (1, 9, 2048, torch.float32, 9),      # eight waves per token, one source
+    (12, 4, 768, torch.float32, 4200),   # more tokens than workgroups
+])
+def test_phase1_split_rows(dtype, S, Q, D, ldt, T):
+    """16-bit rows of a multiple of 256 elements, up to 16 sites: the column-
+    split phase-1 kernels (D / 256 waves per token), forward and backward,
+    every lane-layout width (np = 2 / 4 / 8 / 16) and fp32 / 16-bit logits."""
+    g = gen(5000 + S * 31 + Q * 7 + D + T)
+    B = 2
+    values = [randn(g, (B, T, D), dtype) for _ in range(S)]
+    logits = randn(g, (Q, S, B, T), ldt, 2.0)
+    go = randn(g, (Q, B, T, D), dtype)
+    glse = randn(g, (Q, B, T), torch.float32)
+    print(f"phase-1 split: S{S} Q{Q} D{D} T{T} {dtype} logits {ldt}", flush=True)
+    out, lse, dv, dl = _phase1_hip(values, logits, go, glse, False)
+    e_out, e_lse, e_dv, e_dl = _phase1_oracle(values, logits, go, glse, False)
+    assert_close(out, e_out, dtype, "out")
+    assert_close(lse, e_lse, torch.float32, "lse")
+    for s in range(S):
+        assert_close(dv[s], e_dv[s], dtype, f"dv{s}")
+    assert_close(dl, e_dl, dtype, "dlogits", reduced=True)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("S,Q,D,key_norm", [(3, 2, 256, True), (5, 4, 768, True), (6, 16, 100, False),
                                             (2, 1, 1024, True), (9, 3, 4096, False)])
