@@ -400,8 +400,11 @@ bool base_fast_plan(const attnres_read_desc* d, const Plan& pl, BaseFastPlan* f)
   if (d->n_tok > INT32_MAX) return false;
   for (int s = 0; s < d->n_src; ++s)
     if ((uint64_t)d->value_row_stride[s] * 2 > UINT32_MAX) return false;
+  // source slots: the exact count up to 8 (a slot past n_src is a wasted row
+  // load and its arithmetic: C2's N = 7 in 8 slots cost 4% of the backward),
+  // then 10 / 12 / 14 / 16
   const int N = d->n_src;
-  f->nb = N <= 4 ? 4 : N <= 8 ? 8 : N <= 12 ? 12 : 16;
+  f->nb = N <= 1 ? 2 : N <= 8 ? N : (N + 1) / 2 * 2;
   return true;
 }
 
@@ -727,7 +730,7 @@ extern "C" int attnres_read_backward(const attnres_read_desc* d, const attnres_r
     L.wpt = bf.cb;
     L.nmax = bf.nb;
     L.grid = (int)((bp.f.streams + 3) / 4);
-    L.lds = lr_fast_table_bytes() + 4 * (size_t)PL.n_part * sizeof(float);
+    L.lds = lr_fast_table_bytes() + base_bwd_fast_lds(PL.n_part);
     if (L.lds > lds_limit()) return fail(ATTNRES_EUNSUPPORTED, "base backward needs %zu bytes of LDS", L.lds);
     // D query slots per workgroup: tiles of 16 (64-byte runs) rather than
     // slot-major rows, whose 4-byte writes to a new line per slot cost a

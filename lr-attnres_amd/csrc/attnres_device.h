@@ -378,6 +378,17 @@ __device__ __forceinline__ float wave_sums_get(const float (&z)[V / 4], int m) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(z[m >> 2]), 16 * row));
 }
 
+// wave_sums' value m in the lanes where `take` holds, `keep` elsewhere.  The
+// readlane runs in every lane, outside any lane-dependent branch: under a
+// branch such as `if (lane == s)` the compiler may sink the reduction's last
+// add into the branch, and the readlane then reads a lane the branch masked
+// off (seen as wrong logits with five source slots).
+template <int V>
+__device__ __forceinline__ float wave_sums_pick(const float (&z)[V / 4], int m, bool take, float keep) {
+  const float v = wave_sums_get<V>(z, m);
+  return take ? v : keep;
+}
+
 __device__ __forceinline__ float group_max(float x, int width) {
   if (width > 1) x = fmaxf(x, dpp_f32<kDppXor1>(x));
   if (width > 2) x = fmaxf(x, dpp_f32<kDppXor2>(x));

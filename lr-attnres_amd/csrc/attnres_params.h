@@ -53,6 +53,14 @@ __host__ __device__ constexpr int lr_fast_staged_rows(int cb, int rhc, int nb, i
 }
 
 
+// Fast base backward (attnres_base_fast.h): LDS bytes beyond the source
+// tables -- the fold rows of its four waves, n_part floats each padded to 16
+// bytes (one lane's query slots are written as 16-byte vectors).
+constexpr int kBaseFastWaves = 4;
+__host__ __device__ constexpr size_t base_bwd_fast_lds(int n_part) {
+  return (size_t)kBaseFastWaves * (((size_t)n_part + 3) / 4 * 4) * sizeof(float);
+}
+
 struct ReadParams {
   const void* val[kMaxSources];
   const void* key[kMaxSources];

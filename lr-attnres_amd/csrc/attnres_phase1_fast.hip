@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
     for (int q = 0; q < QB; ++q)
 #pragma unroll
       for (int s = 0; s < SB; ++s)
-        if (s < N && lane == q * np + s) dw = wave_sums_get<V>(z, q * SB + s);
+        dw = wave_sums_pick<V>(z, q * SB + s, s < N && lane == q * np + s, dw);
 
     // ---- logits gradient (lane (q, s)): as phase1_bwd_kernel
     {

@@ -235,17 +235,21 @@ def test_base_shapes(S, D):
     _base_case(700 + S, torch.bfloat16, 1, 5, D, S, True)
 
 
-@pytest.mark.parametrize("S,D,dtype,key_norm,bias", [
-    (2, 768, torch.bfloat16, True, False), (3, 512, torch.bfloat16, True, True),
-    (4, 1024, torch.float16, True, False), (6, 256, torch.float16, False, True),
-    (11, 768, torch.float16, True, True), (16, 1024, torch.bfloat16, True, False),
-    (16, 768, torch.bfloat16, False, False), (8, 512, torch.float16, True, True),
-    (12, 256, torch.bfloat16, True, False)])
+# every slot count of the one-wave base kernels (exact up to 8 sources, then
+# 10 / 12 / 14 / 16 with a spare slot for odd counts), cycling through the four
+# column layouts, both dtypes, key norm on and off, and a learned logit bias
+_ONE_WAVE_CASES = [(S, (768, 512, 1024, 256)[i % 4], (torch.bfloat16, torch.float16)[i % 2], i % 3 != 2, i % 4 in (1, 2))
+                   for i, S in enumerate(range(2, 17))] + [(7, 768, torch.bfloat16, False, False),
+                                                           (7, 768, torch.float16, True, True),
+                                                           (5, 768, torch.bfloat16, True, True)]
+
+
+@pytest.mark.parametrize("S,D,dtype,key_norm,bias", _ONE_WAVE_CASES)
 def test_base_one_wave_rows(S, D, dtype, key_norm, bias):
     """16-bit rows one wave covers exactly (D = 256, 512, 768, 1024): every
-    column layout and slot count (4 / 8 / 12 / 16) of the one-wave base
-    kernels, with and without key norm and a learned logit bias; 74 tokens
-    leave part of the last workgroup's streams idle."""
+    column layout and slot count of the one-wave base kernels, with and
+    without key norm and a learned logit bias; 74 tokens leave part of the
+    last workgroup's streams idle."""
     b = [0.3 * ((i % 3) - 1) for i in range(S)] if bias else None
     _base_case(900 + S + D, dtype, 2, 37, D, S, key_norm, bias=b)
 
