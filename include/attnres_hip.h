@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 6
+#define ATTNRES_ABI_VERSION 7
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -232,6 +232,11 @@ typedef struct attnres_phase1_desc {
   const void* logits;              /* device; (q, s, t) at q*logit_q_stride + s*logit_s_stride + t */
   int64_t logit_q_stride;
   int64_t logit_s_stride;
+  const void* const* source_logits; /* optional [S] device pointers (ABI 7): when set, source s's logit
+                                       for site q, token t is at source_logits[s] + q*logit_q_stride + t
+                                       and logits / logit_s_stride are unused -- each source's logits may
+                                       live in its own tensor (the block decoder keeps one [Q, n_tok] tensor
+                                       per source and block, model.py:1843-1865 builds them per source) */
 } attnres_phase1_desc;
 
 /*
@@ -259,6 +264,64 @@ int attnres_phase1_forward(const attnres_phase1_desc* desc, void* out, void* out
 int attnres_phase1_backward(const attnres_phase1_desc* desc, const void* grad_out, const float* grad_lse,
                             const void* out_prenorm, const float* out_inv_rms, void* const* dvalues,
                             void* dlogits, void* stream);
+
+/*
+ * Phase 1 backward with per-site upstream gradients and per-source logit
+ * gradients (ABI 7): grad_out_sites[q] [n_tok, dim] dense; grad_lse_sites NULL
+ * or [Q] pointers of [n_tok] fp32, each NULL for a site whose lse has no
+ * gradient; dlogits_sources[s] receives source s's logit gradient for site q,
+ * token t at + q*dlogit_q_stride + t (logits_dtype).  Same results as
+ * attnres_phase1_backward on the same values.  Lets a caller hand over the
+ * per-site gradients its autograd graph produced, and receive one gradient per
+ * source, without stacking or slicing [Q, ...] tensors.
+ * Replaces the same reference kernels as attnres_phase1_backward (the
+ * reference stacks the per-site tensors first, model.py:1931-1933).
+ */
+int attnres_phase1_backward_sites(const attnres_phase1_desc* desc, const void* const* grad_out_sites,
+                                  const float* const* grad_lse_sites, const void* out_prenorm,
+                                  const float* out_inv_rms, void* const* dvalues, void* const* dlogits_sources,
+                                  int64_t dlogit_q_stride, void* stream);
+
+/*
+ * Logits of one completed LR source against the read sites that will read it
+ * (the block decoder's per-source logit cache; replaces the eager chain of
+ * make_source_logits, model.py:1843-1865: key rms-norm, F.linear with the site
+ * queries, permute, `* lrid_logit_scale`, `+ logit biases`):
+ *   khat[t]     = rms_norm(key[t]) rounded to dtype (or the key with key_norm off)
+ *   logit[q, t] = rnd(rnd(<khat[t], queries[q]>) * logit_scale)  (+ logit_bias, fp32 logits only)
+ * logits_dtype is dtype, or fp32 when the caller adds a count-prior bias (the
+ * eager chain's bf16 + fp32 add promotes to fp32).
+ */
+#define ATTNRES_SITE_LOGITS_MAX_QUERIES 256
+#define ATTNRES_SITE_LOGITS_MAX_RANK 128
+
+typedef struct attnres_site_logits_desc {
+  int32_t dtype;          /* key and queries (ATTNRES_DTYPE_*) */
+  int32_t logits_dtype;   /* dtype, or ATTNRES_DTYPE_F32 */
+  int64_t n_tok;          /* B*T */
+  int32_t rank;           /* R, 1..ATTNRES_SITE_LOGITS_MAX_RANK */
+  int32_t n_q;            /* read sites, 1..ATTNRES_SITE_LOGITS_MAX_QUERIES; n_q * 4 * (R rounded up to
+                             32 / 64 / 128) bytes of LDS */
+  int32_t key_norm;
+  float norm_eps;
+  float logit_scale;
+  float logit_bias;       /* added after the scale when logits_dtype is fp32 */
+  const void* key;        /* device, [n_tok] rows of rank elements */
+  int64_t key_row_stride; /* elements, >= rank */
+  const void* queries;    /* device [n_q, rank] dense, dtype */
+} attnres_site_logits_desc;
+
+/* logits [n_q, n_tok] dense (logits_dtype). */
+int attnres_site_logits_forward(const attnres_site_logits_desc* desc, void* logits, void* stream);
+
+/*
+ * grad_logits: [n_q] device pointers of [n_tok] gradients (logits_dtype).
+ * Writes dkey [n_tok, rank] dense, and grad_scaled [n_q, n_tok] / key_hat
+ * [n_tok, rank] (dtype, dense): the queries' gradient is grad_scaled @ key_hat
+ * (one GEMM, as the reference's linear backward).
+ */
+int attnres_site_logits_backward(const attnres_site_logits_desc* desc, const void* const* grad_logits, void* dkey,
+                                 void* grad_scaled, void* key_hat, void* stream);
 
 /*
  * Phase 1 from a query bank: the logits of Q queries against the keys of the

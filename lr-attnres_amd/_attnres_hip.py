@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_SOURCES = 64
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -26,6 +26,8 @@ GATE_NONE, GATE_LINEAR, GATE_SIGMOID = 0, 1, 2
 MERGE_ADDCMUL, MERGE_LERP = 0, 1
 PHASE1_MAX_QUERIES = 16
 PHASE_MAX_DIM = 4096
+SITE_LOGITS_MAX_QUERIES = 256
+SITE_LOGITS_MAX_RANK = 128
 FLT_EPSILON = float(torch.finfo(torch.float32).eps)
 
 
@@ -97,6 +99,26 @@ class Phase1Desc(ctypes.Structure):
         ("logits", c_void_p),
         ("logit_q_stride", c_int64),
         ("logit_s_stride", c_int64),
+        ("source_logits", POINTER(c_void_p)),
+    ]
+
+
+class SiteLogitsDesc(ctypes.Structure):
+    """attnres_site_logits_desc."""
+
+    _fields_ = [
+        ("dtype", c_int32),
+        ("logits_dtype", c_int32),
+        ("n_tok", c_int64),
+        ("rank", c_int32),
+        ("n_q", c_int32),
+        ("key_norm", c_int32),
+        ("norm_eps", c_float),
+        ("logit_scale", c_float),
+        ("logit_bias", c_float),
+        ("key", c_void_p),
+        ("key_row_stride", c_int64),
+        ("queries", c_void_p),
     ]
 
 
@@ -221,6 +243,15 @@ def load() -> ctypes.CDLL:
     lib.attnres_phase1_backward.restype = c_int
     lib.attnres_phase1_backward.argtypes = [POINTER(Phase1Desc), c_void_p, POINTER(c_float), c_void_p,
                                             POINTER(c_float), POINTER(c_void_p), c_void_p, c_void_p]
+    lib.attnres_phase1_backward_sites.restype = c_int
+    lib.attnres_phase1_backward_sites.argtypes = [POINTER(Phase1Desc), POINTER(c_void_p), POINTER(c_void_p),
+                                                  c_void_p, POINTER(c_float), POINTER(c_void_p),
+                                                  POINTER(c_void_p), c_int64, c_void_p]
+    lib.attnres_site_logits_forward.restype = c_int
+    lib.attnres_site_logits_forward.argtypes = [POINTER(SiteLogitsDesc), c_void_p, c_void_p]
+    lib.attnres_site_logits_backward.restype = c_int
+    lib.attnres_site_logits_backward.argtypes = [POINTER(SiteLogitsDesc), POINTER(c_void_p), c_void_p, c_void_p,
+                                                 c_void_p, c_void_p]
     lib.attnres_keyed_logits_forward.restype = c_int
     lib.attnres_keyed_logits_forward.argtypes = [POINTER(KeyedLogitsDesc), c_void_p, POINTER(c_float), c_void_p]
     lib.attnres_keyed_logits_backward_workspace_size.restype = c_size_t
@@ -498,6 +529,105 @@ def phase1_backward(desc: Phase1, device, dtype, logits_dtype, grad_out, grad_ls
                                      _ptr(dlog), _stream(device))
     _check(rc, "phase-1 backward")
     return dvals, dlog
+
+
+class Phase1Sources:
+    """Descriptor of one phase-1 call whose logits come per source: S value row
+    tensors [n_tok, D] (any uniform row stride) and S logits tensors [Q, n_tok]
+    (dense, one dtype), source s's logit for site q at logits[s][q]."""
+
+    def __init__(self, values, logits, normalize_output, eps=FLT_EPSILON):
+        n = len(values)
+        self._tensors = (list(values), list(logits))
+        self.n_src = n
+        self.n_q = logits[0].size(0)
+        self.n_tok = values[0].size(0)
+        self.D = values[0].size(1)
+        self._vals = (c_void_p * n)(*[t.data_ptr() for t in values])
+        self._vstr = (c_int64 * n)(*[t.stride(0) for t in values])
+        self._logits = (c_void_p * n)(*[t.data_ptr() for t in logits])
+        d = Phase1Desc()
+        d.n_src = n
+        d.n_q = self.n_q
+        d.dtype = DTYPE_CODE[values[0].dtype]
+        d.logits_dtype = DTYPE_CODE[logits[0].dtype]
+        d.n_tok = self.n_tok
+        d.dim = self.D
+        d.normalize_output = int(bool(normalize_output))
+        d.norm_eps = float(eps)
+        d.values = self._vals
+        d.value_row_stride = self._vstr
+        d.logits = None
+        d.logit_q_stride = self.n_tok
+        d.logit_s_stride = self.n_tok
+        d.source_logits = self._logits
+        self.c = d
+
+
+def phase1_backward_sites(desc, device, dtype, logits_dtype, grads_out, grads_lse, prenorm, inv_rms):
+    """Per-site upstream gradients (Q tensors [n_tok, D]; lse gradients [n_tok]
+    or None each) -> (dvalues list of [n_tok, D], per-source dlogits list of
+    [Q, n_tok])."""
+    lib = load()
+    n, Q = desc.n_src, desc.n_q
+    dvals = _row_blocks(n, desc.n_tok, desc.D, device, dtype, False)
+    dlog = torch.empty((n, Q, desc.n_tok), device=device, dtype=logits_dtype).unbind(0)
+    dv_arr = (c_void_p * n)(*[t.data_ptr() for t in dvals])
+    dl_arr = (c_void_p * n)(*[t.data_ptr() for t in dlog])
+    go_arr = (c_void_p * Q)(*[t.data_ptr() for t in grads_out])
+    gl_arr = (c_void_p * Q)(*[t.data_ptr() if t is not None else None for t in grads_lse])
+    keep = prenorm is not None and prenorm.numel() > 0
+    rc = lib.attnres_phase1_backward_sites(ctypes.byref(desc.c), go_arr, gl_arr, _ptr(prenorm) if keep else None,
+                                           _fptr(inv_rms) if keep else None, dv_arr, dl_arr, desc.n_tok,
+                                           _stream(device))
+    _check(rc, "phase-1 backward")
+    return dvals, list(dlog)
+
+
+class SiteLogits:
+    """Descriptor of one source's site logits: key rows [n_tok, R] (uniform row
+    stride) against queries [n_q, R] (dense, key dtype)."""
+
+    def __init__(self, key, queries, key_norm, logit_scale, logits_dtype, logit_bias=0.0, eps=FLT_EPSILON):
+        self._tensors = (key, queries)
+        self.n_tok, self.R = key.size(0), key.size(1)
+        self.n_q = queries.size(0)
+        self.dtype = key.dtype
+        self.logits_dtype = logits_dtype
+        d = SiteLogitsDesc()
+        d.dtype = DTYPE_CODE[key.dtype]
+        d.logits_dtype = DTYPE_CODE[logits_dtype]
+        d.n_tok = self.n_tok
+        d.rank = self.R
+        d.n_q = self.n_q
+        d.key_norm = int(bool(key_norm))
+        d.norm_eps = float(eps)
+        d.logit_scale = float(logit_scale)
+        d.logit_bias = float(logit_bias)
+        d.key = key.data_ptr()
+        d.key_row_stride = key.stride(0)
+        d.queries = queries.data_ptr()
+        self.c = d
+
+
+def site_logits_forward(desc: SiteLogits, device):
+    """Returns logits [n_q, n_tok] (logits dtype)."""
+    out = torch.empty((desc.n_q, desc.n_tok), device=device, dtype=desc.logits_dtype)
+    _check(load().attnres_site_logits_forward(ctypes.byref(desc.c), _ptr(out), _stream(device)), "site-logits forward")
+    return out
+
+
+def site_logits_backward(desc: SiteLogits, device, grads):
+    """Per-site logit gradients (n_q tensors [n_tok]) -> (dkey [n_tok, R],
+    grad_scaled [n_q, n_tok], key_hat [n_tok, R])."""
+    dkey = torch.empty((desc.n_tok, desc.R), device=device, dtype=desc.dtype)
+    du = torch.empty((desc.n_q, desc.n_tok), device=device, dtype=desc.dtype)
+    khat = torch.empty((desc.n_tok, desc.R), device=device, dtype=desc.dtype)
+    g_arr = (c_void_p * desc.n_q)(*[t.data_ptr() for t in grads])
+    rc = load().attnres_site_logits_backward(ctypes.byref(desc.c), g_arr, _ptr(dkey), _ptr(du), _ptr(khat),
+                                             _stream(device))
+    _check(rc, "site-logits backward")
+    return dkey, du, khat
 
 
 class KeyedLogits:

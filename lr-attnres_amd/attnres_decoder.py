@@ -434,30 +434,27 @@ class Decoder(nn.Module):
             queries = queries.to(x.dtype)
         queries = queries.contiguous()       # [2L, rank]; row i-1 is read site i's query
 
-        def site_logits(value: Tensor, key: Tensor, first_read: int, count: int) -> Tensor:
-            """Logits of one completed source against read sites ``first_read..2L``: ``[2L-first_read+1, B, T]``
-            (``model.py:1838-1873``)."""
-            k = key.reshape(key.size(0), key.size(1), rank)
-            if c.attnres_key_norm:
-                k = norm(k.float()).to(value.dtype)
-            logits = F.linear(k, queries[first_read - 1:].to(k.dtype)).permute(2, 0, 1).contiguous()
-            logits = logits * c.lrid_logit_scale
-            bias = self._count_bias(count)
-            if bias != 0.0:
-                logits = logits + torch.full((logits.size(0),), bias, dtype=torch.float32,
-                                             device=logits.device).view(-1, 1, 1)
-            return logits
-
         def next_end(site: int) -> int:
             for e in ends:
                 if e > site:
                     return e
             return site + 1
 
+        def site_logits(value: Tensor, key: Tensor, first_read: int, count: int) -> dict:
+            """Logits of one completed source against read sites ``first_read..2L`` (``model.py:1838-1873``),
+            as ``{phase start: [Q_phase, B, T]}`` for the block phases that will read them."""
+            spans, s = [], first_read
+            while s <= n_sites:
+                spans.append((s, next_end(s)))
+                s = spans[-1][1]
+            k = key.reshape(key.size(0), key.size(1), rank)
+            parts = ops.lrid_site_logits(k, queries, first_read - 1, [e - b for b, e in spans], c.lrid_logit_scale,
+                                         self._count_bias(count), c.attnres_key_norm)
+            return {b: t for (b, _), t in zip(spans, parts)}
+
         emb_key = self.transformer.lrid_embedding_key(x)
         done_values = [x]
         done_logits = [site_logits(x, emb_key, 1, 1)]
-        done_first = [1]
         partial = partial_key = None
         count = 0
         phase = None                          # (first, end, outputs, lses)
@@ -470,13 +467,12 @@ class Decoder(nn.Module):
             if len(done_values) == 1:
                 # One completed source: its logit is its own lse and the read is the source itself.
                 # The expand/unbind views keep the reference's gradient summation order for it.
-                lse = done_logits[0][site - done_first[0]:end - done_first[0]].float()
+                lse = done_logits[0][site].float()
                 outs = done_values[0].unsqueeze(0).expand(lse.size(0), -1, -1, -1).unbind(0)
                 phase = (site, end, outs, lse.unbind(0))
                 return
-            logits = torch.stack([lg[site - f:end - f] for lg, f in zip(done_logits, done_first)], dim=1).contiguous()
-            out, lse = ops.attention_residual_phase1_from_logits(done_values, logits)
-            phase = (site, end, out.unbind(0), lse.unbind(0))
+            outs, lses = ops.lrid_block_phase1(done_values, [lg[site] for lg in done_logits])
+            phase = (site, end, outs, lses)
 
         def summary(value: Tensor, key: Tensor, n: int):
             """Completed LR block source (``model.py:1003-1018``)."""
@@ -529,7 +525,6 @@ class Decoder(nn.Module):
                 value, key = summary(partial, partial_key, count)
             done_values.append(value)
             done_logits.append(site_logits(value, key, site_after, count))
-            done_first.append(site_after)
             partial = partial_key = None
             count = 0
             phase = None

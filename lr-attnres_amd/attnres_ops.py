@@ -738,6 +738,152 @@ def attention_residual_phase1_from_logits(values, logits: Tensor, force_triton: 
     return out.view(Q, B, T, D), lse.view(Q, B, T)
 
 
+class _Phase1SourcesFn(torch.autograd.Function):
+    """Phase 1 of one block phase with per-source logits and per-site outputs:
+    inputs (n_src, *source logits [Q, n], *value rows [n, D]); outputs the Q
+    site outputs [n, D] and the Q lse rows [n].  The backward takes each
+    site's gradients where the consumers left them and gives each source its
+    own logit gradient, so nothing is stacked or sliced on either side."""
+
+    @staticmethod
+    def forward(ctx, n_src, *tensors):
+        logits, values = tensors[:n_src], tensors[n_src:]
+        v0 = values[0]
+        ctx.set_materialize_grads(False)
+        desc = _hip.Phase1Sources(values, logits, False)
+        with _device_ctx(v0.device):
+            out, lse, _, _ = _hip.phase1_forward(desc, v0.device, v0.dtype, False)
+        ctx.desc = desc
+        ctx.n_src = n_src
+        ctx.ldt = logits[0].dtype
+        ctx.save_for_backward(*logits, *values)
+        return (*out.unbind(0), *lse.unbind(0))
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grads):
+        Q = ctx.desc.n_q
+        values = ctx.saved_tensors[ctx.n_src:]
+        v0 = values[0]
+        g_out = [g.contiguous() if g is not None else v0.new_zeros(v0.shape) for g in grads[:Q]]
+        g_lse = [g.float().contiguous() if g is not None else None for g in grads[Q:]]
+        with _device_ctx(v0.device):
+            dvals, dlog = _hip.phase1_backward_sites(ctx.desc, v0.device, v0.dtype, ctx.ldt, g_out, g_lse, None,
+                                                     None)
+        want = ctx.needs_input_grad
+        n = ctx.n_src
+        return (None, *[d if want[1 + i] else None for i, d in enumerate(dlog)],
+                *[d if want[1 + n + i] else None for i, d in enumerate(dvals)])
+
+
+def lrid_block_phase1(values, source_logits):
+    """Phase 1 of one block phase of the block LR decoder, from per-source logits.
+
+    values: S x [B,T,D]; source_logits: S x [Q,B,T], source s's logits for
+    the phase's Q sites (promoted to one dtype, as a stack of them is).  Returns (Q outputs [B,T,D], Q lse [B,T]
+    fp32) -- what the reference's decoder gets from stacking the sources'
+    logit pieces and calling phase 1 (``model.py:1931-1933``,
+    ``attnres_ops.py:3910-3961``), with the stack and its backward's slices
+    left out.
+    """
+    srcs = _promote(_sources(values))
+    S = len(srcs)
+    if S == 0 or len(source_logits) != S:
+        raise RuntimeError(f"lrid_block_phase1: {len(source_logits)} logit tensors for {S} sources")
+    _check_sources(srcs, "lrid_block_phase1")
+    B, T, D = srcs[0].shape
+    Q = source_logits[0].size(0)
+    # one logits dtype, promoted as the reference's stack of the pieces promotes
+    # (a source without a count prior keeps 16-bit logits, the others are fp32)
+    ldt = source_logits[0].dtype
+    for lg in source_logits[1:]:
+        ldt = torch.promote_types(ldt, lg.dtype)
+    source_logits = [lg.to(ldt) for lg in source_logits]
+    for lg in source_logits:
+        if tuple(lg.shape) != (Q, B, T) or lg.dtype != ldt:
+            raise RuntimeError(f"lrid_block_phase1: logits must all be [{Q}, {B}, {T}] in {ldt}, got "
+                               f"{tuple(lg.shape)} {lg.dtype}")
+    if Q < 1 or Q > _hip.PHASE1_MAX_QUERIES:
+        raise RuntimeError(f"lrid_block_phase1: 1 <= Q <= {_hip.PHASE1_MAX_QUERIES}, got {Q}")
+    if D > _hip.PHASE_MAX_DIM:
+        raise RuntimeError(f"lrid_block_phase1: D={D} exceeds {_hip.PHASE_MAX_DIM}")
+    _check_gpu(srcs + list(source_logits), "lrid_block_phase1")
+    rows = [_rows2d(t) for t in srcs]
+    lgs = [lg.contiguous().view(Q, B * T) for lg in source_logits]
+    res = _Phase1SourcesFn.apply(S, *lgs, *rows)
+    return tuple(o.view(B, T, D) for o in res[:Q]), tuple(l.view(B, T) for l in res[Q:])
+
+
+class _SiteLogitsFn(torch.autograd.Function):
+    """One source's site logits: inputs (meta, key rows [n, R], queries [2L, R]);
+    outputs the phase pieces [Q_b, n] of the [Q', n] logits."""
+
+    @staticmethod
+    def forward(ctx, meta, key, queries):
+        first, sizes, scale, bias, key_norm, ldt = meta
+        ctx.set_materialize_grads(False)
+        desc = _hip.SiteLogits(key, queries[first:], key_norm, scale, ldt, bias)
+        with _device_ctx(key.device):
+            out = _hip.site_logits_forward(desc, key.device)
+        ctx.desc = desc
+        ctx.first = first
+        ctx.sizes = sizes
+        ctx.save_for_backward(key, queries)
+        return tuple(out.split(list(sizes), dim=0))
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grads):
+        key, queries = ctx.saved_tensors
+        n = key.size(0)
+        rows = []
+        for g, sz in zip(grads, ctx.sizes):
+            g = g.contiguous() if g is not None else key.new_zeros((sz, n), dtype=ctx.desc.logits_dtype)
+            rows.extend(g.view(sz, n).unbind(0))
+        with _device_ctx(key.device):
+            dkey, du, khat = _hip.site_logits_backward(ctx.desc, key.device, rows)
+            dq = None
+            if ctx.needs_input_grad[2]:
+                # the queries' gradient is the linear's weight gradient du^T khat (one GEMM)
+                dq = torch.zeros_like(queries)
+                torch.mm(du, khat, out=dq[ctx.first:])
+        return None, dkey if ctx.needs_input_grad[1] else None, dq
+
+
+def lrid_site_logits(key: Tensor, queries: Tensor, first: int, sizes, logit_scale: float,
+                     logit_bias: float = 0.0, key_norm: bool = True):
+    """A completed LR source's logits for every read site that will read it,
+    as the pieces the block phases read (block decoder; reference:
+    ``make_source_logits``, ``model.py:1843-1865``).
+
+    key [B,T,R] (R <= 128); queries [2L, R] in the key dtype, row i-1 for site
+    i; ``first``: row of the first site (its 1-based index minus one); sizes:
+    site counts of the phases (summing to ``2L - first``).  Logits are
+    ``rnd(rnd(<khat, q>) * logit_scale)`` in the key dtype, ``khat`` the
+    fp32 rms-norm of the key rounded to its dtype; a nonzero ``logit_bias``
+    (the count prior) is added in fp32 and makes the logits fp32, as the
+    reference's eager chain does.  Returns the pieces [Q_b, B, T].
+    """
+    if key.dim() != 3 or queries.dim() != 2 or queries.size(1) != key.size(2):
+        raise RuntimeError(f"lrid_site_logits: key [B,T,R] and queries [L,R], got {tuple(key.shape)} and "
+                           f"{tuple(queries.shape)}")
+    B, T, R = key.shape
+    sizes = tuple(int(x) for x in sizes)
+    if first < 0 or sum(sizes) != queries.size(0) - first or min(sizes) < 1:
+        raise RuntimeError(f"lrid_site_logits: phase sizes {sizes} must cover query rows {first}..{queries.size(0) - 1}")
+    if R > _hip.SITE_LOGITS_MAX_RANK:
+        raise RuntimeError(f"lrid_site_logits: rank {R} exceeds {_hip.SITE_LOGITS_MAX_RANK}")
+    if queries.dtype != key.dtype or key.dtype not in _ALLOWED:
+        raise RuntimeError(f"lrid_site_logits: queries ({queries.dtype}) must be in the key dtype ({key.dtype})")
+    _check_gpu([key, queries], "lrid_site_logits")
+    ldt = torch.float32 if float(logit_bias) != 0.0 else key.dtype
+    rows = _rows2d(key)
+    q = queries.contiguous()
+    meta = (int(first), sizes, float(logit_scale), float(logit_bias), bool(key_norm), ldt)
+    parts = _SiteLogitsFn.apply(meta, rows, q)
+    return tuple(p.view(p.size(0), B, T) for p in parts)
+
+
 class _KeyedLogitsFn(torch.autograd.Function):
     """Eager autograd of the query-bank logits: inputs (key_norm, queries [Q,D], *value rows)."""
 

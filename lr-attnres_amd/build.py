@@ -23,7 +23,7 @@ LIB = os.path.join(HERE, "libattnres_hip.so")
 SOURCES = ["attnres_capi.hip", "attnres_lr.hip", "attnres_lr_fast_fwd.hip", "attnres_lr_fast_bwd.hip",
            "attnres_base.hip", "attnres_base_bwd.hip",
            "attnres_base_fast_fwd.hip", "attnres_base_fast_bwd.hip", "attnres_phase1.hip", "attnres_phase1_fast.hip", "attnres_phase2.hip", "attnres_phase2_fast.hip", "attnres_keysplit.hip",
-           "attnres_keyed_logits.hip", "attnres_value_key.hip"]
+           "attnres_keyed_logits.hip", "attnres_value_key.hip", "attnres_site_logits.hip"]
 
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 

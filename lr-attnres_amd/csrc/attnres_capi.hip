@@ -899,6 +899,14 @@ int check_phase1(const attnres_phase1_desc* d) {
       return fail(ATTNRES_EINVAL, "value_row_stride[%d]=%lld must be in [dim, 2^31)", s,
                   (long long)d->value_row_stride[s]);
   }
+  if (d->source_logits) {
+    for (int s = 0; s < d->n_src; ++s)
+      if (live && !d->source_logits[s]) return fail(ATTNRES_EINVAL, "source_logits[%d] is NULL", s);
+    if (d->logit_q_stride < d->n_tok)
+      return fail(ATTNRES_EINVAL, "logit_q_stride %lld < n_tok=%lld", (long long)d->logit_q_stride,
+                  (long long)d->n_tok);
+    return ATTNRES_OK;
+  }
   if (live && !d->logits) return fail(ATTNRES_EINVAL, "logits is NULL");
   if (d->logit_s_stride < d->n_tok || d->logit_q_stride < (int64_t)d->n_src * d->n_tok)
     return fail(ATTNRES_EINVAL, "logit strides (%lld, %lld) overlap for n_tok=%lld, S=%d", (long long)d->logit_q_stride,
@@ -912,9 +920,11 @@ void fill_phase1(const attnres_phase1_desc* d, const PhasePlan& pl, Phase1Params
     p->val[s] = d->values[s];
     p->vstride[s] = (int32_t)d->value_row_stride[s];
   }
-  p->logits = d->logits;
+  const size_t les = elem_size(d->logits_dtype);
+  for (int s = 0; s < d->n_src; ++s)
+    p->lsrc[s] = d->source_logits ? d->source_logits[s]
+                                  : (const void*)((const char*)d->logits + (size_t)s * d->logit_s_stride * les);
   p->lq = d->logit_q_stride;
-  p->ls = d->logit_s_stride;
   p->n_tok = d->n_tok;
   p->n_src = d->n_src;
   p->n_q = d->n_q;
@@ -1138,28 +1148,35 @@ extern "C" int attnres_phase1_forward(const attnres_phase1_desc* d, void* out, v
   return ATTNRES_OK;
 }
 
-extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void* grad_out, const float* grad_lse,
-                                       const void* out_prenorm, const float* out_inv_rms, void* const* dvalues,
-                                       void* dlogits, void* stream) {
+extern "C" int attnres_phase1_backward_sites(const attnres_phase1_desc* d, const void* const* grad_out,
+                                             const float* const* grad_lse, const void* out_prenorm,
+                                             const float* out_inv_rms, void* const* dvalues,
+                                             void* const* dlogits, int64_t dlogit_q_stride, void* stream) {
   int rc = check_phase1(d);
   if (rc) return rc;
   if (d->n_tok == 0) return ATTNRES_OK;
   if (!grad_out || !dvalues || !dlogits) return fail(ATTNRES_EINVAL, "grad_out / dvalues / dlogits is NULL");
   if (d->normalize_output && (!out_prenorm || !out_inv_rms))
     return fail(ATTNRES_EINVAL, "normalize_output backward needs out_prenorm and out_inv_rms");
+  if (dlogit_q_stride < d->n_tok)
+    return fail(ATTNRES_EINVAL, "dlogit_q_stride %lld < n_tok=%lld", (long long)dlogit_q_stride, (long long)d->n_tok);
   PhasePlan pl;
-  const void* rows[2 * ATTNRES_MAX_SOURCES + 2];
-  int64_t strides[2 * ATTNRES_MAX_SOURCES + 2];
+  const void* rows[2 * ATTNRES_MAX_SOURCES + ATTNRES_PHASE1_MAX_QUERIES + 1];
+  int64_t strides[2 * ATTNRES_MAX_SOURCES + ATTNRES_PHASE1_MAX_QUERIES + 1];
   int n = 0;
   for (int s = 0; s < d->n_src; ++s) {
     if (!dvalues[s]) return fail(ATTNRES_EINVAL, "dvalues[%d] is NULL", s);
+    if (!dlogits[s]) return fail(ATTNRES_EINVAL, "dlogits[%d] is NULL", s);
     rows[n] = d->values[s];
     strides[n++] = d->value_row_stride[s];
     rows[n] = dvalues[s];
     strides[n++] = d->dim;
   }
-  rows[n] = grad_out;
-  strides[n++] = d->dim;
+  for (int q = 0; q < d->n_q; ++q) {
+    if (!grad_out[q]) return fail(ATTNRES_EINVAL, "grad_out[%d] is NULL", q);
+    rows[n] = grad_out[q];
+    strides[n++] = d->dim;
+  }
   rows[n] = d->normalize_output ? out_prenorm : nullptr;
   strides[n++] = d->dim;
   // three 8-byte columns hold the upstream rows of at most 4 sites in registers
@@ -1167,12 +1184,17 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   if (rc) return rc;
   Phase1Params p;
   fill_phase1(d, pl, &p);
-  for (int s = 0; s < d->n_src; ++s) p.dval[s] = dvalues[s];
-  p.gout = grad_out;
-  p.glse = grad_lse;
+  for (int s = 0; s < d->n_src; ++s) {
+    p.dval[s] = dvalues[s];
+    p.dlsrc[s] = dlogits[s];
+  }
+  p.dlq = dlogit_q_stride;
+  for (int q = 0; q < d->n_q; ++q) {
+    p.gout[q] = grad_out[q];
+    p.glse[q] = grad_lse ? grad_lse[q] : nullptr;
+  }
   p.out_prenorm = d->normalize_output ? const_cast<void*>(out_prenorm) : nullptr;
   p.out_inv_rms = d->normalize_output ? const_cast<float*>(out_inv_rms) : nullptr;
-  p.dlogits = dlogits;
   Launch L;
   memset(&L, 0, sizeof(L));
   if (phase1_fast(d, pl, &L)) {
@@ -1196,6 +1218,28 @@ extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void*
   hipError_t err = launch_phase1_backward(d->dtype, p, L, (hipStream_t)stream);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-1 backward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
+}
+
+extern "C" int attnres_phase1_backward(const attnres_phase1_desc* d, const void* grad_out, const float* grad_lse,
+                                       const void* out_prenorm, const float* out_inv_rms, void* const* dvalues,
+                                       void* dlogits, void* stream) {
+  int rc = check_phase1(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!grad_out || !dvalues || !dlogits) return fail(ATTNRES_EINVAL, "grad_out / dvalues / dlogits is NULL");
+  // the stacked layouts as per-site and per-source pointers: grad_out [Q, n_tok,
+  // dim], grad_lse [Q, n_tok], dlogits [Q, S, n_tok]
+  const void* go[ATTNRES_PHASE1_MAX_QUERIES];
+  const float* gl[ATTNRES_PHASE1_MAX_QUERIES];
+  void* dl[ATTNRES_MAX_SOURCES];
+  const size_t es = elem_size(d->dtype), les = elem_size(d->logits_dtype);
+  for (int q = 0; q < d->n_q; ++q) {
+    go[q] = (const char*)grad_out + (size_t)q * d->n_tok * d->dim * es;
+    gl[q] = grad_lse ? grad_lse + (size_t)q * d->n_tok : nullptr;
+  }
+  for (int s = 0; s < d->n_src; ++s) dl[s] = (char*)dlogits + (size_t)s * d->n_tok * les;
+  return attnres_phase1_backward_sites(d, go, grad_lse ? gl : nullptr, out_prenorm, out_inv_rms, dvalues, dl,
+                                       (int64_t)d->n_src * d->n_tok, stream);
 }
 
 extern "C" size_t attnres_phase2_backward_workspace_size(const attnres_phase2_desc* d) {
@@ -1393,6 +1437,89 @@ void fill_keyed_logits(const attnres_keyed_logits_desc* d, KeyedLogitsParams* p,
 int64_t keyed_logits_groups(int64_t n_tok) { return n_tok < kKeyedLogitsGroups ? n_tok : kKeyedLogitsGroups; }
 
 }  // namespace
+
+namespace {
+
+int check_site_logits(const attnres_site_logits_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  if (d->dtype < 0 || d->dtype > 2) return fail(ATTNRES_EINVAL, "unknown dtype %d", d->dtype);
+  if (d->logits_dtype != d->dtype && d->logits_dtype != ATTNRES_DTYPE_F32)
+    return fail(ATTNRES_EINVAL, "logits_dtype %d must be the dtype %d or fp32", d->logits_dtype, d->dtype);
+  if (d->n_tok < 0) return fail(ATTNRES_EINVAL, "n_tok=%lld < 0", (long long)d->n_tok);
+  if (d->rank < 1 || d->rank > ATTNRES_SITE_LOGITS_MAX_RANK)
+    return fail(ATTNRES_EUNSUPPORTED, "rank=%d outside [1, %d]", d->rank, ATTNRES_SITE_LOGITS_MAX_RANK);
+  if (d->n_q < 1 || d->n_q > ATTNRES_SITE_LOGITS_MAX_QUERIES)
+    return fail(ATTNRES_EUNSUPPORTED, "n_q=%d outside [1, %d]", d->n_q, ATTNRES_SITE_LOGITS_MAX_QUERIES);
+  if (d->key_row_stride < d->rank) return fail(ATTNRES_EINVAL, "key_row_stride %lld < rank", (long long)d->key_row_stride);
+  if (d->n_tok > 0 && (!d->key || !d->queries)) return fail(ATTNRES_EINVAL, "key / queries is NULL");
+  return ATTNRES_OK;
+}
+
+// rank slots of the kernel (32 / 64 / 128), LDS for the queries, 16-byte key loads
+int plan_site_logits(const attnres_site_logits_desc* d, SiteLogitsParams* p, Launch* L) {
+  memset(p, 0, sizeof(*p));
+  memset(L, 0, sizeof(*L));
+  L->nmax = d->rank <= 32 ? 32 : d->rank <= 64 ? 64 : 128;
+  L->lds = (size_t)d->n_q * L->nmax * sizeof(float);
+  if (L->lds > lds_limit())
+    return fail(ATTNRES_EUNSUPPORTED, "site logits need %zu bytes of LDS for %d queries", L->lds, d->n_q);
+  const int64_t groups = (d->n_tok + 255) / 256;
+  L->grid = (int)(groups < kMaxFwdGroups ? groups : kMaxFwdGroups);
+  const size_t es = elem_size(d->dtype);
+  p->key = d->key;
+  p->kstride = d->key_row_stride;
+  p->queries = d->queries;
+  p->n_tok = d->n_tok;
+  p->R = d->rank;
+  p->n_q = d->n_q;
+  p->key_norm = d->key_norm ? 1 : 0;
+  p->odt = d->logits_dtype;
+  p->vec = ((uintptr_t)d->key % 16 == 0 && (d->key_row_stride * es) % 16 == 0 && (d->rank * es) % 16 == 0) ? 1 : 0;
+  p->eps = d->norm_eps;
+  p->scale = d->logit_scale;
+  p->bias = d->logits_dtype == ATTNRES_DTYPE_F32 ? d->logit_bias : 0.f;
+  return ATTNRES_OK;
+}
+
+}  // namespace
+
+extern "C" int attnres_site_logits_forward(const attnres_site_logits_desc* d, void* logits, void* stream) {
+  int rc = check_site_logits(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!logits) return fail(ATTNRES_EINVAL, "logits is NULL");
+  SiteLogitsParams p;
+  Launch L;
+  rc = plan_site_logits(d, &p, &L);
+  if (rc) return rc;
+  p.out = logits;
+  hipError_t err = launch_site_logits_forward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "site-logits forward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
+
+extern "C" int attnres_site_logits_backward(const attnres_site_logits_desc* d, const void* const* grad_logits,
+                                            void* dkey, void* grad_scaled, void* key_hat, void* stream) {
+  int rc = check_site_logits(d);
+  if (rc) return rc;
+  if (d->n_tok == 0) return ATTNRES_OK;
+  if (!grad_logits || !dkey || !grad_scaled || !key_hat)
+    return fail(ATTNRES_EINVAL, "grad_logits / dkey / grad_scaled / key_hat is NULL");
+  SiteLogitsParams p;
+  Launch L;
+  rc = plan_site_logits(d, &p, &L);
+  if (rc) return rc;
+  for (int q = 0; q < d->n_q; ++q) {
+    if (!grad_logits[q]) return fail(ATTNRES_EINVAL, "grad_logits[%d] is NULL", q);
+    p.dout[q] = grad_logits[q];
+  }
+  p.dkey = dkey;
+  p.du = grad_scaled;
+  p.khat = key_hat;
+  hipError_t err = launch_site_logits_backward(d->dtype, p, L, (hipStream_t)stream);
+  if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "site-logits backward launch failed: %s", hipGetErrorString(err));
+  return ATTNRES_OK;
+}
 
 extern "C" int attnres_keyed_logits_forward(const attnres_keyed_logits_desc* d, void* logits, float* inv_rms,
                                             void* stream) {

@@ -66,6 +66,11 @@ hipError_t launch_keyed_logits_backward(int dtype, const KeyedLogitsParams& p, c
 hipError_t launch_keyed_split_forward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);
 hipError_t launch_keyed_split_backward(int dtype, const KeySplitParams& p, const Launch& L, hipStream_t st);
 
+// one source's site logits: L.nmax = rank slots (32/64/128), L.grid x 4 waves,
+// L.lds = n_q * nmax floats (the queries)
+hipError_t launch_site_logits_forward(int dtype, const SiteLogitsParams& p, const Launch& L, hipStream_t st);
+hipError_t launch_site_logits_backward(int dtype, const SiteLogitsParams& p, const Launch& L, hipStream_t st);
+
 // dtype switch of the launchers
 #define ATTNRES_DISPATCH(dtype, fn, ...)                          \
   switch (dtype) {                                                \

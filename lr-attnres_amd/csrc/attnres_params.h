@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "../../include/attnres_hip.h"
+#include "attnres_device.h"
 
 namespace attnres {
 
@@ -168,21 +169,59 @@ struct Phase1Params {
   const void* val[kMaxSources];
   void* dval[kMaxSources];     // backward: [n_tok, D] dense
   int32_t vstride[kMaxSources];
-  const void* logits;          // (q, s, t) at q*lq + s*ls + t
-  int64_t lq, ls;
+  const void* lsrc[kMaxSources];  // source s's logits: (q, t) at lsrc[s] + q*lq + t (elements)
+  int64_t lq;
+  void* dlsrc[kMaxSources];       // backward: source s's logit gradient, (q, t) at dlsrc[s] + q*dlq + t
+  int64_t dlq;
   void* out;                   // [Q, n_tok, D]
   void* out_prenorm;           // [Q, n_tok, D] or null
   float* lse;                  // [Q, n_tok]
   float* out_inv_rms;          // [Q, n_tok] or null
-  const void* gout;            // backward: [Q, n_tok, D]
-  const float* glse;           // backward: [Q, n_tok] or null
-  void* dlogits;               // backward: [Q, S, n_tok] dense, logits dtype
+  const void* gout[ATTNRES_PHASE1_MAX_QUERIES];   // backward: site q's output gradient [n_tok, D] dense
+  const float* glse[ATTNRES_PHASE1_MAX_QUERIES];  // backward: site q's lse gradient [n_tok], null = zero
   int64_t n_tok;
   int32_t n_src, n_q, D, ncols;
   int32_t ldt;                 // logits dtype code
   int32_t norm_out;
   int32_t np;                  // lanes per softmax row: next power of two >= n_src
   float eps;
+};
+
+// Phase-1 accessors (the source and site indices may differ across lanes: the
+// pointer tables are read from the kernel arguments per lane)
+__device__ __forceinline__ float p1_logit(const Phase1Params& p, int q, int s, int64_t t) {
+  return load_any(p.lsrc[s], (int64_t)q * p.lq + t, p.ldt);
+}
+__device__ __forceinline__ void p1_store_dlogit(const Phase1Params& p, int q, int s, int64_t t, float v) {
+  store_any(p.dlsrc[s], (int64_t)q * p.dlq + t, p.ldt, v);
+}
+// site q's lse gradient (0 for a site without one; q < n_q; the table index is
+// clamped so that a load the compiler hoists out of a lane condition stays
+// inside the table)
+__device__ __forceinline__ float p1_glse(const Phase1Params& p, int q, int64_t t) {
+  const float* g = p.glse[q < kPhase1MaxQ ? q : kPhase1MaxQ - 1];
+  return g ? g[t] : 0.f;
+}
+// dl = w (dW - <w, dW>) plus the lse term w * glse, rounded as the eager op
+// rounds its logit gradient (a site without an lse gradient adds 0)
+__device__ __forceinline__ float p1_dlogit(const Phase1Params& p, float dl, float gl) {
+  return p.ldt == ATTNRES_DTYPE_F32 ? dl + gl : round_any(round_any(dl, p.ldt) + round_any(gl, p.ldt), p.ldt);
+}
+
+// Logits of one LR source against its read sites (attnres_site_logits.hip)
+constexpr int kSiteLogitsMaxQ = ATTNRES_SITE_LOGITS_MAX_QUERIES;
+struct SiteLogitsParams {
+  const void* key;        // [n_tok] rows of R elements, row stride kstride (elements)
+  int64_t kstride;
+  const void* queries;    // [n_q, R] dense, dtype
+  void* out;              // forward: [n_q, n_tok] dense, odt
+  const void* dout[kSiteLogitsMaxQ];  // backward: site q's logit gradient [n_tok], odt
+  void* dkey;             // backward: [n_tok, R] dense
+  void* du;               // backward: [n_q, n_tok] dense, dtype
+  void* khat;             // backward: [n_tok, R] dense, dtype
+  int64_t n_tok;
+  int32_t R, n_q, key_norm, odt, vec;
+  float eps, scale, bias;
 };
 
 // Phase 2 (merge of a read site's phase-1 result with the partial block)

@@ -40,7 +40,7 @@ __device__ __forceinline__ void phase1_softmax(const Phase1Params& p, int64_t to
   for (int q0 = 0; q0 < Q; q0 += qpr) {
     const int q = q0 + ql;
     const bool ok = sl < N && q < Q;
-    const float l = ok ? load_any(p.logits, (int64_t)q * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
+    const float l = ok ? p1_logit(p, q, sl, tok) : -INFINITY;
     const float m = group_max(l, np);
     const float e = ok ? expf(l - m) : 0.f;
     const float z = group_sum(e, np);
@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
 #pragma unroll
     for (int q = 0; q < QMAX; ++q) {
       if (q < Q) {
-        const S* gp = (const S*)p.gout + ((int64_t)q * p.n_tok + tok) * D;
+        const S* gp = (const S*)p.gout[q] + tok * (int64_t)D;
 #pragma unroll
         for (int c = 0; c < CB; ++c)
           if (cl.ok[c]) load_raw<DT, E, true>(gp + cl.eoff[c], gr[q][c]);
@@ -298,13 +298,8 @@ __global__ void __launch_bounds__(512) phase1_bwd_kernel(const Phase1Params p) {
         const float dwb = DT::rnd(dw);  // gradient of the dtype-rounded weights
         const float inner = group_sum(wt * dwb, np);
         float dl = wt * (dwb - inner);
-        if (p.glse) {
-          const float gl = ok ? p.glse[(int64_t)q * p.n_tok + tok] * wt : 0.f;
-          dl = p.ldt == ATTNRES_DTYPE_F32 ? dl + gl : round_any(round_any(dl, p.ldt) + round_any(gl, p.ldt), p.ldt);
-        } else {
-          dl = round_any(dl, p.ldt);
-        }
-        if (ok) store_any(p.dlogits, ((int64_t)q * N + sl) * p.n_tok + tok, p.ldt, dl);
+        dl = p1_dlogit(p, dl, ok ? p1_glse(p, q, tok) * wt : 0.f);
+        if (ok) p1_store_dlogit(p, q, sl, tok, dl);
       }
     }
 

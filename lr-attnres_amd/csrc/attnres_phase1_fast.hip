@@ -45,7 +45,7 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
     Raw<DT, E> gr[QB][CB], vr[SB][CB];
 #pragma unroll
     for (int q = 0; q < QB; ++q) {
-      const S* gp = (const S*)p.gout + ((int64_t)min(q, Q - 1) * p.n_tok + tok) * D;
+      const S* gp = (const S*)p.gout[min(q, Q - 1)] + tok * (int64_t)D;
 #pragma unroll
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gp + (c * kWave + lane) * E, gr[q][c]);
     }
@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
     }
     // ---- softmax rows in the (site, source) lane layout
-    const float l = own ? load_any(p.logits, (int64_t)ql * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
+    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float wt = ex / group_sum(ex, np);
@@ -89,13 +89,8 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
       const float dwb = DT::rnd(dw);  // gradient of the dtype-rounded weights
       const float inner = group_sum(own ? wt * dwb : 0.f, np);
       float dl = wt * (dwb - inner);
-      if (p.glse) {
-        const float gl = own ? p.glse[(int64_t)ql * p.n_tok + tok] * wt : 0.f;
-        dl = p.ldt == ATTNRES_DTYPE_F32 ? dl + gl : round_any(round_any(dl, p.ldt) + round_any(gl, p.ldt), p.ldt);
-      } else {
-        dl = round_any(dl, p.ldt);
-      }
-      if (own) store_any(p.dlogits, ((int64_t)ql * N + sl) * p.n_tok + tok, p.ldt, dl);
+      dl = p1_dlogit(p, dl, own ? p1_glse(p, ql, tok) * wt : 0.f);
+      if (own) p1_store_dlogit(p, ql, sl, tok, dl);
     }
 
     // ---- dv[s] = rnd(sum_q rnd(w[q, s]) g[q]): upstream rows interleaved by
@@ -168,7 +163,7 @@ __global__ void __launch_bounds__(256) phase1_fwd_fast_kernel(const Phase1Params
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
     }
     // softmax rows and lse in the (site, source) lane layout
-    const float l = own ? load_any(p.logits, (int64_t)ql * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
+    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float z = group_sum(ex, np);
@@ -253,7 +248,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_split_kernel(const Phase1Param
       const int j = min(s, N - 1);
       load_raw<DT, 4, true>((const S*)p.val[j] + tok * (int64_t)p.vstride[j] + col, vr[s]);
     }
-    const float l = own ? load_any(p.logits, (int64_t)ql * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
+    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float z = group_sum(ex, np);
@@ -314,14 +309,14 @@ __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Param
     Raw<DT, 4> gr[QB], vr[SB];
 #pragma unroll
     for (int q = 0; q < QB; ++q)
-      load_raw<DT, 4, true>((const S*)p.gout + ((int64_t)min(q, Q - 1) * p.n_tok + tok) * D + col, gr[q]);
+      load_raw<DT, 4, true>((const S*)p.gout[min(q, Q - 1)] + tok * (int64_t)D + col, gr[q]);
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
       const int j = min(s, N - 1);
       load_raw<DT, 4, true>((const S*)p.val[j] + tok * (int64_t)p.vstride[j] + col, vr[s]);
     }
-    const float l = own ? load_any(p.logits, (int64_t)ql * p.lq + (int64_t)sl * p.ls + tok, p.ldt) : -INFINITY;
-    const float glse = (p.glse && own) ? p.glse[(int64_t)ql * p.n_tok + tok] : 0.f;
+    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
+    const float glse = own ? p1_glse(p, ql, tok) : 0.f;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float wt = ex / group_sum(ex, np);
@@ -362,13 +357,8 @@ __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Param
       const float dwb = DT::rnd(dw);
       const float inner = group_sum(own ? wt * dwb : 0.f, np);
       float dl = wt * (dwb - inner);
-      if (p.glse) {
-        const float gl = own ? glse * wt : 0.f;
-        dl = p.ldt == ATTNRES_DTYPE_F32 ? dl + gl : round_any(round_any(dl, p.ldt) + round_any(gl, p.ldt), p.ldt);
-      } else {
-        dl = round_any(dl, p.ldt);
-      }
-      if (chunk == 0 && own) store_any(p.dlogits, ((int64_t)ql * N + sl) * p.n_tok + tok, p.ldt, dl);
+      dl = p1_dlogit(p, dl, own ? glse * wt : 0.f);
+      if (chunk == 0 && own) p1_store_dlogit(p, ql, sl, tok, dl);
     }
 
     // dv[s] = rnd(sum_q rnd(w[q, s]) g[q]) over this wave's columns: upstream

@@ -55,6 +55,10 @@ lrid_block_accumulate_ref                 composition of the pinned split and
                                           block_* helpers; the decoder built on
                                           it reproduces the reference-model
                                           golden vectors
+lrid_site_logits_ref,                     the decoder built on them reproduces the
+lrid_block_phase1_ref                     reference-model golden vectors bit for bit
+                                          (tests/test_decoder_host.py): they are the
+                                          decoder's former inline eager chain
 phase1_from_logits_ref / phase2_*_ref     phase1+phase2 == full read identity
                                           (tests/test_attnres_ops.py:582-610),
                                           golden fixtures with gradients,
@@ -351,6 +355,39 @@ def phase1_from_logits_ref(values, logits: Tensor, normalize_output: bool = Fals
     if normalize_output:
         out = norm(out)
     return out, torch.logsumexp(logits.float(), dim=1)
+
+
+def lrid_site_logits_ref(key: Tensor, queries: Tensor, first: int, sizes, logit_scale: float,
+                         logit_bias: float = 0.0, key_norm: bool = True):
+    """One completed LR source's logits for the read sites that will read it,
+    split into the phases that read them -- ``make_source_logits``
+    (``model.py:1843-1865``): key rms-normed in fp32 and rounded to its dtype,
+    ``F.linear`` with the queries of sites ``first + 1 ..`` (rows ``first ..``
+    of ``queries``), permuted to [Q', B, T], ``* logit_scale`` and, when the
+    count prior gives a nonzero bias, ``+ bias`` in fp32.
+
+    key [B, T, R]; queries [2L, R] (the key dtype).  Returns ``sizes``-long
+    pieces of the [Q', B, T] logits along the sites (views).
+    """
+    k = key
+    if key_norm:
+        k = norm(k.float()).to(key.dtype)
+    logits = F.linear(k, queries[first:].to(k.dtype)).permute(2, 0, 1).contiguous()
+    logits = logits * logit_scale
+    if logit_bias != 0.0:
+        logits = logits + torch.full((logits.size(0),), logit_bias, dtype=torch.float32,
+                                     device=logits.device).view(-1, 1, 1)
+    return logits.split(list(sizes), dim=0)
+
+
+def lrid_block_phase1_ref(values, source_logits):
+    """Phase 1 of one block phase from the per-source logits of its sites: the
+    decoder's stack of the sources' logit pieces along S (``model.py:1931-1933``)
+    followed by phase 1 (``attnres_ops.py:3956-3961``).  values S x [B,T,D];
+    source_logits S x [Q,B,T].  Returns per-site (out [B,T,D] ..., lse [B,T] ...)."""
+    logits = torch.stack(list(source_logits), dim=1).contiguous()
+    out, lse = phase1_from_logits_ref(values, logits)
+    return out.unbind(0), lse.unbind(0)
 
 
 def attention_residual_phase1_ref(values, queries: Tensor, key_norm: bool):

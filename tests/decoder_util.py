@@ -32,6 +32,14 @@ class OracleOps:
         return O.phase1_from_logits_ref(values, logits, normalize_output)
 
     @staticmethod
+    def lrid_site_logits(key, queries, first, sizes, logit_scale, logit_bias=0.0, key_norm=True):
+        return O.lrid_site_logits_ref(key, queries, first, sizes, logit_scale, logit_bias, key_norm)
+
+    @staticmethod
+    def lrid_block_phase1(values, source_logits):
+        return O.lrid_block_phase1_ref(values, source_logits)
+
+    @staticmethod
     def lrid_attention_residual_phase2_torch(pv, pk, q, inter, lse, scale, key_norm, normalize_output=False,
                                              logit_bias=0.0, partial_scale=None, scale_key=False):
         return _phase2(pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias, partial_scale,

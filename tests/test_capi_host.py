@@ -42,7 +42,8 @@ def test_library_exports_every_declared_symbol():
                             "attnres_kernel_times", "attnres_read_backward_noalloc", "attnres_test_phase2_block_layout",
                             "attnres_value_norm_forward", "attnres_value_norm_backward",
                             "attnres_block_accum_forward", "attnres_block_accum_backward",
-                            "attnres_block_accum_backward_workspace_size"])
+                            "attnres_block_accum_backward_workspace_size", "attnres_phase1_backward_sites",
+                            "attnres_site_logits_forward", "attnres_site_logits_backward"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -53,7 +54,7 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 6
+    assert lib.attnres_abi_version() == 7
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()

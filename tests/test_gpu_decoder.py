@@ -76,6 +76,25 @@ class CheckingOps:
         self.calls.append(("phase1", len(values), logits.size(0)))
         return out, lse
 
+    def lrid_block_phase1(self, values, source_logits):
+        outs, lses = ops.lrid_block_phase1(values, source_logits)
+        e_outs, e_lses = O.lrid_block_phase1_ref([v.cpu() for v in values], [lg.cpu() for lg in source_logits])
+        for a, e in zip(outs, e_outs):
+            assert_close(a, e, values[0].dtype, "phase1 out")
+        for a, e in zip(lses, e_lses):
+            assert_close(a, e, values[0].dtype, "phase1 lse")
+        self.calls.append(("phase1", len(values), len(outs)))
+        return outs, lses
+
+    def lrid_site_logits(self, key, queries, first, sizes, logit_scale, logit_bias=0.0, key_norm=True):
+        parts = ops.lrid_site_logits(key, queries, first, sizes, logit_scale, logit_bias, key_norm)
+        e_parts = O.lrid_site_logits_ref(key.cpu(), queries.cpu(), first, sizes, logit_scale, logit_bias, key_norm)
+        for a, e in zip(parts, e_parts):
+            assert a.dtype == e.dtype
+            assert_close(a, e, key.dtype, "site logits")
+        self.calls.append(("site_logits", first, tuple(sizes)))
+        return parts
+
     def lrid_fused_projection_split(self, projected, output_dim, rank, num_heads=1, key_norm=True):
         out, key = ops.lrid_fused_projection_split(projected, output_dim, rank, num_heads, key_norm)
         e_out, e_key = O.lrid_fused_projection_split_ref(projected.cpu(), output_dim, rank, num_heads, key_norm)
@@ -147,6 +166,8 @@ def test_config5_every_read_matches_oracle(torch_phase2):
     # three in-block sites of each block (site 1..3 read the embedding alone in phase 1).
     assert n1 == 6
     assert n2 == 18
+    # the embedding and the 6 block sources each get their logits once, split into the phases after them
+    assert sum(1 for c in checker.calls if c[0] == "site_logits") == 7
     # every sublayer grows the partial block in one fused pass; 6 of them end a block
     assert sum(1 for c in checker.calls if c[0] == "accumulate") == 24
     assert sum(1 for c in checker.calls if c == ("accumulate", True)) == 6
