@@ -1463,7 +1463,7 @@ int plan_site_logits(const attnres_site_logits_desc* d, SiteLogitsParams* p, Lau
   L->lds = (size_t)d->n_q * L->nmax * sizeof(float);
   if (L->lds > lds_limit())
     return fail(ATTNRES_EUNSUPPORTED, "site logits need %zu bytes of LDS for %d queries", L->lds, d->n_q);
-  const int64_t groups = (d->n_tok + 255) / 256;
+  const int64_t groups = (d->n_tok + 31) / 32;  // 32 tokens per workgroup (8 lanes each)
   L->grid = (int)(groups < kMaxFwdGroups ? groups : kMaxFwdGroups);
   const size_t es = elem_size(d->dtype);
   p->key = d->key;

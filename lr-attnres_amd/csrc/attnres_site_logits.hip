@@ -3,9 +3,9 @@
 // make_source_logits):
 //   khat[t]      = rnd(rms_norm(key[t]))        (fp32 norm, rounded to the dtype; or the key itself)
 //   logit[q, t]  = rnd(rnd(<khat[t], query[q]>) * scale)   (+ bias in fp32 when the count prior is on)
-// One lane per token: a token's key row (R <= 128) sits in the lane's
-// registers, the site queries in LDS (read as broadcasts), and a wave's stores
-// of one site are 64 consecutive logits.  The backward follows the eager op's
+// Eight lanes per token, each with the token's key row (R <= 128) in
+// registers and every eighth site; the site queries sit in LDS (read as
+// broadcasts).  The backward follows the eager op's
 // autograd: the bias add hands the 16-bit branch rnd(g), the scale gives
 // du = rnd(g * scale), the linear gives dkhat = rnd(sum_q du[q] query[q]) and
 // the rms-norm backward dkey = rnd(inv (dkhat - khat_f32 <dkhat, khat_f32> / R));
@@ -18,7 +18,8 @@
 namespace attnres {
 
 constexpr int kSLWaves = 4;  // waves per workgroup
-constexpr int kSLBatch = 8;  // backward: site gradients loaded per batch
+constexpr int kSLBatch = 4;  // backward: site gradients a lane loads per batch
+constexpr int kSLLanes = 8;  // lanes per token
 
 // this lane's key row (R elements, RM >= R slots; slots past R are 0)
 template <class DT, int RM>
@@ -65,21 +66,30 @@ __device__ __forceinline__ void sl_queries_to_lds(const SiteLogitsParams& p, flo
   __syncthreads();
 }
 
+// Eight lanes per token (kSLLanes): lane c of a token's group takes the sites
+// c, c + 8, ..., so that short inputs (a 2048-token batch has 2048 tokens to
+// spread over 256 CUs) still have 8 waves per 64 tokens; the group's lanes are
+// adjacent, and the token loop runs wave-uniformly (the last tokens clamped,
+// their stores dropped) so that the group sums stay inside full groups.
 template <class DT, int RM>
 __global__ void __launch_bounds__(kSLWaves * kWave) site_logits_fwd_kernel(const SiteLogitsParams p) {
   using S = typename DT::S;
   extern __shared__ float s_q[];
   sl_queries_to_lds<DT, RM>(p, s_q);
-  for (int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; tok < p.n_tok;
-       tok += (int64_t)gridDim.x * blockDim.x) {
+  const int c = threadIdx.x & (kSLLanes - 1);
+  const int64_t per_wave = kWave / kSLLanes;
+  const int64_t step = (int64_t)gridDim.x * kSLWaves * per_wave;
+  for (int64_t w0 = ((int64_t)blockIdx.x * kSLWaves + threadIdx.x / kWave) * per_wave; w0 < p.n_tok; w0 += step) {
+    const int64_t tok = w0 + (threadIdx.x & (kWave - 1)) / kSLLanes;
+    const bool live = tok < p.n_tok;
     float k[RM];
-    sl_load_key<DT, RM>(p, tok, k);
+    sl_load_key<DT, RM>(p, live ? tok : p.n_tok - 1, k);
     if (p.key_norm) {
       const float inv = sl_inv_rms<RM>(p, k);
 #pragma unroll
       for (int j = 0; j < RM; ++j) k[j] = DT::rnd(k[j] * inv);
     }
-    for (int q = 0; q < p.n_q; ++q) {
+    for (int q = c; q < p.n_q; q += kSLLanes) {
       const float4* qr = (const float4*)(s_q + q * RM);
       float dot = 0.f;
 #pragma unroll
@@ -92,8 +102,10 @@ __global__ void __launch_bounds__(kSLWaves * kWave) site_logits_fwd_kernel(const
       }
       const float t = DT::rnd(DT::rnd(dot) * p.scale);
       const int64_t o = (int64_t)q * p.n_tok + tok;
-      if (p.odt == ATTNRES_DTYPE_F32) ((float*)p.out)[o] = t + p.bias;
-      else DT::store1((S*)p.out + o, t);
+      if (live) {
+        if (p.odt == ATTNRES_DTYPE_F32) ((float*)p.out)[o] = t + p.bias;
+        else DT::store1((S*)p.out + o, t);
+      }
     }
   }
 }
@@ -105,29 +117,34 @@ __global__ void __launch_bounds__(kSLWaves * kWave) site_logits_bwd_kernel(const
   sl_queries_to_lds<DT, RM>(p, s_q);
   // the bias add hands a 16-bit branch its gradient rounded to the dtype
   const bool round_in = p.odt == ATTNRES_DTYPE_F32 && DT::kCode != 0;
-  for (int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; tok < p.n_tok;
-       tok += (int64_t)gridDim.x * blockDim.x) {
+  const int c = threadIdx.x & (kSLLanes - 1);
+  const int64_t per_wave = kWave / kSLLanes;
+  const int64_t step = (int64_t)gridDim.x * kSLWaves * per_wave;
+  for (int64_t w0 = ((int64_t)blockIdx.x * kSLWaves + threadIdx.x / kWave) * per_wave; w0 < p.n_tok; w0 += step) {
+    const int64_t tok = w0 + (threadIdx.x & (kWave - 1)) / kSLLanes;
+    const bool live = tok < p.n_tok;
+    const int64_t t = live ? tok : p.n_tok - 1;
     float inv = 1.f;
     if (p.key_norm) {
       float k[RM];
-      sl_load_key<DT, RM>(p, tok, k);
+      sl_load_key<DT, RM>(p, t, k);
       inv = sl_inv_rms<RM>(p, k);
     }
+    // this lane's sites: loads issued in batches, then du and its share of dkhat
     float dk[RM];
 #pragma unroll
     for (int j = 0; j < RM; ++j) dk[j] = 0.f;
-    // sites in batches of kSLBatch: the batch's gradient loads are issued
-    // together (clamped to the last site, unconditionally) before any is used
-    for (int q0 = 0; q0 < p.n_q; q0 += kSLBatch) {
+    for (int q0 = c; q0 < p.n_q; q0 += kSLBatch * kSLLanes) {
       float g[kSLBatch];
 #pragma unroll
-      for (int i = 0; i < kSLBatch; ++i) g[i] = load_any(p.dout[min(q0 + i, p.n_q - 1)], tok, p.odt);
+      for (int i = 0; i < kSLBatch; ++i)
+        g[i] = load_any(p.dout[min(q0 + i * kSLLanes, p.n_q - 1)], t, p.odt);
 #pragma unroll
       for (int i = 0; i < kSLBatch; ++i) {
-        const int q = q0 + i;
+        const int q = q0 + i * kSLLanes;
         if (q < p.n_q) {
           const float du = DT::rnd((round_in ? DT::rnd(g[i]) : g[i]) * p.scale);
-          DT::store1((S*)p.du + (int64_t)q * p.n_tok + tok, du);
+          if (live) DT::store1((S*)p.du + (int64_t)q * p.n_tok + tok, du);
           const float4* qr = (const float4*)(s_q + q * RM);
 #pragma unroll
           for (int j4 = 0; j4 < RM / 4; ++j4) {
@@ -140,31 +157,30 @@ __global__ void __launch_bounds__(kSLWaves * kWave) site_logits_bwd_kernel(const
         }
       }
     }
+    // dkhat summed over the token's eight lanes (every lane ends with the sum)
+#pragma unroll
+    for (int j = 0; j < RM; ++j) dk[j] = DT::rnd(group_sum(dk[j], kSLLanes));
     float k[RM];  // loaded again: not held through the site loop
-    sl_load_key<DT, RM>(p, tok, k);
-    S* khp = (S*)p.khat + tok * (int64_t)p.R;
-    S* dkp = (S*)p.dkey + tok * (int64_t)p.R;
+    sl_load_key<DT, RM>(p, t, k);
+    float mr = 0.f;
     if (p.key_norm) {
       float m = 0.f;
 #pragma unroll
-      for (int j = 0; j < RM; ++j) {
-        dk[j] = DT::rnd(dk[j]);
-        m += dk[j] * (k[j] * inv);
-      }
-      const float mr = m / (float)p.R;
+      for (int j = 0; j < RM; ++j) m += dk[j] * (k[j] * inv);
+      mr = m / (float)p.R;
+    }
+    // lane c writes elements c, c + 8, ... of khat and dkey
+    S* khp = (S*)p.khat + tok * (int64_t)p.R;
+    S* dkp = (S*)p.dkey + tok * (int64_t)p.R;
 #pragma unroll
-      for (int j = 0; j < RM; ++j) {
-        if (j < p.R) {
+    for (int j = 0; j < RM; ++j) {
+      if ((j & (kSLLanes - 1)) == c && j < p.R && live) {
+        if (p.key_norm) {
           DT::store1(khp + j, DT::rnd(k[j] * inv));
           DT::store1(dkp + j, DT::rnd(inv * (dk[j] - k[j] * inv * mr)));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < RM; ++j) {
-        if (j < p.R) {
+        } else {
           DT::store1(khp + j, k[j]);
-          DT::store1(dkp + j, DT::rnd(dk[j]));
+          DT::store1(dkp + j, dk[j]);
         }
       }
     }
