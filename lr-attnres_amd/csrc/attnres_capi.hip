@@ -914,6 +914,19 @@ int check_phase1(const attnres_phase1_desc* d) {
   return ATTNRES_OK;
 }
 
+// true when ptr[i] = ptr[0] + i * stride for one stride in elements of es bytes
+// (returned in *stride); a single pointer is trivially uniform
+bool uniform_stride(const void* const* ptr, int n, size_t es, int64_t* stride) {
+  *stride = 0;
+  if (n <= 1) return true;
+  const int64_t d = (int64_t)((intptr_t)ptr[1] - (intptr_t)ptr[0]);
+  if (d % (int64_t)es) return false;
+  for (int i = 2; i < n; ++i)
+    if ((int64_t)((intptr_t)ptr[i] - (intptr_t)ptr[0]) != d * i) return false;
+  *stride = d / (int64_t)es;
+  return true;
+}
+
 void fill_phase1(const attnres_phase1_desc* d, const PhasePlan& pl, Phase1Params* p) {
   memset(p, 0, sizeof(*p));
   for (int s = 0; s < d->n_src; ++s) {
@@ -925,6 +938,7 @@ void fill_phase1(const attnres_phase1_desc* d, const PhasePlan& pl, Phase1Params
     p->lsrc[s] = d->source_logits ? d->source_logits[s]
                                   : (const void*)((const char*)d->logits + (size_t)s * d->logit_s_stride * les);
   p->lq = d->logit_q_stride;
+  p->stacked = uniform_stride(p->lsrc, d->n_src, les, &p->ls) ? 1 : 0;  // the backward refines it
   p->n_tok = d->n_tok;
   p->n_src = d->n_src;
   p->n_q = d->n_q;
@@ -1189,9 +1203,21 @@ extern "C" int attnres_phase1_backward_sites(const attnres_phase1_desc* d, const
     p.dlsrc[s] = dlogits[s];
   }
   p.dlq = dlogit_q_stride;
+  int n_glse = 0;
   for (int q = 0; q < d->n_q; ++q) {
     p.gout[q] = grad_out[q];
     p.glse[q] = grad_lse ? grad_lse[q] : nullptr;
+    n_glse += p.glse[q] != nullptr;
+  }
+  // one base and uniform strides for every table (e.g. the stacked layouts of
+  // attnres_phase1_backward): the column-split kernels then address rows from
+  // the first entry
+  if (p.stacked) {
+    const size_t les = elem_size(d->logits_dtype);
+    const bool ok = uniform_stride((const void* const*)p.dlsrc, d->n_src, les, &p.dls) &&
+                    uniform_stride(p.gout, d->n_q, elem_size(d->dtype), &p.gq) &&
+                    (n_glse == 0 || (n_glse == d->n_q && uniform_stride((const void* const*)p.glse, d->n_q, 4, &p.glq)));
+    p.stacked = ok ? 1 : 0;
   }
   p.out_prenorm = d->normalize_output ? const_cast<void*>(out_prenorm) : nullptr;
   p.out_inv_rms = d->normalize_output ? const_cast<float*>(out_inv_rms) : nullptr;

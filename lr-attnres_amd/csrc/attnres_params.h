@@ -179,6 +179,12 @@ struct Phase1Params {
   float* out_inv_rms;          // [Q, n_tok] or null
   const void* gout[ATTNRES_PHASE1_MAX_QUERIES];   // backward: site q's output gradient [n_tok, D] dense
   const float* glse[ATTNRES_PHASE1_MAX_QUERIES];  // backward: site q's lse gradient [n_tok], null = zero
+  // stacked: every table above is entry 0 plus a uniform stride (elements):
+  // lsrc[s] = lsrc[0] + s*ls, dlsrc[s] = dlsrc[0] + s*dls, gout[q] = gout[0] +
+  // q*gq, glse[q] = glse[0] + q*glq (or all null); the column-split kernels
+  // then address rows from entry 0 instead of holding every table entry
+  int32_t stacked;
+  int64_t ls, dls, gq, glq;
   int64_t n_tok;
   int32_t n_src, n_q, D, ncols;
   int32_t ldt;                 // logits dtype code
@@ -186,6 +192,18 @@ struct Phase1Params {
   int32_t np;                  // lanes per softmax row: next power of two >= n_src
   float eps;
 };
+
+// Entry idx (< K) of a pointer table in the kernel arguments: the K entries
+// are read as scalars and the lane's one picked by a chain of selects, so that
+// no lane waits on a per-lane load of its pointer before the load it addresses.
+template <int K, class T, int M>
+__device__ __forceinline__ T p1_pick(T const (&tab)[M], int idx) {
+  static_assert(K <= M, "table smaller than the slots picked from");
+  T r = tab[0];
+#pragma unroll
+  for (int i = 1; i < K; ++i) r = idx == i ? tab[i] : r;
+  return r;
+}
 
 // Phase-1 accessors (the source and site indices may differ across lanes: the
 // pointer tables are read from the kernel arguments per lane)

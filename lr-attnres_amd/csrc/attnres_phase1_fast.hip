@@ -38,6 +38,10 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
   // (site, source) lane of the softmax rows: lane = q * np + s
   const int sl = lane & (np - 1), ql = lane / np;
   const bool own = sl < N && ql < Q;
+  // this lane's logits row pointers, picked once (loop-invariant)
+  const void* lrow = p1_pick<SB>(p.lsrc, sl);
+  const float* glrow = p1_pick<QB>(p.glse, ql);
+  void* dlrow = p1_pick<SB>(p.dlsrc, sl);
 
   const int64_t t0 = (int64_t)xcd_block(blockIdx.x, gridDim.x) * kP1FastWaves + wave;  // XCD-major: logits / lse lines
   for (int64_t tok = t0; tok < p.n_tok; tok += (int64_t)gridDim.x * kP1FastWaves) {
@@ -57,7 +61,7 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
     }
     // ---- softmax rows in the (site, source) lane layout
-    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
+    const float l = own ? load_any(lrow, (int64_t)ql * p.lq + tok, p.ldt) : -INFINITY;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float wt = ex / group_sum(ex, np);
@@ -89,8 +93,8 @@ __global__ void __launch_bounds__(256) phase1_bwd_fast_kernel(const Phase1Params
       const float dwb = DT::rnd(dw);  // gradient of the dtype-rounded weights
       const float inner = group_sum(own ? wt * dwb : 0.f, np);
       float dl = wt * (dwb - inner);
-      dl = p1_dlogit(p, dl, own ? p1_glse(p, ql, tok) * wt : 0.f);
-      if (own) p1_store_dlogit(p, ql, sl, tok, dl);
+      dl = p1_dlogit(p, dl, own ? (glrow ? glrow[tok] : 0.f) * wt : 0.f);
+      if (own) store_any(dlrow, (int64_t)ql * p.dlq + tok, p.ldt, dl);
     }
 
     // ---- dv[s] = rnd(sum_q rnd(w[q, s]) g[q]): upstream rows interleaved by
@@ -151,6 +155,8 @@ __global__ void __launch_bounds__(256) phase1_fwd_fast_kernel(const Phase1Params
   const int N = p.n_src, Q = p.n_q, D = p.D, np = p.np;
   const int sl = lane & (np - 1), ql = lane / np;
   const bool own = sl < N && ql < Q;
+  // this lane's logits row pointers, picked once (loop-invariant)
+  const void* lrow = p1_pick<SB>(p.lsrc, sl);
 
   const int64_t t0 = (int64_t)xcd_block(blockIdx.x, gridDim.x) * kP1FastWaves + wave;  // XCD-major: logits / lse lines
   for (int64_t tok = t0; tok < p.n_tok; tok += (int64_t)gridDim.x * kP1FastWaves) {
@@ -163,7 +169,7 @@ __global__ void __launch_bounds__(256) phase1_fwd_fast_kernel(const Phase1Params
       for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(vp + (c * kWave + lane) * E, vr[s][c]);
     }
     // softmax rows and lse in the (site, source) lane layout
-    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
+    const float l = own ? load_any(lrow, (int64_t)ql * p.lq + tok, p.ldt) : -INFINITY;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float z = group_sum(ex, np);
@@ -228,7 +234,7 @@ __global__ void __launch_bounds__(256) phase1_fwd_fast_kernel(const Phase1Params
 // [Q, n] are token-minor, so neighbouring tokens share their cache lines.
 constexpr int kP1SplitCols = 256;  // columns per wave (64 lanes x 4 elements)
 
-template <class DT, int QB, int SB>
+template <class DT, int QB, int SB, bool ST>
 __global__ void __launch_bounds__(512) phase1_fwd_split_kernel(const Phase1Params p) {
   using S = typename DT::S;
   static_assert(QB * SB <= 64 && SB % 2 == 0, "one (site, source) pair per lane, sources in pairs");
@@ -240,6 +246,9 @@ __global__ void __launch_bounds__(512) phase1_fwd_split_kernel(const Phase1Param
   const int N = p.n_src, Q = p.n_q, D = p.D, np = p.np;
   const int sl = lane & (np - 1), ql = lane / np;
   const bool own = sl < N && ql < Q;
+  // this lane's logits row pointer (loop-invariant), as in the backward
+  const void* lrow = ST ? p.lsrc[0] : p1_pick<SB>(p.lsrc, sl);
+  const int64_t loff = ST ? (int64_t)sl * p.ls : 0;
   const int col = chunk * kP1SplitCols + lane * 4;
   for (int64_t tok = xcd_block(blockIdx.x, gridDim.x); tok < p.n_tok; tok += gridDim.x) {
     Raw<DT, 4> vr[SB];
@@ -248,7 +257,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_split_kernel(const Phase1Param
       const int j = min(s, N - 1);
       load_raw<DT, 4, true>((const S*)p.val[j] + tok * (int64_t)p.vstride[j] + col, vr[s]);
     }
-    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
+    const float l = own ? load_any(lrow, loff + (int64_t)ql * p.lq + tok, p.ldt) : -INFINITY;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float z = group_sum(ex, np);
@@ -290,7 +299,7 @@ __global__ void __launch_bounds__(512) phase1_fwd_split_kernel(const Phase1Param
   }
 }
 
-template <class DT, int QB, int SB>
+template <class DT, int QB, int SB, bool ST>
 __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Params p) {
   using S = typename DT::S;
   static_assert(QB * SB <= 64 && QB % 2 == 0 && SB % 2 == 0, "one (site, source) pair per lane");
@@ -304,19 +313,29 @@ __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Param
   const int N = p.n_src, Q = p.n_q, D = p.D, np = p.np;
   const int sl = lane & (np - 1), ql = lane / np;
   const bool own = sl < N && ql < Q;
+  // this lane's logits row pointers (loop-invariant): from entry 0 and the
+  // strides when the tables are stacked, else picked from the tables
+  const void* lrow = ST ? p.lsrc[0] : p1_pick<SB>(p.lsrc, sl);
+  const int64_t loff = ST ? (int64_t)sl * p.ls : 0;
+  const float* glrow = ST ? p.glse[0] : p1_pick<QB>(p.glse, ql);
+  const int64_t goff = ST ? (int64_t)ql * p.glq : 0;
+  void* dlrow = ST ? p.dlsrc[0] : p1_pick<SB>(p.dlsrc, sl);
+  const int64_t doff = ST ? (int64_t)sl * p.dls : 0;
   const int col = chunk * kP1SplitCols + lane * 4;
   for (int64_t tok = xcd_block(blockIdx.x, gridDim.x); tok < p.n_tok; tok += gridDim.x) {
     Raw<DT, 4> gr[QB], vr[SB];
 #pragma unroll
     for (int q = 0; q < QB; ++q)
-      load_raw<DT, 4, true>((const S*)p.gout[min(q, Q - 1)] + tok * (int64_t)D + col, gr[q]);
+      load_raw<DT, 4, true>((ST ? (const S*)p.gout[0] + (int64_t)min(q, Q - 1) * p.gq : (const S*)p.gout[min(q, Q - 1)]) +
+                                tok * (int64_t)D + col,
+                            gr[q]);
 #pragma unroll
     for (int s = 0; s < SB; ++s) {
       const int j = min(s, N - 1);
       load_raw<DT, 4, true>((const S*)p.val[j] + tok * (int64_t)p.vstride[j] + col, vr[s]);
     }
-    const float l = own ? p1_logit(p, ql, sl, tok) : -INFINITY;
-    const float glse = own ? p1_glse(p, ql, tok) : 0.f;
+    const float l = own ? load_any(lrow, loff + (int64_t)ql * p.lq + tok, p.ldt) : -INFINITY;
+    const float glse = own ? (glrow ? glrow[goff + tok] : 0.f) : 0.f;
     const float lm = group_max(l, np);
     const float ex = own ? expf(l - lm) : 0.f;
     const float wt = ex / group_sum(ex, np);
@@ -358,7 +377,7 @@ __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Param
       const float inner = group_sum(own ? wt * dwb : 0.f, np);
       float dl = wt * (dwb - inner);
       dl = p1_dlogit(p, dl, own ? glse * wt : 0.f);
-      if (chunk == 0 && own) p1_store_dlogit(p, ql, sl, tok, dl);
+      if (chunk == 0 && own) store_any(dlrow, doff + (int64_t)ql * p.dlq + tok, p.ldt, dl);
     }
 
     // dv[s] = rnd(sum_q rnd(w[q, s]) g[q]) over this wave's columns: upstream
@@ -403,9 +422,14 @@ __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Param
 template <class DT, bool BWD>
 static hipError_t phase1_split_dt(const Phase1Params& p, const Launch& L, hipStream_t st) {
   const dim3 g(L.grid), b(L.wpt * kWave);
-#define ATTNRES_P1S(QB, SB)                                                                        \
-  if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_split_kernel<DT, QB, SB>), g, b, 0, st, p); \
-  else hipLaunchKernelGGL((phase1_fwd_split_kernel<DT, QB, SB>), g, b, 0, st, p);
+#define ATTNRES_P1S(QB, SB)                                                                               \
+  if (p.stacked) {                                                                                        \
+    if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_split_kernel<DT, QB, SB, true>), g, b, 0, st, p);    \
+    else hipLaunchKernelGGL((phase1_fwd_split_kernel<DT, QB, SB, true>), g, b, 0, st, p);                  \
+  } else {                                                                                                \
+    if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_split_kernel<DT, QB, SB, false>), g, b, 0, st, p);   \
+    else hipLaunchKernelGGL((phase1_fwd_split_kernel<DT, QB, SB, false>), g, b, 0, st, p);                 \
+  }
   switch (L.nmax) {
     case 2: ATTNRES_P1S(16, 2) break;
     case 4: ATTNRES_P1S(16, 4) break;
