@@ -90,6 +90,9 @@ def parse_args(argv=None):
     p.add_argument("--graph", type=_bool, default=False,
                    help="train steps with everything after the embedding lookup replayed from HIP graphs "
                         "(torch.cuda.make_graphed_callables); the lookup, its backward and the update stay eager")
+    p.add_argument("--tunable_gemm", type=_bool, default=False,
+                   help="let PyTorch's TunableOp pick the library GEMM kernels by timing them (both cases; the "
+                        "tuning runs in the warmup steps, results kept in a file under $TMPDIR)")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args(argv)
 
@@ -272,6 +275,12 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
     targets = torch.randint(0, args.vocab_size, (batch, args.block_size), device=device, generator=gen)
 
     graph_check = None
+    if args.tunable_gemm and args.phase == "train":
+        # one eager step first: it meets every GEMM shape, so the tuning happens
+        # here rather than inside the graph warmup
+        train_step(args, model, idx, targets)
+        torch.cuda.synchronize()
+        print(f"# {label}: GEMM tuning step done", flush=True)
     if args.phase == "forward":
         def step():
             with torch.inference_mode():
@@ -287,8 +296,11 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
             train_step(args, model, idx, targets)
 
     try:
-        for _ in range(args.warmup):
+        for i in range(args.warmup):
             step()
+            if args.tunable_gemm:  # GEMM tuning makes the first steps long: say where the run is
+                torch.cuda.synchronize()
+                print(f"# {label}: warmup step {i + 1}/{args.warmup} done", flush=True)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -331,6 +343,17 @@ def main(argv=None):
     if not torch.cuda.is_available():
         raise RuntimeError("a ROCm GPU is required for this benchmark")
     device = torch.device("cuda")
+    if args.tunable_gemm:
+        # TunableOp times the candidate GEMM solutions of each new shape once
+        # and keeps the fastest: the fused [out | key] projections are d + r
+        # wide (1056 at d1024 r32), a width the default choice fits badly
+        import tempfile
+
+        torch.cuda.tunable.set_filename(os.path.join(tempfile.gettempdir(), "attnres_tunableop.csv"))
+        torch.cuda.tunable.set_max_tuning_duration(10)
+        torch.cuda.tunable.set_max_tuning_iterations(20)
+        torch.cuda.tunable.tuning_enable(True)
+        torch.cuda.tunable.enable(True)
     dtype = resolve_dtype(args.dtype)
     batches = [int(x) for x in args.batch_sizes.split(",") if x.strip()]
     ranks = [int(x) for x in args.lrid_ranks.split(",") if x.strip()]
@@ -342,7 +365,7 @@ def main(argv=None):
     print(f"dtype={args.dtype} phase={args.phase} loss={args.loss} optimizer_step={args.optimizer_step} "
           f"n_layer={args.n_layer} n_embd={args.n_embd} n_head={args.n_head} vocab={args.vocab_size} "
           f"T={args.block_size} blocks={args.attnres_num_blocks} fold_block_summary={args.fold_block_summary} "
-          f"graph={args.graph} "
+          f"graph={args.graph} tunable_gemm={args.tunable_gemm} "
           f"torch={torch.__version__} device={torch.cuda.get_device_name(0)}", flush=True)
     print("case,batch,rank,latency_ms,overhead_vs_baseline_pct,tokens_per_s,attnres_kernel_ms,"
           "attnres_kernel_share_pct", flush=True)
@@ -378,6 +401,7 @@ def main(argv=None):
                              args.attnres_num_blocks) == (12, 768, 12, 100277, 1024, 6) else "custom",
         "phase": args.phase, "loss": args.loss, "optimizer_step": args.optimizer_step, "dtype": args.dtype,
         "graph": bool(args.graph and args.phase == "train"),
+        "tunable_gemm": bool(args.tunable_gemm),
         "data": "synthetic (uniform random token ids, random init)",
         "cases": summary,
     }), flush=True)
