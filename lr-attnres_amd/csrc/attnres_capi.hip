@@ -349,7 +349,7 @@ bool lr_fast_plan(const attnres_read_desc* d, const Plan& pl, bool backward, Fas
   // slices) is instantiated for slot counts close together.
   f->nb = N <= 8 ? 8 : N <= 16 ? 16 : 32;
   if (f->cb == 1 && f->rhc == 2) {
-    static const int kFineSlots[] = {8, 12, 14, 16, 20, 24, 32};
+    static const int kFineSlots[] = {8, 12, 14, 16, 18, 20, 24, 32};
     for (int nb : kFineSlots)
       if (N <= nb) {
         f->nb = nb;

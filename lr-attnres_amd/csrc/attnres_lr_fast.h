@@ -844,7 +844,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
 
 // Launch switch shared by the forward and backward translation units:
 // L.vec = value vector bytes (16), L.wpt = columns per item (1/2), L.nmax =
-// source slots (8/16/32; also 12/14/20/24 for one column and two key chunks),
+// source slots (8/16/32; also 12/14/18/20/24 for one column and two key chunks),
 // L.teams = key chunks per head slot (2/8); FEATV is the FEAT set.
 #define ATTNRES_FAST_SWITCH(fn, P, FEATV)                            \
   switch (L.vec * 10000 + L.wpt * 1000 + L.nmax * 10 + L.teams) {     \
@@ -852,6 +852,7 @@ __global__ void __launch_bounds__(256) lr_bwd_fast_kernel(const ReadBwdParams bp
     case 161122: return fn<DT, 16, 1, 12, 2, FEATV>(P, L, st);       \
     case 161142: return fn<DT, 16, 1, 14, 2, FEATV>(P, L, st);       \
     case 161162: return fn<DT, 16, 1, 16, 2, FEATV>(P, L, st);       \
+    case 161182: return fn<DT, 16, 1, 18, 2, FEATV>(P, L, st);       \
     case 161202: return fn<DT, 16, 1, 20, 2, FEATV>(P, L, st);       \
     case 161242: return fn<DT, 16, 1, 24, 2, FEATV>(P, L, st);       \
     case 161322: return fn<DT, 16, 1, 32, 2, FEATV>(P, L, st);       \

@@ -27,7 +27,8 @@ constexpr int kPhase1SplitGroups = 65536;  // phase-1 split kernels: at most thi
 // kernels assume it, so their per-slot branches below it fold away.
 __host__ __device__ constexpr int lr_fast_slot_floor(int cb, int rhc, int nb) {
   if (cb == 1 && rhc == 2)
-    return nb <= 8 ? 1 : nb <= 12 ? 9 : nb <= 14 ? 13 : nb <= 16 ? 15 : nb <= 20 ? 17 : nb <= 24 ? 21 : 25;
+    return nb <= 8 ? 1 : nb <= 12 ? 9 : nb <= 14 ? 13 : nb <= 16 ? 15 : nb <= 18 ? 17 : nb <= 20 ? 19 : nb <= 24 ? 21
+                                                                                                             : 25;
   return nb <= 8 ? 1 : nb <= 16 ? 9 : 17;
 }
 
