@@ -203,6 +203,23 @@ def test_static_key_workspace_is_checked_before_any_launch():
     assert f"workspace of {need} bytes needed, got {rows}".encode() in lib.attnres_last_error()
 
 
+@needs_lib
+def test_noalloc_backward_refuses_descriptions_beyond_its_scratch():
+    """The no-allocation backward checks the partial-sum size against its fixed
+    per-device array before it looks the array up or launches anything."""
+    lib = H.load()
+    d = _desc(n_src=64, n_tok=1 << 20, dim=8192, rank=0, heads=1)  # base read: 64 x 8192 fp32 partials per group
+    need = lib.attnres_read_backward_workspace_size(ctypes.byref(d))
+    assert need > H.NOALLOC_SCRATCH_BYTES
+    g = H.ReadGrads()
+    dv = (ctypes.c_void_p * 64)(*([0x8000] * 64))
+    g.grad_out, g.weights, g.dvalues = 0x9000, ctypes.cast(ctypes.c_void_p(0xa000), ctypes.POINTER(ctypes.c_float)), dv
+    g.dquery = 0xc000
+    assert lib.attnres_read_backward_noalloc(ctypes.byref(d), ctypes.byref(g), None) == -4
+    err = lib.attnres_last_error()
+    assert f"needs {need} bytes of partial sums".encode() in err and b"holds 33554432" in err
+
+
 def test_static_keys_shape_is_checked_on_the_host():
     vs = [torch.randn(1, 2, 8) for _ in range(3)]
     ks = [torch.randn(1, 2, 4) for _ in range(3)]
