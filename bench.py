@@ -26,6 +26,7 @@ import ctypes
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -231,7 +232,9 @@ def bench_phase(args, dev):
     bpt = phase_bytes_per_token(c)
     kern = {}
     for k in parts:
-        ms = sum(a.elapsed_time(b) for a, b in ev[k]) / args.steps
+        # median over the steps: a pair that spans a gap in the host's
+        # submission (the GPU idle between the two events) would skew a mean
+        ms = statistics.median(a.elapsed_time(b) for a, b in ev[k])
         calls = c["Q"] if k.startswith(("phase2", "accum")) else 1
         gbs = bpt[k] * wl.n_tok * calls / (ms / 1e3) / 1e9
         kern[k] = {"ms": round(ms, 5), "calls": calls, "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),

@@ -1089,9 +1089,17 @@ bool phase1_fast(const attnres_phase1_desc* d, const PhasePlan& pl, Launch* L) {
   if (d->dim != 256 && d->dim != 512 && d->dim != 768 && d->dim != 1024) return false;
   L->vb = (d->dim == 256 || d->dim == 768) ? 8 : 16;
   L->wpt = d->dim / (kWaveSize * (L->vb / 2));
-  L->nmax = d->n_src <= 4 ? 4 : 8;
-  const int64_t streams = d->n_tok < base_fast_streams() ? d->n_tok : base_fast_streams();
-  L->grid = (int)((streams + 3) / 4);
+  // source slots: the count rounded up to a pair (the forward mixes sources
+  // in pairs); a slot past n_src is a wasted row load and its dot products
+  // (p5's six sources in eight slots cost the backward 3 waves per SIMD)
+  L->nmax = d->n_src <= 2 ? 2 : (d->n_src + 1) / 2 * 2;
+  // one token per wave: no cross-token sums here, and fresh waves balance the
+  // CUs better than a resident round walking four tokens each (p5: forward
+  // 50.5 -> 49.2 us, backward 79.9 -> 77.2 us at 16384 tokens)
+  // (the kernels stride over tokens, so the grid may stop short: at most 2^22
+  // workgroups keep the launch's work-item count within 32 bits)
+  const int64_t groups = (d->n_tok + 3) / 4;
+  L->grid = (int)(groups < (1 << 22) ? groups : (1 << 22));
   return true;
 }
 

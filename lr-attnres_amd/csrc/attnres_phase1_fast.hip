@@ -453,24 +453,24 @@ hipError_t launch_phase1_split_backward(int dtype, const Phase1Params& p, const 
 }
 
 // L.vb = vector bytes (8/16), L.wpt = columns per lane (1/2/3), L.nmax =
-// source slots (4/8)
+// source slots (2/4/6/8: the source count rounded up to a pair)
 template <class DT, bool BWD>
 static hipError_t phase1_fast_dt(const Phase1Params& p, const Launch& L, hipStream_t st) {
   const dim3 g(L.grid), b(kP1FastWaves * kWave);
-#define ATTNRES_P1F(VB, CB, SB)                                                                \
-  if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, VB, CB, SB>), g, b, 0, st, p); \
-  else hipLaunchKernelGGL((phase1_fwd_fast_kernel<DT, VB, CB, SB>), g, b, 0, st, p);
-  switch (L.vb * 100 + L.wpt * 10 + L.nmax / 4) {
-    case 811: ATTNRES_P1F(8, 1, 4) break;
-    case 812: ATTNRES_P1F(8, 1, 8) break;
-    case 831: ATTNRES_P1F(8, 3, 4) break;
-    case 832: ATTNRES_P1F(8, 3, 8) break;
-    case 1611: ATTNRES_P1F(16, 1, 4) break;
-    case 1612: ATTNRES_P1F(16, 1, 8) break;
-    case 1621: ATTNRES_P1F(16, 2, 4) break;
-    case 1622: ATTNRES_P1F(16, 2, 8) break;
+#define ATTNRES_P1F(VB, CB, SB)                                                                    \
+  case VB * 100 + CB * 10 + SB:                                                                    \
+    if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_fast_kernel<DT, VB, CB, SB>), g, b, 0, st, p); \
+    else hipLaunchKernelGGL((phase1_fwd_fast_kernel<DT, VB, CB, SB>), g, b, 0, st, p);             \
+    break;
+#define ATTNRES_P1F_SB(VB, CB) ATTNRES_P1F(VB, CB, 2) ATTNRES_P1F(VB, CB, 4) ATTNRES_P1F(VB, CB, 6) ATTNRES_P1F(VB, CB, 8)
+  switch (L.vb * 100 + L.wpt * 10 + L.nmax) {
+    ATTNRES_P1F_SB(8, 1)
+    ATTNRES_P1F_SB(8, 3)
+    ATTNRES_P1F_SB(16, 1)
+    ATTNRES_P1F_SB(16, 2)
     default: return hipErrorInvalidValue;
   }
+#undef ATTNRES_P1F_SB
 #undef ATTNRES_P1F
   return hipGetLastError();
 }
