@@ -67,7 +67,8 @@ def _both(y, pv, pk, D, R, heads, key_norm, g_value, g_key, **kw):
 
 
 SHAPES = [
-    (768, 64, 64, 1, True),     # the whole-model configuration
+    (768, 64, 64, 1, True),     # the whole-model configuration (16-bit: three columns of 8-byte vectors)
+    (256, 32, 32, 2, True),     # 16-bit: one column of 8-byte vectors
     (1024, 64, 64, 4, True),    # per-head norm
     (2048, 128, 128, 1, True),  # 128-column head
     (768, 32, 48, 1, False),    # padding columns, no key norm
