@@ -234,17 +234,18 @@ def kernel_category(name):
 
 def kernel_share(step, iters):
     """(attnres kernel µs per step, all kernels µs per step, µs per step by
-    KERNEL_CATEGORIES) from torch.profiler, or (None, None, None)."""
+    KERNEL_CATEGORIES, kernel launches per step by category) from
+    torch.profiler, or Nones."""
     try:
         from torch.profiler import ProfilerActivity, profile
     except ImportError:
-        return None, None, None
+        return None, None, None, None
     with profile(activities=[ProfilerActivity.CUDA]) as prof:
         for _ in range(iters):
             step()
         torch.cuda.synchronize()
     total = attn = 0.0
-    cats = {}
+    cats, counts = {}, {}
     for ev in prof.key_averages():
         t = _device_time_us(ev)
         if t == 0.0:
@@ -254,9 +255,11 @@ def kernel_share(step, iters):
             attn += t
         c = kernel_category(ev.key)
         cats[c] = cats.get(c, 0.0) + t
+        counts[c] = counts.get(c, 0) + ev.count
     if total == 0.0:
-        return None, None, None
-    return attn / iters, total / iters, {k: v / iters for k, v in sorted(cats.items())}
+        return None, None, None, None
+    return (attn / iters, total / iters, {k: v / iters for k, v in sorted(cats.items())},
+            {k: v / iters for k, v in sorted(counts.items())})
 
 
 def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
@@ -310,9 +313,9 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
         end.record()
         torch.cuda.synchronize()
         latency_ms = start.elapsed_time(end) / args.iters
-        attn_us = total_us = cats_us = None
+        attn_us = total_us = cats_us = counts = None
         if args.profile_iters > 0:
-            attn_us, total_us, cats_us = kernel_share(step, args.profile_iters)
+            attn_us, total_us, cats_us, counts = kernel_share(step, args.profile_iters)
         n_params = model.get_num_params()
     finally:
         del model, idx, targets
@@ -328,6 +331,7 @@ def measure_case(args, device, dtype, batch, label, use_attnres, rank=None):
         "attnres_kernel_ms": None if attn_us is None else attn_us / 1000.0,
         "device_kernel_ms": None if total_us is None else total_us / 1000.0,
         "device_ms_by_category": None if cats_us is None else {k: v / 1000.0 for k, v in cats_us.items()},
+        "kernels_by_category": counts,
         "params": n_params,
         "graph": bool(args.graph and args.phase == "train"),
         "graph_check": graph_check,
@@ -390,6 +394,11 @@ def main(argv=None):
             row["device_ms_delta_by_category"] = (None if bc is None or rc is None else
                                                   {k: rc.get(k, 0.0) - bc.get(k, 0.0)
                                                    for k in sorted(set(bc) | set(rc))})
+            # and the extra kernel launches (each costs a graph node's dispatch too)
+            bn = None if base is None else base.get("kernels_by_category")
+            rn = row.get("kernels_by_category")
+            row["kernels_delta_by_category"] = (None if bn is None or rn is None else
+                                                {k: rn.get(k, 0) - bn.get(k, 0) for k in sorted(set(bn) | set(rn))})
             print(f"{row['label']},{row['batch']},{row['rank']},{row['latency_ms']:.3f},"
                   f"{_fmt(row['overhead_vs_baseline_pct'], '.2f')},{row['tokens_per_s']:.0f},"
                   f"{_fmt(row['attnres_kernel_ms'], '.3f')},{_fmt(row['attnres_kernel_share_pct'], '.2f')}",
