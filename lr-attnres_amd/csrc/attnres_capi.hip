@@ -1117,6 +1117,11 @@ bool phase1_split(const attnres_phase1_desc* d, const PhasePlan& pl, Phase1Param
   p->np = np;
   L->wpt = d->dim / 256;
   L->nmax = np;
+  // site slots: a site past n_q loads an upstream row and computes S row dot
+  // products for nothing (the published block's 12 sites in 16 slots cost the
+  // backward a quarter of its upstream loads and dot products)
+  const int q = d->n_q;
+  L->teams = q <= 4 ? 4 : q <= 6 ? 6 : q <= 8 ? 8 : q <= 12 ? 12 : 16;
   L->grid = (int)(d->n_tok < kPhase1SplitGroups ? d->n_tok : kPhase1SplitGroups);
   return true;
 }

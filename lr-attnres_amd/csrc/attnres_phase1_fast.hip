@@ -304,7 +304,9 @@ __global__ void __launch_bounds__(512) phase1_bwd_split_kernel(const Phase1Param
   using S = typename DT::S;
   static_assert(QB * SB <= 64 && QB % 2 == 0 && SB % 2 == 0, "one (site, source) pair per lane");
   constexpr int V = QB * SB;                 // row dot products per token (multiple of 4)
-  constexpr int VB16 = V < 16 ? V : 16;      // reduced 16 at a time
+  // reduced 16 at a time (12 when V = 24; V itself up to 16)
+  constexpr int VB16 = V <= 16 ? V : V % 16 == 0 ? 16 : 12;
+  static_assert(V % VB16 == 0 && VB16 % 4 == 0, "the row dot products reduce in whole groups of four");
   __shared__ float s_dw[8][64];              // [wave][pair]: this wave's partial dW of pair (q, s) = q * SB + s
   __shared__ uint16_t s_wh[8][64];           // [wave][s * QB + q]: rounded weights, 16-bit
   const int lane = threadIdx.x & (kWave - 1);
@@ -430,11 +432,23 @@ static hipError_t phase1_split_dt(const Phase1Params& p, const Launch& L, hipStr
     if constexpr (BWD) hipLaunchKernelGGL((phase1_bwd_split_kernel<DT, QB, SB, false>), g, b, 0, st, p);   \
     else hipLaunchKernelGGL((phase1_fwd_split_kernel<DT, QB, SB, false>), g, b, 0, st, p);                 \
   }
-  switch (L.nmax) {
-    case 2: ATTNRES_P1S(16, 2) break;
-    case 4: ATTNRES_P1S(16, 4) break;
-    case 8: ATTNRES_P1S(8, 8) break;
-    case 16: ATTNRES_P1S(4, 16) break;
+  // L.nmax = source lanes np, L.teams = site slots (the site count rounded up
+  // to 4, 6, 8, 12 or 16 within np * slots <= 64)
+  switch (L.nmax * 100 + L.teams) {
+    case 204: ATTNRES_P1S(4, 2) break;
+    case 206: ATTNRES_P1S(6, 2) break;
+    case 208: ATTNRES_P1S(8, 2) break;
+    case 212: ATTNRES_P1S(12, 2) break;
+    case 216: ATTNRES_P1S(16, 2) break;
+    case 404: ATTNRES_P1S(4, 4) break;
+    case 406: ATTNRES_P1S(6, 4) break;
+    case 408: ATTNRES_P1S(8, 4) break;
+    case 412: ATTNRES_P1S(12, 4) break;
+    case 416: ATTNRES_P1S(16, 4) break;
+    case 804: ATTNRES_P1S(4, 8) break;
+    case 806: ATTNRES_P1S(6, 8) break;
+    case 808: ATTNRES_P1S(8, 8) break;
+    case 1604: ATTNRES_P1S(4, 16) break;
     default: return hipErrorInvalidValue;
   }
 #undef ATTNRES_P1S
