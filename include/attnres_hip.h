@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 7
+#define ATTNRES_ABI_VERSION 8
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -405,6 +405,14 @@ typedef struct attnres_phase2_grads {
   float* dvalue_scale;         /* fp32 scalar, or NULL */
   void* workspace;             /* for the cross-token sums */
   size_t workspace_bytes;
+  /* dquery as one row of a query bank (ABI 8; zero = the query's own
+     gradient): with dquery_rows > 1, dquery points at a [dquery_rows, rank]
+     (or [dquery_rows, dim]) table whose row dquery_row receives the query's
+     gradient and whose other rows are set to zero -- the gradient a row
+     select of the bank would hand back (the block decoder reads site i's
+     query as row i - 1 of one table), without a separate fill and copy. */
+  int32_t dquery_rows;
+  int32_t dquery_row;
 } attnres_phase2_grads;
 
 /*

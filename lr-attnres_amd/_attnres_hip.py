@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_SOURCES = 64
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -186,6 +186,8 @@ class Phase2Grads(ctypes.Structure):
         ("dvalue_scale", POINTER(c_float)),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("dquery_rows", c_int32),
+        ("dquery_row", c_int32),
     ]
 
 
@@ -736,9 +738,10 @@ def phase2_forward(desc: Phase2, device, dtype):
 
 
 def phase2_backward(desc: Phase2, device, dtype, grad_out, want_dquery, query_shape, logit_dtype, want_dbias,
-                    want_dscale):
+                    want_dscale, query_row=None):
     """Returns (dpartial, dpartial_key | None, dquery | None, dinter, dlse, dlogit | None, dbias | None,
-    dscale | None)."""
+    dscale | None).  With query_row, query_shape is a bank's [rows, width] and dquery the bank's
+    gradient: the query's gradient in row query_row, zeros elsewhere."""
     lib = load()
     n, D, R = desc.n_tok, desc.D, desc.R
     lr = R > 0
@@ -760,6 +763,9 @@ def phase2_backward(desc: Phase2, device, dtype, grad_out, want_dquery, query_sh
     g.dpartial_logit = dlg.data_ptr() if dlg is not None else None
     g.dlogit_bias = _fptr(db)
     g.dvalue_scale = _fptr(ds)
+    if dq is not None and query_row is not None:
+        g.dquery_rows = int(query_shape[0])
+        g.dquery_row = int(query_row)
     ws_bytes = lib.attnres_phase2_backward_workspace_size(ctypes.byref(desc.c))
     ws = torch.empty((max(int(ws_bytes), 1),), device=device, dtype=torch.uint8)
     g.workspace = ws.data_ptr()

@@ -491,15 +491,17 @@ class Decoder(nn.Module):
             inter, lse = phase[2][i], phase[3][i]
             if partial is None:
                 return norm(inter) if fused_norm else inter
-            q = queries[site - 1]
+            # site i reads row i - 1 of the query bank; the merge takes the bank and
+            # the row, so the bank's gradient comes back without a select's fill and copy
             pkey = partial_key.reshape(partial_key.size(0), partial_key.size(1), rank)
             if c.fold_block_summary:
-                return phase2(partial, pkey, q, inter, lse, c.lrid_logit_scale, c.attnres_key_norm,
+                return phase2(partial, pkey, queries, inter, lse, c.lrid_logit_scale, c.attnres_key_norm,
                               normalize_output=fused_norm, logit_bias=self._count_bias(count),
-                              partial_scale=self._block_scale(count), scale_key=not c.attnres_key_norm)
+                              partial_scale=self._block_scale(count), scale_key=not c.attnres_key_norm,
+                              query_row=site - 1)
             value, key = summary(partial, pkey, count)
-            return phase2(value, key, q, inter, lse, c.lrid_logit_scale, c.attnres_key_norm,
-                          normalize_output=fused_norm, logit_bias=self._count_bias(count))
+            return phase2(value, key, queries, inter, lse, c.lrid_logit_scale, c.attnres_key_norm,
+                          normalize_output=fused_norm, logit_bias=self._count_bias(count), query_row=site - 1)
 
         def add(out: Tensor, key: Optional[Tensor], site_after: int):
             nonlocal partial, partial_key, count, phase

@@ -1031,9 +1031,11 @@ class _Phase2Fn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, meta, partial_value, inter, lse, *opt_flat):
-        has, merge, key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key = meta
+        has, merge, key_norm, normalize_output, logit_scale, bias_value, scale_value, scale_key, qrow = meta
         partial_key, query, partial_logit, bias_t, scale_t = _unflatten_opt(has, opt_flat)
-        desc = _hip.Phase2(partial_value, partial_key, query, partial_logit, inter, lse, merge, key_norm,
+        # query_row: `query` is a bank and the merge reads one of its rows (a view)
+        qd = query[qrow] if qrow is not None else query
+        desc = _hip.Phase2(partial_value, partial_key, qd, partial_logit, inter, lse, merge, key_norm,
                            normalize_output, logit_scale, bias_value, bias_t, scale_value, scale_t, scale_key)
         dev = partial_value.device
         with _device_ctx(dev):
@@ -1064,10 +1066,10 @@ class _Phase2Fn(torch.autograd.Function):
         with _device_ctx(dev):
             dp, dpk, dq, di, dl, dlg, db, ds = _hip.phase2_backward(
                 ctx.desc, dev, partial_value.dtype, grad_out.contiguous(),
-                want_dquery=query is not None and partial_logit is None,
+                want_dquery=query is not None and partial_logit is None and want[pos["q"]],
                 query_shape=tuple(query.shape) if query is not None else (0,),
                 logit_dtype=partial_logit.dtype if partial_logit is not None else None,
-                want_dbias=want_dbias, want_dscale=want_dscale)
+                want_dbias=want_dbias, want_dscale=want_dscale, query_row=ctx.meta[-1])
         grads = [None, dp if want[1] else None, di if want[2] else None, dl if want[3] else None]
         for name, g in (("pk", dpk), ("q", dq), ("pl", dlg), ("b", db), ("s", ds)):
             if name in pos:
@@ -1092,7 +1094,7 @@ def _scalar_arg(x, device, what):
 
 
 def _phase2(partial_value, partial_key, query, partial_logit, interblock_output, interblock_lse, merge, key_norm,
-            normalize_output, logit_scale, logit_bias, partial_scale, scale_key, what):
+            normalize_output, logit_scale, logit_bias, partial_scale, scale_key, what, query_row=None):
     if partial_value.dim() != 3:
         raise RuntimeError(f"{what}: partial_value must be [B, T, D]")
     B, T, D = partial_value.shape
@@ -1120,10 +1122,20 @@ def _phase2(partial_value, partial_key, query, partial_logit, interblock_output,
             raise RuntimeError(f"{what}: partial_logit must be [B, T]")
         pl = partial_logit.reshape(B * T).contiguous()
     elif partial_key is not None:
-        pk = _rows2d(partial_key.reshape(B, T, -1).to(dtype))
-        q = query.reshape(-1).to(dtype).contiguous()
-        if q.numel() != pk.size(1):
-            raise RuntimeError(f"{what}: query must have {pk.size(1)} elements, got {q.numel()}")
+        pk = _rows2d(partial_key.reshape(B, T, partial_key.size(-1)).to(dtype))
+        if query_row is not None:
+            # a bank [rows, width] and the row this merge reads
+            if query.dim() != 2 or query.size(1) != pk.size(1):
+                raise RuntimeError(f"{what}: a query bank must be [rows, {pk.size(1)}], got {tuple(query.shape)}")
+            if not 0 <= int(query_row) < query.size(0):
+                raise RuntimeError(f"{what}: query_row={query_row} outside [0, {query.size(0)})")
+            q = query.to(dtype).contiguous()
+            if _compiling():  # the custom op takes one row: select it
+                q, query_row = q[int(query_row)], None
+        else:
+            q = query.reshape(-1).to(dtype).contiguous()
+            if q.numel() != pk.size(1):
+                raise RuntimeError(f"{what}: query must have {pk.size(1)} elements, got {q.numel()}")
     else:
         q = query.reshape(-1).to(dtype).contiguous()
         if q.numel() != D:
@@ -1134,7 +1146,8 @@ def _phase2(partial_value, partial_key, query, partial_logit, interblock_output,
     else:
         opt = (pk, q, pl, bias_t, scale_t)
         meta = (tuple(t is not None for t in opt), int(merge), bool(key_norm), bool(normalize_output),
-                float(logit_scale), bias_value, scale_value, bool(scale_key))
+                float(logit_scale), bias_value, scale_value, bool(scale_key),
+                None if query_row is None else int(query_row))
         out = _Phase2Fn.apply(meta, pv, it, lse, *[t for t in opt if t is not None])
     return out.view(B, T, D)
 
@@ -1175,25 +1188,33 @@ def attention_residual_phase2_from_logit(partial_value: Tensor, partial_logit: T
 def lrid_attention_residual_phase2(partial_value: Tensor, partial_key: Tensor, query: Tensor,
                                    interblock_output: Tensor, interblock_lse: Tensor, logit_scale: float,
                                    key_norm: bool, force_triton: bool = False, normalize_output: bool = False,
-                                   logit_bias=0.0, partial_scale=None, scale_key: bool = False) -> Tensor:
+                                   logit_bias=0.0, partial_scale=None, scale_key: bool = False,
+                                   query_row: Optional[int] = None) -> Tensor:
     """LR merge, ``addcmul`` form (reference: attnres_ops.py:4075-4139; single head).
 
     ``partial_scale`` multiplies the partial value (and, with ``scale_key``,
     the partial key) first: the LR block source of model.py:1003-1018.
+    ``query_row`` (an addition to the reference's signature): ``query`` is a
+    [rows, rank] bank and the merge reads row ``query_row``; the backward
+    hands the bank its gradient directly (the row's, zeros elsewhere), the
+    tensor ``query[query_row]``'s select would produce, without the select's
+    fill and copy launches.
     """
     return _phase2(partial_value, partial_key, query, None, interblock_output, interblock_lse, _hip.MERGE_ADDCMUL,
                    key_norm, normalize_output, logit_scale, logit_bias, partial_scale, scale_key,
-                   "lrid_attention_residual_phase2")
+                   "lrid_attention_residual_phase2", query_row)
 
 
 def lrid_attention_residual_phase2_torch(partial_value: Tensor, partial_key: Tensor, query: Tensor,
                                          interblock_output: Tensor, interblock_lse: Tensor, logit_scale: float,
                                          key_norm: bool, normalize_output: bool = False, logit_bias=0.0,
-                                         partial_scale=None, scale_key: bool = False) -> Tensor:
-    """LR merge, ``torch.lerp`` form (reference: attnres_ops.py:4142-4160), on the HIP kernel."""
+                                         partial_scale=None, scale_key: bool = False,
+                                         query_row: Optional[int] = None) -> Tensor:
+    """LR merge, ``torch.lerp`` form (reference: attnres_ops.py:4142-4160), on the HIP kernel
+    (``query_row`` as in lrid_attention_residual_phase2)."""
     return _phase2(partial_value, partial_key, query, None, interblock_output, interblock_lse, _hip.MERGE_LERP,
                    key_norm, normalize_output, logit_scale, logit_bias, partial_scale, scale_key,
-                   "lrid_attention_residual_phase2_torch")
+                   "lrid_attention_residual_phase2_torch", query_row)
 
 
 # ------------------------------------------------------------------ key-producer epilogue

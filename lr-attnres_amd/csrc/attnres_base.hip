@@ -369,7 +369,14 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
 #pragma unroll
       for (int v = 0; v < kWaves; ++v) t += sh[v][tid];
       if (slot >= rp.part_q && slot < rp.part_q + rp.n_q) {
-        if (rp.dquery) DT::store1((typename DT::S*)rp.dquery + (slot - rp.part_q), t);
+        if (rp.dquery) {
+          typename DT::S* dq = (typename DT::S*)rp.dquery + (slot - rp.part_q);
+          if (rp.q_rows > 1) {
+            for (int r = 0; r < rp.q_rows; ++r) DT::store1(dq + (int64_t)r * rp.n_q, r == rp.q_row ? t : 0.f);
+          } else {
+            DT::store1(dq, t);
+          }
+        }
       } else if (slot >= rp.part_gate && slot < rp.part_gate + rp.n_gate) {
         if (rp.dgate) DT::store1((typename DT::S*)rp.dgate + (slot - rp.part_gate), t);
       } else if (slot >= rp.part_bias && slot < rp.part_bias + rp.n_bias) {

@@ -1339,8 +1339,12 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
   if (!g) return fail(ATTNRES_EINVAL, "grads is NULL");
   const bool lr = d->rank > 0 && !d->logit_given;
   hipStream_t st = (hipStream_t)stream;
+  const int q_rows = g->dquery_rows > 1 ? g->dquery_rows : 1;
+  if (g->dquery_rows > 1 && (g->dquery_row < 0 || g->dquery_row >= g->dquery_rows))
+    return fail(ATTNRES_EINVAL, "dquery_row=%d outside [0, %d)", g->dquery_row, g->dquery_rows);
   if (d->n_tok == 0) {
-    if (g->dquery && !d->logit_given) zero_async(g->dquery, (size_t)(lr ? d->rank : d->dim) * elem_size(d->dtype), st);
+    if (g->dquery && !d->logit_given)
+      zero_async(g->dquery, (size_t)q_rows * (lr ? d->rank : d->dim) * elem_size(d->dtype), st);
     if (g->dlogit_bias) zero_async(g->dlogit_bias, sizeof(float), st);
     if (g->dvalue_scale) zero_async(g->dvalue_scale, sizeof(float), st);
     return ATTNRES_OK;
@@ -1418,6 +1422,8 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     rp.part_extra = PL.part_scale;
     rp.n_extra = PL.part_scale >= 0 ? PL.n_part - PL.part_scale : 0;
     rp.dquery = g->dquery;
+    rp.q_rows = q_rows;
+    rp.q_row = q_rows > 1 ? g->dquery_row : 0;
     rp.dbias = g->dlogit_bias;
     rp.dextra = g->dvalue_scale;
     err = launch_reduce_partials(d->dtype, rp, st);

@@ -162,6 +162,7 @@ struct ReduceParams {
   void* dgate;                // dtype
   float* dbias;
   float* dextra;
+  int32_t q_rows, q_row;      // q_rows > 1: dquery is a [q_rows][n_q] bank, row q_row written, the others zeroed
 };
 
 // Phase 1 (cached-logit read of completed sources for Q read sites)

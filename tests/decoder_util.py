@@ -41,7 +41,9 @@ class OracleOps:
 
     @staticmethod
     def lrid_attention_residual_phase2_torch(pv, pk, q, inter, lse, scale, key_norm, normalize_output=False,
-                                             logit_bias=0.0, partial_scale=None, scale_key=False):
+                                             logit_bias=0.0, partial_scale=None, scale_key=False, query_row=None):
+        if query_row is not None:  # the reference reads the site's row of the bank
+            q = q[query_row]
         return _phase2(pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias, partial_scale,
                        scale_key, "lerp")
 
@@ -57,7 +59,10 @@ class OracleOps:
 
     @staticmethod
     def lrid_attention_residual_phase2(pv, pk, q, inter, lse, scale, key_norm, force_triton=False,
-                                       normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False):
+                                       normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False,
+                                       query_row=None):
+        if query_row is not None:  # the reference reads the site's row of the bank
+            q = q[query_row]
         return _phase2(pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias, partial_scale,
                        scale_key, "addcmul")
 

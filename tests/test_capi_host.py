@@ -54,7 +54,7 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 7
+    assert lib.attnres_abi_version() == 8
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()

@@ -117,9 +117,11 @@ class CheckingOps:
         return value, key
 
     def _phase2(self, fn, merge, pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias,
-                partial_scale, scale_key):
+                partial_scale, scale_key, query_row=None):
         out = fn(pv, pk, q, inter, lse, scale, key_norm, normalize_output=normalize_output, logit_bias=logit_bias,
-                 partial_scale=partial_scale, scale_key=scale_key)
+                 partial_scale=partial_scale, scale_key=scale_key, query_row=query_row)
+        if query_row is not None:
+            q = q[query_row]
         epv, epk = pv.cpu(), pk.cpu()
         if partial_scale is not None:
             epv = epv * partial_scale
@@ -132,14 +134,15 @@ class CheckingOps:
         return out
 
     def lrid_attention_residual_phase2_torch(self, pv, pk, q, inter, lse, scale, key_norm, normalize_output=False,
-                                             logit_bias=0.0, partial_scale=None, scale_key=False):
+                                             logit_bias=0.0, partial_scale=None, scale_key=False, query_row=None):
         return self._phase2(ops.lrid_attention_residual_phase2_torch, "lerp", pv, pk, q, inter, lse, scale,
-                            key_norm, normalize_output, logit_bias, partial_scale, scale_key)
+                            key_norm, normalize_output, logit_bias, partial_scale, scale_key, query_row)
 
     def lrid_attention_residual_phase2(self, pv, pk, q, inter, lse, scale, key_norm, force_triton=False,
-                                       normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False):
+                                       normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False,
+                                       query_row=None):
         return self._phase2(ops.lrid_attention_residual_phase2, "addcmul", pv, pk, q, inter, lse, scale, key_norm,
-                            normalize_output, logit_bias, partial_scale, scale_key)
+                            normalize_output, logit_bias, partial_scale, scale_key, query_row)
 
 
 def _config5(**kw):

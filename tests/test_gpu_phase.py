@@ -440,6 +440,62 @@ def test_phase2_partial_scale_is_the_block_summary(dtype, variant, scale_kind, k
         assert_close(a_d.grad.reshape(1), a_t.grad.reshape(1), dtype, "dalpha", reduced=True)
 
 
+# ------------------------------------------------------------------ query bank rows
+
+@pytest.mark.parametrize("variant", ["lrid", "lrid_addcmul"])
+@pytest.mark.parametrize("row", [0, 5, 47])
+@pytest.mark.parametrize("T", [37, 2048])
+def test_lrid_phase2_query_bank_row(variant, row, T):
+    """phase2(query=bank, query_row=i) is phase2(query=bank[i]) bit for bit, and
+    the bank's gradient is the select's: the row's gradient in row i, zeros
+    elsewhere (written by the reduction, no fill or copy)."""
+    g = gen(4100 + row)
+    B, D, R, L = 1, 1024, 32, 48
+    dt = torch.bfloat16
+    pv, it, go = (randn(g, (B, T, D), dt) for _ in range(3))
+    pk = randn(g, (B, T, R), dt)
+    lse = randn(g, (B, T), torch.float32)
+    bank = randn(g, (L, R), dt, 0.5)
+    fn = ops.lrid_attention_residual_phase2_torch if variant == "lrid" else ops.lrid_attention_residual_phase2
+    kw = dict(normalize_output=True, logit_bias=0.6931, partial_scale=0.5)
+
+    b1 = leaf(bank)
+    a = [leaf(x) for x in (pv, pk, it, lse)]
+    out1 = fn(a[0], a[1], b1, a[2], a[3], 0.125, True, query_row=row, **kw)
+    out1.backward(go.to(DEV))
+
+    b2 = leaf(bank)
+    c = [leaf(x) for x in (pv, pk, it, lse)]
+    out2 = fn(c[0], c[1], b2[row], c[2], c[3], 0.125, True, **kw)
+    out2.backward(go.to(DEV))
+
+    assert torch.equal(out1, out2)
+    assert torch.equal(b1.grad, b2.grad)
+    assert int(torch.count_nonzero(b1.grad[torch.arange(L, device=DEV) != row])) == 0
+    for x, y in zip(a, c):
+        assert torch.equal(x.grad, y.grad)
+
+
+def test_lrid_phase2_query_bank_row_limits():
+    B, T, D, R = 1, 4, 256, 32
+    pv = torch.zeros((B, T, D), device=DEV, dtype=torch.bfloat16)
+    pk = torch.zeros((B, T, R), device=DEV, dtype=torch.bfloat16)
+    lse = torch.zeros((B, T), device=DEV)
+    with pytest.raises(RuntimeError, match="query_row=6 outside"):
+        ops.lrid_attention_residual_phase2(pv, pk, torch.zeros((6, R), device=DEV, dtype=torch.bfloat16), pv, lse,
+                                           0.125, True, query_row=6)
+    with pytest.raises(RuntimeError, match="query bank must be"):
+        ops.lrid_attention_residual_phase2(pv, pk, torch.zeros((6, R + 1), device=DEV, dtype=torch.bfloat16), pv,
+                                           lse, 0.125, True, query_row=1)
+    # no tokens: the bank's gradient is all zeros
+    e = torch.empty((1, 0, D), device=DEV, dtype=torch.bfloat16)
+    bank = torch.ones((6, R), device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    out = ops.lrid_attention_residual_phase2(e, torch.empty((1, 0, R), device=DEV, dtype=torch.bfloat16), bank, e,
+                                             torch.empty((1, 0), device=DEV), 0.125, True, query_row=2)
+    out.sum().backward()
+    assert bank.grad.shape == (6, R) and float(bank.grad.abs().sum()) == 0.0
+
+
 # ------------------------------------------------------------------ composition and sizes
 
 def test_phase1_phase2_compose_to_the_full_read():
