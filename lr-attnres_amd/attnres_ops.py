@@ -22,9 +22,8 @@ deterministically.
 from __future__ import annotations
 
 import contextlib
-import math
 from collections import OrderedDict
-from typing import Optional, Sequence
+from typing import Optional
 
 import torch
 from torch import Tensor

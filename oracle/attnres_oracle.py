@@ -71,7 +71,6 @@ attention_residual_phase1_ref             one query == the base read (pinned
 from __future__ import annotations
 
 import math
-from typing import Sequence
 
 import torch
 from torch import Tensor
