@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define ATTNRES_ABI_VERSION 8
+#define ATTNRES_ABI_VERSION 9
 #define ATTNRES_MAX_SOURCES 64
 
 /* element type of values / keys / queries / gate / out / gradients */
@@ -537,6 +537,47 @@ int attnres_block_accum_backward(const attnres_block_accum_desc* desc, const voi
                                  int64_t grad_value_row_stride, const void* grad_key, const float* key_inv_rms,
                                  const float* value_inv_rms, void* grad_projected, void* grad_partial_key,
                                  float* grad_value_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Block accumulation fused with the next read's LR merge: one pass per token
+ * grows the live partial block by this sublayer's projection (as
+ * attnres_block_accum_forward with complete = 0) and merges the grown block
+ * into the next site's read (as attnres_phase2_forward on it).  No single
+ * counterpart in the reference, whose model grows the partial block after the
+ * projection split (model.py:363-388, 2377-2389) and then calls
+ * lrid_attention_residual_phase2[_torch] (attnres_ops.py:4075-4160); the block
+ * decoder calls this after every sublayer that does not end a block.
+ *   accum: the sublayer's projection and the live block before it
+ *          (complete = 0; partial_value / partial_key NULL for a block's first
+ *          sublayer).
+ *   read:  the merge at the next read site, rank <= 64, its rows one-wave
+ *          16-bit rows of 256/512/768/1024 (else ATTNRES_EUNSUPPORTED: compose
+ *          the two calls then).  The forward ignores read.partial_value /
+ *          partial_key; the backward takes them as the grown block the
+ *          forward wrote.
+ * Forward: value_out [n_tok, dim], key_out [n_tok, rank] (the grown block),
+ * key_inv_rms [n_tok, heads] with key_norm, out [n_tok, dim] (the read).
+ * Backward: grads as for attnres_phase2_backward (workspace from
+ * attnres_phase2_backward_workspace_size(&desc->read); dpartial_value and
+ * dpartial_key unused); grad_value [n_tok, dim] (rows grad_value_row_stride
+ * elements apart) / grad_key [n_tok, rank] dense: the grown block's gradients
+ * from its other consumers (NULL: none); writes
+ * grad_projected [n_tok, proj_cols] -- value columns the grown value's total
+ * gradient, which is also the old partial value's; key columns through the
+ * key norm; padding zero -- and grad_partial_key, the old partial key's
+ * gradient (the grown key's total; NULL without an old partial key).
+ */
+typedef struct attnres_accum_read_desc {
+  attnres_block_accum_desc accum;
+  attnres_phase2_desc read;
+} attnres_accum_read_desc;
+
+int attnres_accum_read_forward(const attnres_accum_read_desc* desc, void* value_out, void* key_out,
+                               float* key_inv_rms, void* out, void* stream);
+int attnres_accum_read_backward(const attnres_accum_read_desc* desc, const attnres_phase2_grads* grads,
+                                const void* grad_value, int64_t grad_value_row_stride, const void* grad_key,
+                                const float* key_inv_rms, void* grad_projected, void* grad_partial_key,
+                                void* stream);
 
 /*
  * Value-derived LR keys (config 4's key producer): the rms-norm on either side

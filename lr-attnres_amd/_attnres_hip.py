@@ -16,7 +16,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libattnres_hip.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_SOURCES = 64
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -212,6 +212,11 @@ class BlockAccumDesc(ctypes.Structure):
                 ("value_scale", c_float), ("value_scale_dev", POINTER(c_float))]
 
 
+class AccumReadDesc(ctypes.Structure):
+    """attnres_accum_read_desc (include/attnres_hip.h): a block accumulation and the merge that reads it."""
+    _fields_ = [("accum", BlockAccumDesc), ("read", Phase2Desc)]
+
+
 class ValueKeyDesc(ctypes.Structure):
     """attnres_value_key_desc (include/attnres_hip.h)."""
     _fields_ = [("n_src", c_int32), ("dtype", c_int32), ("n_tok", c_int64), ("dim", c_int32),
@@ -273,6 +278,12 @@ def load() -> ctypes.CDLL:
     lib.attnres_keyed_split_backward.restype = c_int
     lib.attnres_keyed_split_backward.argtypes = [POINTER(KeyedSplitDesc), c_void_p, c_void_p, POINTER(c_float),
                                                  c_void_p, c_void_p]
+    lib.attnres_accum_read_forward.restype = c_int
+    lib.attnres_accum_read_forward.argtypes = [POINTER(AccumReadDesc), c_void_p, c_void_p, POINTER(c_float), c_void_p,
+                                               c_void_p]
+    lib.attnres_accum_read_backward.restype = c_int
+    lib.attnres_accum_read_backward.argtypes = [POINTER(AccumReadDesc), POINTER(Phase2Grads), c_void_p, c_int64,
+                                                c_void_p, POINTER(c_float), c_void_p, c_void_p, c_void_p]
     lib.attnres_block_accum_forward.restype = c_int
     lib.attnres_block_accum_forward.argtypes = [POINTER(BlockAccumDesc), c_void_p, c_void_p, POINTER(c_float),
                                                 POINTER(c_float), c_void_p]
@@ -874,6 +885,58 @@ def block_accum_backward(d: BlockAccumDesc, device, dtype, grad_value, grad_key,
         _ptr(gy), _ptr(dpk), _fptr(ds), _ptr(ws), ws_bytes, _stream(device))
     _check(rc, "block accumulation backward")
     return gy, dpk, ds
+
+
+def accum_read_desc(accum: BlockAccumDesc, read: Phase2) -> AccumReadDesc:
+    d = AccumReadDesc()
+    d.accum = accum
+    d.read = read.c
+    return d
+
+
+def accum_read_forward(d: AccumReadDesc, value, key, kinv, out, device):
+    """Block accumulation fused with the next merge: writes the grown block into value [n, dim] / key
+    [n, rank], the key's 1/rms into kinv (with key norm) and the read into out [n, dim]."""
+    lib = load()
+    rc = lib.attnres_accum_read_forward(ctypes.byref(d), _ptr(value), _ptr(key), _fptr(kinv) if kinv.numel() else None,
+                                        _ptr(out), _stream(device))
+    _check(rc, "accumulate-and-read forward")
+
+
+def accum_read_backward(d: AccumReadDesc, device, dtype, grad_out, grad_value, grad_key, kinv, want_dquery,
+                        query_shape, query_row, want_dbias, want_dscale, want_dpk_old):
+    """(grad_projected [n, proj_cols], grad_partial_key [n, rank] | None, dquery | None, dinter, dlse,
+    dbias | None, dscale | None).  grad_value may be a row-strided [n, dim] view, grad_key dense."""
+    lib = load()
+    n, D, R, P = d.read.n_tok, d.read.dim, d.read.rank, d.accum.split.proj_cols
+    gy = torch.empty((n, P), device=device, dtype=dtype)
+    dpk = torch.empty((n, R), device=device, dtype=dtype) if want_dpk_old else None
+    dq = torch.empty(query_shape, device=device, dtype=dtype) if want_dquery else None
+    di = torch.empty((n, D), device=device, dtype=dtype)
+    dl = torch.empty((n,), device=device, dtype=torch.float32)
+    db = torch.empty((1,), device=device, dtype=torch.float32) if want_dbias else None
+    ds = torch.empty((1,), device=device, dtype=torch.float32) if want_dscale else None
+    g = Phase2Grads()
+    g.grad_out = grad_out.data_ptr()
+    g.dquery = dq.data_ptr() if dq is not None else None
+    g.dinterblock_output = di.data_ptr()
+    g.dinterblock_lse = _fptr(dl)
+    g.dlogit_bias = _fptr(db)
+    g.dvalue_scale = _fptr(ds)
+    if dq is not None and query_row is not None:
+        g.dquery_rows = int(query_shape[0])
+        g.dquery_row = int(query_row)
+    ws_bytes = lib.attnres_phase2_backward_workspace_size(ctypes.byref(d.read))
+    ws = torch.empty((max(int(ws_bytes), 1),), device=device, dtype=torch.uint8)
+    g.workspace = ws.data_ptr()
+    g.workspace_bytes = int(ws_bytes)
+    gv_stride = grad_value.stride(0) if grad_value is not None else D
+    rc = lib.attnres_accum_read_backward(ctypes.byref(d), ctypes.byref(g), _ptr(grad_value), gv_stride,
+                                         _ptr(grad_key),
+                                         _fptr(kinv) if kinv is not None and kinv.numel() else None, _ptr(gy),
+                                         _ptr(dpk), _stream(device))
+    _check(rc, "accumulate-and-read backward")
+    return gy, dpk, dq, di, dl, db, ds
 
 
 # ---------------------------------------------------------------------------

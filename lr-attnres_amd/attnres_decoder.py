@@ -29,7 +29,11 @@ with ``partial_scale = count**-alpha`` instead of being multiplied out first
 same rounding), and with pre-norm sublayers each sublayer's fused projection
 goes straight into ``lrid_block_accumulate``, which splits it, norms the key,
 adds both to the partial block and, at a block end, forms the block source in
-one pass (``fuse_block_accumulation``; bit-identical too).  Module and parameter names match the reference's, so a
+one pass (``fuse_block_accumulation``; bit-identical too); a sublayer that does
+not end a block also merges the grown block into the next site's read in that
+pass (``lrid_block_accumulate_read``, ``fuse_accumulate_read``; bit-identical,
+gradients included; off by default: eager steps only, not cleared for HIP-graph
+capture).  Module and parameter names match the reference's, so a
 reference state dict for this configuration loads with ``load_state_dict``.
 
 The read functions are looked up on ``ops`` (default: the HIP-backed
@@ -105,6 +109,7 @@ class DecoderConfig:
     lrid_logit_scale: Optional[float] = None
     fold_block_summary: bool = True
     fuse_block_accumulation: bool = True
+    fuse_accumulate_read: bool = False
 
     def __post_init__(self):
         if self.norm_pos not in {"before", "after", "both"}:
@@ -503,9 +508,25 @@ class Decoder(nn.Module):
             return phase2(value, key, queries, inter, lse, c.lrid_logit_scale, c.attnres_key_norm,
                           normalize_output=fused_norm, logit_bias=self._count_bias(count), query_row=site - 1)
 
-        def add(out: Tensor, key: Optional[Tensor], site_after: int):
+        def add(out: Tensor, key: Optional[Tensor], site_after: int) -> Optional[Tensor]:
+            """Grows the partial block by a sublayer's output; returns the read at
+            ``site_after`` when the accumulation produced it as well."""
             nonlocal partial, partial_key, count, phase
             complete = site_after in self.block_ends
+            if key is None and not complete and c.fuse_accumulate_read and c.fold_block_summary:
+                # the grown block and the next site's merge of it in one pass (model.py:2377-2389
+                # then :1919-1942): the read() below, on the block this call grows
+                ensure_phase(site_after)
+                i = site_after - phase[0]
+                n = count + 1
+                partial, partial_key, h = ops.lrid_block_accumulate_read(
+                    out, partial, partial_key, queries, phase[2][i], phase[3][i], c.n_embd, rank,
+                    c.lrid_logit_scale, c.lrid_num_heads, c.attnres_key_norm,
+                    lerp=c.attnres_training_torch_phase2, normalize_output=fused_norm,
+                    logit_bias=self._count_bias(n), partial_scale=self._block_scale(n),
+                    scale_key=not c.attnres_key_norm, query_row=site_after - 1)
+                count = n
+                return h
             if key is None:
                 # ``out`` is the sublayer's fused projection: split, key norm, partial-block add
                 # and, at a block end, the block source in one pass (model.py:2377-2389, 1003-1018)
@@ -515,7 +536,7 @@ class Decoder(nn.Module):
                     scale_key=complete and not c.attnres_key_norm)
                 if not complete:
                     partial, partial_key, count = value, key, count + 1
-                    return
+                    return None
                 count += 1
             else:
                 if partial is None:
@@ -523,20 +544,24 @@ class Decoder(nn.Module):
                 else:
                     partial, partial_key, count = partial + out, partial_key + key, count + 1
                 if not complete:
-                    return
+                    return None
                 value, key = summary(partial, partial_key, count)
             done_values.append(value)
             done_logits.append(site_logits(value, key, site_after, count))
             partial = partial_key = None
             count = 0
             phase = None
+            return None
 
+        h = read(0)
         for layer_idx, block in enumerate(self.transformer.layers):
-            h = read(2 * layer_idx)
             out, key = block.attention(h, x_is_normalized=fused_norm)
-            add(out, key, 2 * layer_idx + 1)
-            h = read(2 * layer_idx + 1)
+            site = 2 * layer_idx + 1
+            h = add(out, key, site)
+            if h is None:
+                h = read(site)
             out, key = block.feed_forward(h, x_is_normalized=fused_norm)
-            add(out, key, 2 * layer_idx + 2)
-        h = read(n_sites)
+            h = add(out, key, site + 1)
+            if h is None:
+                h = read(site + 1)
         return h if fused_norm else norm(h)

@@ -1500,3 +1500,143 @@ def lrid_block_accumulate(projected: Tensor, partial_value: Optional[Tensor], pa
             bool(scale_key), scale_value)
     value, key = _BlockAccumFn.apply(meta, y, pv, pk, scale_t)
     return value.view(*lead, output_dim), key.view(*lead, rank)
+
+
+class _AccumReadFn(torch.autograd.Function):
+    """Eager autograd of the block accumulation fused with the merge that reads
+    the grown block: inputs (meta, y [n, P], partial value rows [n, D] | None,
+    partial key rows [n, R] | None, query bank [rows, R], inter rows [n, D],
+    lse fp32 [n], logit bias fp32 [1] | None, value scale fp32 [1] | None);
+    outputs (value [n, D], key [n, R], out [n, D])."""
+
+    @staticmethod
+    def forward(ctx, meta, y, pv, pk, query, inter, lse, bias_t, scale_t):
+        (dim, rank, heads, key_norm, merge, merge_key_norm, normalize_output, logit_scale, bias_value, scale_value,
+         scale_key, qrow) = meta
+        ctx.set_materialize_grads(False)
+        n, dev, dtype = y.size(0), y.device, y.dtype
+        acc = _hip.block_accum_desc(y, dim, rank, heads, key_norm, pv, pk, False, False, False, 1.0, None)
+        value = torch.empty((n, dim), device=dev, dtype=dtype)
+        key = torch.empty((n, rank), device=dev, dtype=dtype)
+        kinv = torch.empty((n, heads) if key_norm else (0,), device=dev, dtype=torch.float32)
+        out = torch.empty((n, dim), device=dev, dtype=dtype)
+        read = _hip.Phase2(value, key, query[qrow], None, inter, lse, merge, merge_key_norm, normalize_output,
+                           logit_scale, bias_value, bias_t, scale_value, scale_t, scale_key)
+        d = _hip.accum_read_desc(acc, read)
+        with _device_ctx(dev):
+            _hip.accum_read_forward(d, value, key, kinv, out, dev)
+        ctx.meta = meta
+        # the descriptor is plain bytes; the tensors its pointers name (y, the old
+        # and grown blocks, the merge's inputs) live on as saved tensors -- the
+        # outputs only there, so that ctx holds no reference cycle through them
+        ctx.desc = d
+        ctx.save_for_backward(y, pv, pk, query, inter, lse, bias_t, scale_t, kinv, value, key)
+        return value, key, out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, g_value, g_key, g_out):
+        if g_value is None and g_key is None and g_out is None:
+            return (None,) * 9
+        y, pv, pk, query, inter, lse, bias_t, scale_t, kinv, value, key = ctx.saved_tensors
+        dim, qrow = ctx.meta[0], ctx.meta[-1]
+        want = ctx.needs_input_grad  # (meta, y, pv, pk, query, inter, lse, bias, scale)
+        d = ctx.desc
+        g_out = torch.zeros_like(value) if g_out is None else g_out.contiguous()
+        if g_value is not None and (g_value.stride(-1) != 1 or g_value.stride(0) < dim):
+            g_value = g_value.contiguous()
+        gk = g_key.contiguous() if g_key is not None else None
+        dev = y.device
+        with _device_ctx(dev):
+            gy, dpk, dq, di, dl, db, ds = _hip.accum_read_backward(
+                d, dev, y.dtype, g_out, g_value, gk, kinv if kinv.numel() else None, want_dquery=want[4],
+                query_shape=tuple(query.shape), query_row=qrow, want_dbias=bias_t is not None and want[7],
+                want_dscale=scale_t is not None and want[8], want_dpk_old=pk is not None and want[3])
+        # the grown value's total gradient is also the old partial value's: columns [0, D) of gy
+        return (None, gy if want[1] else None, gy[:, :dim] if pv is not None and want[2] else None,
+                dpk if pk is not None and want[3] else None, dq if want[4] else None, di if want[5] else None,
+                dl if want[6] else None, db.reshape(bias_t.shape) if db is not None else None,
+                ds.reshape(scale_t.shape) if ds is not None else None)
+
+
+def _accum_read_fits(y: Tensor, inter: Tensor, D: int, R: int, heads: int) -> bool:
+    """Shapes the fused accumulate-and-read kernels take: 16-bit rows one wave
+    covers exactly (D = 256, 512, 768, 1024), rank <= 64, 16-byte aligned rows."""
+    if y.dtype not in (torch.bfloat16, torch.float16) or D not in (256, 512, 768, 1024):
+        return False
+    if not 1 <= R <= 64 or R % heads != 0:
+        return False
+    return all(t.data_ptr() % 16 == 0 and (t.stride(0) * t.element_size()) % 16 == 0 for t in (y, inter))
+
+
+def lrid_block_accumulate_read(projected: Tensor, partial_value: Optional[Tensor], partial_key: Optional[Tensor],
+                               query: Tensor, interblock_output: Tensor, interblock_lse: Tensor, output_dim: int,
+                               rank: int, logit_scale: float, num_heads: int = 1, key_norm: bool = True,
+                               merge_key_norm: Optional[bool] = None, lerp: bool = False,
+                               normalize_output: bool = False, logit_bias=0.0, partial_scale=None,
+                               scale_key: bool = False, query_row: Optional[int] = None):
+    """A sublayer's block accumulation and the read at the next site, in one pass.
+
+    Not in the reference's op module: its model grows the live partial block
+    after the projection split (model.py:363-388, 2377-2389) and the next read
+    site merges it with ``lrid_attention_residual_phase2[_torch]``
+    (attnres_ops.py:4075-4160).  Same results, bit for bit, as::
+
+        value, key = lrid_block_accumulate(projected, partial_value, partial_key, output_dim, rank,
+                                           num_heads, key_norm)
+        out = lrid_attention_residual_phase2[_torch](value, key, query, interblock_output, interblock_lse,
+                                                     logit_scale, merge_key_norm, ...)
+
+    (``_torch``, the ``lerp`` merge, with ``lerp``), and the gradients of all
+    three outputs as autograd sums them there.  ``merge_key_norm`` defaults to
+    ``key_norm``.  Returns ``(value, key, out)``: the grown block and the read.
+    Shapes the fused kernels do not take run the two calls.
+    """
+    mkn = key_norm if merge_key_norm is None else bool(merge_key_norm)
+    D, R = int(output_dim), int(rank)
+    if interblock_output.dim() != 3 or interblock_output.size(-1) != D:
+        raise RuntimeError(f"lrid_block_accumulate_read: interblock_output must be [B, T, {D}]")
+    B, T = interblock_output.shape[:2]
+    P = projected.size(-1)
+    y = projected.reshape(B * T, P) if projected.numel() == B * T * P else None
+    inter = _rows2d(interblock_output) if interblock_output.dtype == projected.dtype else None
+    fused = (y is not None and inter is not None and y.stride(-1) == 1 and B * T > 0 and not _compiling()
+             and P >= D + R and _accum_read_fits(y, inter, D, R, int(num_heads)))
+    if not fused:
+        value, key = lrid_block_accumulate(projected, partial_value, partial_key, D, R, num_heads, key_norm)
+        value, key = value.reshape(B, T, D), key.reshape(B, T, R)
+        phase2 = lrid_attention_residual_phase2_torch if lerp else lrid_attention_residual_phase2
+        out = phase2(value, key, query, interblock_output, interblock_lse, logit_scale, mkn,
+                     normalize_output=normalize_output, logit_bias=logit_bias, partial_scale=partial_scale,
+                     scale_key=scale_key, query_row=query_row)
+        return value, key, out
+    what = "lrid_block_accumulate_read"
+    dev = _check_gpu([t for t in (projected, partial_value, partial_key, query, interblock_output, interblock_lse)
+                      if t is not None], what)
+    if interblock_lse.numel() != B * T:
+        raise RuntimeError(f"{what}: interblock_lse must be [B, T]")
+
+    def rows(t, width, name):
+        if t is None:
+            return None
+        if t.dtype != projected.dtype or t.numel() != B * T * width:
+            raise RuntimeError(f"{what}: {name} must be {(B, T, width)} in {projected.dtype}")
+        return t.reshape(B * T, width).contiguous()
+
+    pv = rows(partial_value, D, "partial_value")
+    pk = rows(partial_key, R, "partial_key")
+    if query_row is None:
+        if query.numel() != R:
+            raise RuntimeError(f"{what}: query must have {R} elements, got {query.numel()}")
+        bank, qrow = query.reshape(1, R).to(projected.dtype).contiguous(), 0
+    else:
+        if query.dim() != 2 or query.size(1) != R or not 0 <= int(query_row) < query.size(0):
+            raise RuntimeError(f"{what}: a query bank must be [rows, {R}] with query_row in range")
+        bank, qrow = query.to(projected.dtype).contiguous(), int(query_row)
+    bias_value, bias_t = _scalar_arg(logit_bias, dev, "logit_bias")
+    scale_value, scale_t = (1.0, None) if partial_scale is None else _scalar_arg(partial_scale, dev, "partial_scale")
+    lse = interblock_lse.float().reshape(B * T).contiguous()
+    meta = (D, R, int(num_heads), bool(key_norm), _hip.MERGE_LERP if lerp else _hip.MERGE_ADDCMUL, mkn,
+            bool(normalize_output), float(logit_scale), bias_value, scale_value, bool(scale_key), qrow)
+    value, key, out = _AccumReadFn.apply(meta, y, pv, pk, bank, inter, lse, bias_t, scale_t)
+    return value.view(B, T, D), key.view(B, T, R), out.view(B, T, D)

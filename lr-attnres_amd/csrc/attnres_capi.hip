@@ -1288,16 +1288,56 @@ extern "C" size_t attnres_phase2_backward_workspace_size(const attnres_phase2_de
   return (size_t)bwd_groups(d->n_tok) * part_stride(PL.n_part) * sizeof(float);
 }
 
-extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, void* stream) {
+namespace {
+
+// The block accumulation fused in front of an LR merge
+// (attnres_accum_read_*): the accumulation's description and buffers.
+struct AccRead {
+  const attnres_block_accum_desc* a;
+  void* value_out;          // forward: the grown block
+  void* key_out;
+  float* key_inv_rms;       // forward writes, backward reads ([n_tok, heads] with key norm)
+  const void* grad_value;   // backward: the grown block's other gradients, or NULL
+  int64_t grad_value_stride;
+  const void* grad_key;
+  void* grad_projected;     // backward: [n_tok, proj_cols]
+  void* grad_partial_key;   // backward: the old partial key's gradient, or NULL
+};
+
+// phase-2 parameters of the fused accumulation (the merge reads the grown block)
+void fill_accum(const AccRead& acc, Phase2Params* p) {
+  const attnres_keyed_split_desc& s = acc.a->split;
+  p->acc_y = s.projected;
+  p->acc_y_stride = s.row_stride;
+  p->acc_P = s.proj_cols;
+  p->acc_H = s.heads;
+  p->acc_hd = s.rank / s.heads;
+  p->acc_key_norm = s.key_norm ? 1 : 0;
+  p->acc_eps = s.norm_eps;
+  p->acc_pv_old = acc.a->partial_value;
+  p->acc_pk_old = acc.a->partial_key;
+  p->acc_pv_out = acc.value_out;
+  p->acc_pk_out = acc.key_out;
+  p->acc_inv = acc.key_inv_rms;
+  p->acc_gv = acc.grad_value;
+  p->acc_gv_stride = acc.grad_value_stride;
+  p->acc_gk = acc.grad_key;
+  p->acc_gy = acc.grad_projected;
+  p->acc_dpk_old = acc.grad_partial_key;
+}
+
+int phase2_forward_impl(const attnres_phase2_desc* d, void* out, void* stream, const AccRead* acc) {
   int rc = check_phase2(d);
   if (rc) return rc;
   if (d->n_tok == 0) return ATTNRES_OK;
   if (!out) return fail(ATTNRES_EINVAL, "out is NULL");
   PhasePlan pl;
-  const void* rows[4] = {d->partial_value, d->interblock_output, out,
-                         (d->rank == 0 && !d->logit_given) ? d->query : nullptr};
-  const int64_t strides[4] = {d->partial_value_row_stride, d->interblock_row_stride, d->dim, d->dim};
-  rc = phase_plan(d->dtype, d->dim, rows, strides, 4, &pl);
+  const void* rows[6] = {d->partial_value, d->interblock_output, out,
+                         (d->rank == 0 && !d->logit_given) ? d->query : nullptr,
+                         acc ? acc->a->split.projected : nullptr, acc ? acc->a->partial_value : nullptr};
+  const int64_t strides[6] = {d->partial_value_row_stride, d->interblock_row_stride, d->dim, d->dim,
+                              acc ? acc->a->split.row_stride : d->dim, d->dim};
+  rc = phase_plan(d->dtype, d->dim, rows, strides, 6, &pl);
   if (rc) return rc;
   Phase2Params p;
   fill_phase2(d, pl, &p);
@@ -1327,13 +1367,29 @@ extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, v
     L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
   }
   const bool fast = L.teams > 0 && phase2_fast(d, wv);
+  if (acc) {
+    if (!fast || L.nmax != 1 || d->rank > kWaveSize)
+      return fail(ATTNRES_EUNSUPPORTED, "the fused accumulation needs the one-wave LR merge (16-bit rows of "
+                  "256/512/768/1024 aligned to 16 bytes, rank <= 64)");
+    fill_accum(*acc, &p);
+    L.feat |= 4;
+  }
   hipError_t err = fast ? launch_phase2_fast_forward(d->dtype, p, L, (hipStream_t)stream)
                         : launch_phase2_forward(d->dtype, p, L, (hipStream_t)stream);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 forward launch failed: %s", hipGetErrorString(err));
   return ATTNRES_OK;
 }
 
-extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnres_phase2_grads* g, void* stream) {
+}  // namespace
+
+extern "C" int attnres_phase2_forward(const attnres_phase2_desc* d, void* out, void* stream) {
+  return phase2_forward_impl(d, out, stream, nullptr);
+}
+
+namespace {
+
+int phase2_backward_impl(const attnres_phase2_desc* d, const attnres_phase2_grads* g, void* stream,
+                         const AccRead* acc) {
   int rc = check_phase2(d);
   if (rc) return rc;
   if (!g) return fail(ATTNRES_EINVAL, "grads is NULL");
@@ -1349,14 +1405,18 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     if (g->dvalue_scale) zero_async(g->dvalue_scale, sizeof(float), st);
     return ATTNRES_OK;
   }
-  if (!g->grad_out || !g->dpartial_value || !g->dinterblock_output || !g->dinterblock_lse)
+  if (!g->grad_out || !(acc || g->dpartial_value) || !g->dinterblock_output || !g->dinterblock_lse)
     return fail(ATTNRES_EINVAL, "grad_out / dpartial_value / dinterblock_output / dinterblock_lse is NULL");
-  if (lr && !g->dpartial_key) return fail(ATTNRES_EINVAL, "LR merge backward needs dpartial_key");
+  if (lr && !acc && !g->dpartial_key) return fail(ATTNRES_EINVAL, "LR merge backward needs dpartial_key");
   PhasePlan pl;
-  const void* rows[6] = {d->partial_value, d->interblock_output, g->grad_out, g->dpartial_value,
-                         g->dinterblock_output, (d->rank == 0 && !d->logit_given) ? d->query : nullptr};
-  const int64_t strides[6] = {d->partial_value_row_stride, d->interblock_row_stride, d->dim, d->dim, d->dim, d->dim};
-  rc = phase_plan(d->dtype, d->dim, rows, strides, 6, &pl);
+  const void* rows[9] = {d->partial_value, d->interblock_output, g->grad_out, acc ? nullptr : g->dpartial_value,
+                         g->dinterblock_output, (d->rank == 0 && !d->logit_given) ? d->query : nullptr,
+                         acc ? acc->grad_projected : nullptr, acc ? acc->grad_value : nullptr,
+                         acc ? acc->a->split.projected : nullptr};
+  const int64_t strides[9] = {d->partial_value_row_stride, d->interblock_row_stride, d->dim, d->dim, d->dim, d->dim,
+                              acc ? acc->a->split.proj_cols : d->dim, acc ? acc->grad_value_stride : d->dim,
+                              acc ? acc->a->split.row_stride : d->dim};
+  rc = phase_plan(d->dtype, d->dim, rows, strides, 9, &pl);
   if (rc) return rc;
   Phase2Params p;
   fill_phase2(d, pl, &p);
@@ -1405,6 +1465,13 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     L.lds = (2 * (size_t)L.wpt + 8) * sizeof(float);
   }
   const bool fast = L.teams > 0 && phase2_fast(d, wv);
+  if (acc) {
+    if (!fast || L.nmax != 1 || d->rank > kWaveSize)
+      return fail(ATTNRES_EUNSUPPORTED, "the fused accumulation needs the one-wave LR merge (16-bit rows of "
+                  "256/512/768/1024 aligned to 16 bytes, rank <= 64)");
+    fill_accum(*acc, &p);
+    L.feat |= 4;
+  }
   hipError_t err = fast ? launch_phase2_fast_backward(d->dtype, p, L, st) : launch_phase2_backward(d->dtype, p, L, st);
   if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "phase-2 backward launch failed: %s", hipGetErrorString(err));
   if (PL.n_part > 0) {
@@ -1430,6 +1497,64 @@ extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnr
     if (err != hipSuccess) return fail(ATTNRES_ELAUNCH, "reduce launch failed: %s", hipGetErrorString(err));
   }
   return ATTNRES_OK;
+}
+
+int check_block_accum(const attnres_block_accum_desc* d);  // the block accumulation's checks (below)
+
+// the fused accumulation's description against its merge's
+int check_accum_read(const attnres_accum_read_desc* d) {
+  if (!d) return fail(ATTNRES_EINVAL, "desc is NULL");
+  int rc = check_block_accum(&d->accum);
+  if (rc) return rc;
+  const attnres_keyed_split_desc& s = d->accum.split;
+  const attnres_phase2_desc& r = d->read;
+  if (d->accum.complete) return fail(ATTNRES_EINVAL, "the fused accumulation grows a live block (complete = 0)");
+  if (r.logit_given || r.rank < 1) return fail(ATTNRES_EINVAL, "the fused accumulation feeds an LR merge");
+  if (r.dtype != s.dtype || r.n_tok != s.n_tok || r.dim != s.dim || r.rank != s.rank)
+    return fail(ATTNRES_EINVAL, "accum and read disagree on dtype / n_tok / dim / rank");
+  return ATTNRES_OK;
+}
+
+}  // namespace
+
+extern "C" int attnres_phase2_backward(const attnres_phase2_desc* d, const attnres_phase2_grads* g, void* stream) {
+  return phase2_backward_impl(d, g, stream, nullptr);
+}
+
+extern "C" int attnres_accum_read_forward(const attnres_accum_read_desc* d, void* value_out, void* key_out,
+                                          float* key_inv_rms, void* out, void* stream) {
+  int rc = check_accum_read(d);
+  if (rc) return rc;
+  if (d->read.n_tok == 0) return ATTNRES_OK;
+  if (!value_out || !key_out) return fail(ATTNRES_EINVAL, "value_out / key_out is NULL");
+  if (d->accum.split.key_norm && !key_inv_rms) return fail(ATTNRES_EINVAL, "key_norm needs key_inv_rms");
+  // the merge reads the grown block this call writes
+  attnres_phase2_desc r = d->read;
+  r.partial_value = value_out;
+  r.partial_value_row_stride = r.dim;
+  r.partial_key = key_out;
+  r.partial_key_row_stride = r.rank;
+  AccRead acc{&d->accum, value_out, key_out, key_inv_rms, nullptr, 0, nullptr, nullptr, nullptr};
+  return phase2_forward_impl(&r, out, stream, &acc);
+}
+
+extern "C" int attnres_accum_read_backward(const attnres_accum_read_desc* d, const attnres_phase2_grads* g,
+                                           const void* grad_value, int64_t grad_value_row_stride,
+                                           const void* grad_key, const float* key_inv_rms, void* grad_projected,
+                                           void* grad_partial_key, void* stream) {
+  int rc = check_accum_read(d);
+  if (rc) return rc;
+  if (!g) return fail(ATTNRES_EINVAL, "grads is NULL");
+  if (grad_value && (grad_value_row_stride < d->read.dim || grad_value_row_stride > INT32_MAX))
+    return fail(ATTNRES_EINVAL, "grad_value_row_stride=%lld must be in [dim, 2^31)", (long long)grad_value_row_stride);
+  if (d->read.n_tok > 0) {
+    if (!grad_projected) return fail(ATTNRES_EINVAL, "grad_projected is NULL");
+    if (d->accum.split.key_norm && !key_inv_rms) return fail(ATTNRES_EINVAL, "key_norm backward needs key_inv_rms");
+  }
+  AccRead acc{&d->accum, nullptr, nullptr, const_cast<float*>(key_inv_rms), grad_value, grad_value_row_stride,
+              grad_key, grad_projected,
+              d->accum.partial_key ? grad_partial_key : nullptr};
+  return phase2_backward_impl(&d->read, g, stream, &acc);
 }
 
 // ---------------------------------------------------------------- query-bank logits

@@ -410,6 +410,31 @@ __device__ __forceinline__ S* global_ptr(uint64_t a) {
 // the value of lane i ^ 1 (quad permute [1, 0, 3, 2])
 __device__ __forceinline__ float lane_xor1(float x) { return dpp_f32<kDppXor1>(x); }
 
+// Per-element sums of a[j] over each key head of hd columns, for a key row
+// held as element lane + 64 j (j < KJ): a group sum for hd < 64, else wave
+// sums added over the head's chunks (all lanes get their head's sum).
+template <int KJ>
+__device__ __forceinline__ void key_head_sums(int hd, const float (&a)[KJ], float (&s)[KJ]) {
+  if (hd < kWave) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) s[j] = group_sum(a[j], hd);
+  } else {
+    float t[KJ];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) t[j] = wave_sum(a[j]);
+    const int cph = hd / kWave;  // chunks per head
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int h0 = (j / cph) * cph;
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KJ; ++k)
+        if (k >= h0 && k < h0 + cph) acc += t[k];
+      s[j] = acc;
+    }
+  }
+}
+
 // orders one wave's LDS writes before its later LDS reads by other lanes
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

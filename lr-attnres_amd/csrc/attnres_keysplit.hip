@@ -46,24 +46,7 @@ __device__ __forceinline__ void key_inv_load(const KeySplitParams& p, int64_t to
 // per-element head sums of a[j] over each key head (all lanes get their head's sum)
 template <int KJ>
 __device__ __forceinline__ void head_sums(const KeySplitParams& p, const float (&a)[KJ], float (&s)[KJ]) {
-  if (p.hd < kWave) {
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) s[j] = group_sum(a[j], p.hd);
-  } else {
-    float t[KJ];
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) t[j] = wave_sum(a[j]);
-    const int cph = p.hd / kWave;  // chunks per head
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      const int h0 = (j / cph) * cph;
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < KJ; ++k)
-        if (k >= h0 && k < h0 + cph) acc += t[k];
-      s[j] = acc;
-    }
-  }
+  key_head_sums<KJ>(p.hd, a, s);
 }
 
 template <class DT, int E, int KJ>

@@ -267,6 +267,31 @@ struct Phase2Params {
   int32_t D, R, ncols;
   int32_t logit_given, merge, key_norm, norm_out, scale_key, pl_dt;
   float scale, eps, bias, vscale;
+  // Block accumulation fused in front of the LR merge (the fast LR kernels'
+  // ACC instantiations).  Forward: the partial block read here is the live
+  // block grown by this sublayer -- value rnd(acc_pv_old + y[:D]), key
+  // rnd(acc_pk_old + key(y[D:D+R])), the key rms-normed over heads of acc_hd
+  // columns when acc_key_norm -- written to acc_pv_out / acc_pk_out with the
+  // key's 1/rms in acc_inv [n_tok, acc_H]; pv / pk are not read.  Backward
+  // (pv / pk = the grown block): the grown block's total gradient (the
+  // merge's share plus acc_gv / acc_gk from its other consumers, if any) goes
+  // to the projection gradient acc_gy [n_tok, acc_P] (value columns as they
+  // are, key columns through the key norm, padding zero) and, for the key, to
+  // acc_dpk_old (the old partial key's gradient); dpv / dpk are not written.
+  const void* acc_y;           // [n_tok, acc_y_stride]
+  int64_t acc_y_stride;
+  int32_t acc_P, acc_H, acc_hd, acc_key_norm;
+  float acc_eps;
+  const void* acc_pv_old;      // [n_tok, D] or null (a block's first sublayer)
+  const void* acc_pk_old;      // [n_tok, R] or null
+  void* acc_pv_out;            // [n_tok, D]
+  void* acc_pk_out;            // [n_tok, R]
+  float* acc_inv;              // [n_tok, acc_H]
+  const void* acc_gv;          // [n_tok, D] rows acc_gv_stride apart, or null
+  int64_t acc_gv_stride;
+  const void* acc_gk;          // [n_tok, R] or null
+  void* acc_gy;                // [n_tok, acc_P]
+  void* acc_dpk_old;           // [n_tok, R] or null
 };
 
 // Logits of a query bank against the sources' keys (phase 1 from a query bank)

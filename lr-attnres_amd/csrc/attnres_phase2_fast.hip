@@ -409,7 +409,72 @@ __device__ __forceinline__ void p2lr_forward_state(const Phase2Params& p, int la
   st.prob = DT::rnd(st.sg);
 }
 
-template <class DT, int VB, int CB, int KJ, bool LERP>
+// The block accumulation fused in front of the merge (ACC): this sublayer's
+// projection y = [out | key | pad] grows the live partial block, value
+// rnd(pv_old + y[:D]) and key rnd(pk_old + k) with k = rnd(x inv) over each
+// key head (x = y[D:D+R]; the key split's arithmetic and sum order), and the
+// grown block is what the merge reads.  One token's loads (raw bits) and the
+// grown rows: pvr (packed, as the merge's partial rows) and kr (floats).
+template <class DT, int VB, int CB, int KJ>
+__device__ __forceinline__ void p2lr_accumulate(const Phase2Params& p, int64_t tok, int lane,
+                                                const Raw<DT, VB / 2> (&yv)[CB], const Raw<DT, VB / 2> (&po)[CB],
+                                                const uint32_t (&xb)[KJ], const uint32_t (&ob)[KJ],
+                                                Raw<DT, VB / 2> (&pvr)[CB], float (&kr)[KJ]) {
+  using S = typename DT::S;
+  constexpr int E = VB / 2;
+  constexpr int W = VB / 4;
+  const bool old = p.acc_pv_old != nullptr;
+  S* pvo = (S*)p.acc_pv_out + tok * (int64_t)p.D;
+#pragma unroll
+  for (int c = 0; c < CB; ++c) {
+    float f[E];
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      float y0, y1;
+      unpack2<DT>(yv[c].w[i], y0, y1);
+      if (old) {
+        float a0, a1;
+        unpack2<DT>(po[c].w[i], a0, a1);
+        pvr[c].w[i] = pack2<DT>(a0 + y0, a1 + y1);
+      } else {
+        pvr[c].w[i] = yv[c].w[i];
+      }
+      unpack2<DT>(pvr[c].w[i], f[2 * i], f[2 * i + 1]);
+    }
+    store_vec<DT, E, true>(pvo + (c * kWave + lane) * E, f);
+  }
+  float x[KJ];
+  row_bits_floats<DT, KJ>(xb, p.R, lane, kWave, x);
+#pragma unroll
+  for (int j = 0; j < KJ; ++j) kr[j] = x[j];
+  if (p.acc_key_norm) {
+    float sq[KJ], ss[KJ];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) sq[j] = x[j] * x[j];
+    key_head_sums<KJ>(p.acc_hd, sq, ss);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int r = lane + j * kWave;
+      const float inv = 1.0f / sqrtf(ss[j] / (float)p.acc_hd + p.acc_eps);
+      kr[j] = DT::rnd(x[j] * inv);
+      if (r < p.R && r % p.acc_hd == 0) p.acc_inv[tok * p.acc_H + r / p.acc_hd] = inv;
+    }
+  }
+  if (p.acc_pk_old) {
+    float o[KJ];
+    row_bits_floats<DT, KJ>(ob, p.R, lane, kWave, o);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) kr[j] = DT::rnd(o[j] + kr[j]);
+  }
+  S* pko = (S*)p.acc_pk_out + tok * (int64_t)p.R;
+#pragma unroll
+  for (int j = 0; j < KJ; ++j) {
+    const int r = lane + j * kWave;
+    if (r < p.R) DT::store1(pko + r, kr[j]);
+  }
+}
+
+template <class DT, int VB, int CB, int KJ, bool LERP, bool ACC>
 __global__ void __launch_bounds__(256) phase2_lr_fwd_fast_kernel(const Phase2Params p) {
   using S = typename DT::S;
   constexpr int E = VB / 2;
@@ -427,19 +492,38 @@ __global__ void __launch_bounds__(256) phase2_lr_fwd_fast_kernel(const Phase2Par
   const int64_t stride = (int64_t)gridDim.x * kP2FastWaves;
   for (int64_t tok = (int64_t)blockIdx.x * kP2FastWaves + wave; tok < p.n_tok; tok += stride) {
     Raw<DT, E> pvr[CB], itr[CB];
-    const S* pvp = (const S*)p.pv + tok * p.pv_stride;
     const S* itp = (const S*)p.inter + tok * p.inter_stride;
-#pragma unroll
-    for (int c = 0; c < CB; ++c) {
-      load_raw<DT, E, true>(pvp + (c * kWave + lane) * E, pvr[c]);
-      load_raw<DT, E, true>(itp + (c * kWave + lane) * E, itr[c]);
-    }
-    uint32_t kb[KJ];
-    row_bits_load<DT, KJ>((const S*)p.pk + tok * p.pk_stride, p.R, lane, kWave, kb);
-    const float lse = p.lse[tok];
     float kr[KJ], qk[KJ];
-    row_bits_floats<DT, KJ>(qb, p.R, lane, kWave, qk);
-    row_bits_floats<DT, KJ>(kb, p.R, lane, kWave, kr);
+    float lse;
+    if constexpr (ACC) {
+      const S* yr = (const S*)p.acc_y + tok * p.acc_y_stride;
+      const S* pop = p.acc_pv_old ? (const S*)p.acc_pv_old + tok * (int64_t)p.D : nullptr;
+      Raw<DT, E> yv[CB], po[CB];
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        load_raw<DT, E, true>(yr + (c * kWave + lane) * E, yv[c]);
+        if (pop) load_raw<DT, E, true>(pop + (c * kWave + lane) * E, po[c]);
+        load_raw<DT, E, true>(itp + (c * kWave + lane) * E, itr[c]);
+      }
+      uint32_t xb[KJ], ob[KJ];
+      row_bits_load<DT, KJ>(yr + p.D, p.R, lane, kWave, xb);
+      if (p.acc_pk_old) row_bits_load<DT, KJ>((const S*)p.acc_pk_old + tok * (int64_t)p.R, p.R, lane, kWave, ob);
+      lse = p.lse[tok];
+      row_bits_floats<DT, KJ>(qb, p.R, lane, kWave, qk);
+      p2lr_accumulate<DT, VB, CB, KJ>(p, tok, lane, yv, po, xb, ob, pvr, kr);
+    } else {
+      const S* pvp = (const S*)p.pv + tok * p.pv_stride;
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        load_raw<DT, E, true>(pvp + (c * kWave + lane) * E, pvr[c]);
+        load_raw<DT, E, true>(itp + (c * kWave + lane) * E, itr[c]);
+      }
+      uint32_t kb[KJ];
+      row_bits_load<DT, KJ>((const S*)p.pk + tok * p.pk_stride, p.R, lane, kWave, kb);
+      lse = p.lse[tok];
+      row_bits_floats<DT, KJ>(qb, p.R, lane, kWave, qk);
+      row_bits_floats<DT, KJ>(kb, p.R, lane, kWave, kr);
+    }
     P2LR<DT, VB, CB, KJ> st;
     p2lr_forward_state<DT, VB, CB, KJ>(p, lane, pvr, kr, qk, vs, bias, lse, st);
     const float w = st.prob;
@@ -473,7 +557,7 @@ __global__ void __launch_bounds__(256) phase2_lr_fwd_fast_kernel(const Phase2Par
   }
 }
 
-template <class DT, int VB, int CB, int KJ, bool LERP>
+template <class DT, int VB, int CB, int KJ, bool LERP, bool ACC>
 __global__ void __launch_bounds__(256) phase2_lr_bwd_fast_kernel(const Phase2Params p) {
   using S = typename DT::S;
   constexpr int E = VB / 2;
@@ -508,6 +592,24 @@ __global__ void __launch_bounds__(256) phase2_lr_bwd_fast_kernel(const Phase2Par
     }
     uint32_t kb[KJ];
     row_bits_load<DT, KJ>((const S*)p.pk + tok * p.pk_stride, p.R, lane, kWave, kb);
+    // ACC: the grown block's gradients from its other consumers, the
+    // projection's key columns and their 1/rms (the accumulation's backward)
+    Raw<DT, E> gvr[CB];
+    uint32_t gkb[KJ], xab[KJ];
+    float ia[KJ];
+    if constexpr (ACC) {
+      if (p.acc_gv) {
+        const S* gvp = (const S*)p.acc_gv + tok * p.acc_gv_stride;
+#pragma unroll
+        for (int c = 0; c < CB; ++c) load_raw<DT, E, true>(gvp + (c * kWave + lane) * E, gvr[c]);
+      }
+      if (p.acc_gk) row_bits_load<DT, KJ>((const S*)p.acc_gk + tok * (int64_t)p.R, p.R, lane, kWave, gkb);
+      if (p.acc_key_norm) {
+        row_bits_load<DT, KJ>((const S*)p.acc_y + tok * p.acc_y_stride + D, p.R, lane, kWave, xab);
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) ia[j] = p.acc_inv[tok * p.acc_H + min(lane + j * kWave, p.R - 1) / p.acc_hd];
+      }
+    }
     const float lse = p.lse[tok];
     float kr[KJ], qk[KJ];
     row_bits_floats<DT, KJ>(qb, p.R, lane, kWave, qk);
@@ -607,23 +709,67 @@ __global__ void __launch_bounds__(256) phase2_lr_bwd_fast_kernel(const Phase2Par
 #pragma unroll
         for (int j = 0; j < KJ; ++j) dk[j] = DT::rnd(iv * dk[j] - st.kv[j] * k3);
       }
-      S* dkp = (S*)p.dpk + tok * (int64_t)p.R;
+      if constexpr (ACC) {
+        // the grown key's total gradient rnd(merge share + other consumers'),
+        // the old partial key's too; through the key norm into the projection
+        float tot[KJ], gd[KJ];
+        if (p.acc_gk) row_bits_floats<DT, KJ>(gkb, p.R, lane, kWave, gd);
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) {
-        const int r = lane + j * kWave;
-        if (r < p.R) {
+        for (int j = 0; j < KJ; ++j) {
+          const int r = lane + j * kWave;
           float gk = dk[j];
           if (p.scale_key) {
             acc_sk += DT::rnd(gk * kr[j]);
-            gk = gk * vs;  // the store rounds
+            gk = gk * vs;
           }
-          DT::store1(dkp + r, gk);
+          gk = DT::rnd(gk);
+          tot[j] = r < p.R ? (p.acc_gk ? DT::rnd(gk + gd[j]) : gk) : 0.f;
+          if (r < p.R && p.acc_dpk_old) DT::store1((S*)p.acc_dpk_old + tok * (int64_t)p.R + r, tot[j]);
+        }
+        S* gyr = (S*)p.acc_gy + tok * (int64_t)p.acc_P;
+        if (p.acc_key_norm) {
+          float xa[KJ], gx[KJ], kd[KJ];
+          row_bits_floats<DT, KJ>(xab, p.R, lane, kWave, xa);
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) gx[j] = tot[j] * xa[j];
+          key_head_sums<KJ>(p.acc_hd, gx, kd);
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) {
+            const int r = lane + j * kWave;
+            if (r < p.R) {
+              const float k3k = ia[j] * ia[j] * ia[j] * (kd[j] / (float)p.acc_hd);
+              DT::store1(gyr + D + r, ia[j] * tot[j] - xa[j] * k3k);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) {
+            const int r = lane + j * kWave;
+            if (r < p.R) DT::store1(gyr + D + r, tot[j]);
+          }
+        }
+        for (int cc = D + p.R + lane; cc < p.acc_P; cc += kWave) DT::store1(gyr + cc, 0.f);
+      } else {
+        S* dkp = (S*)p.dpk + tok * (int64_t)p.R;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+          const int r = lane + j * kWave;
+          if (r < p.R) {
+            float gk = dk[j];
+            if (p.scale_key) {
+              acc_sk += DT::rnd(gk * kr[j]);
+              gk = gk * vs;  // the store rounds
+            }
+            DT::store1(dkp + r, gk);
+          }
         }
       }
     }
 
-    // ---- d p = rnd(dpm vs); the value's share of the block scale: rnd(dpm pv)
-    S* dpvp = (S*)p.dpv + tok * (int64_t)D;
+    // ---- d p = rnd(dpm vs); the value's share of the block scale: rnd(dpm pv).
+    // ACC: plus the other consumers' gradient, into the projection's value
+    // columns (the old partial value's gradient too)
+    S* dpvp = ACC ? (S*)p.acc_gy + tok * (int64_t)p.acc_P : (S*)p.dpv + tok * (int64_t)D;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
       float dp[E];
@@ -637,8 +783,14 @@ __global__ void __launch_bounds__(256) phase2_lr_bwd_fast_kernel(const Phase2Par
           acc_sv += DT::rnd(m0 * r0);
           acc_sv += DT::rnd(m1 * r1);
         }
-        dp[2 * i] = m0 * vs;
+        dp[2 * i] = m0 * vs;  // the store rounds
         dp[2 * i + 1] = m1 * vs;
+        if (ACC && p.acc_gv) {
+          float g0, g1;
+          unpack2<DT>(gvr[c].w[i], g0, g1);
+          dp[2 * i] = DT::rnd(dp[2 * i]) + g0;
+          dp[2 * i + 1] = DT::rnd(dp[2 * i + 1]) + g1;
+        }
       }
       store_vec<DT, E, true>(dpvp + (c * kWave + lane) * E, dp);
     }
@@ -702,12 +854,21 @@ hipError_t p2fast_dt(bool bwd, const Phase2Params& p, const Launch& L, hipStream
   return (L.feat & 1) ? p2fast_shape<DT, true>(bwd, p, L, st) : p2fast_shape<DT, false>(bwd, p, L, st);
 }
 
-// LR keys (L.nmax == 1): KJ key elements per lane from p.R, L.feat bit 1 = lerp merge
+// LR keys (L.nmax == 1): KJ key elements per lane from p.R, L.feat bit 1 =
+// lerp merge, bit 2 = the block accumulation fused in front (R <= 64)
 template <class DT, int VB, int CB, int KJ, bool LERP>
 hipError_t p2lr_launch(bool bwd, const Phase2Params& p, const Launch& L, hipStream_t st) {
   const dim3 g(L.grid), b(kP2FastWaves * kWave);
-  if (bwd) hipLaunchKernelGGL((phase2_lr_bwd_fast_kernel<DT, VB, CB, KJ, LERP>), g, b, L.lds, st, p);
-  else hipLaunchKernelGGL((phase2_lr_fwd_fast_kernel<DT, VB, CB, KJ, LERP>), g, b, 0, st, p);
+  if (L.feat & 4) {
+    if constexpr (KJ == 1) {
+      if (bwd) hipLaunchKernelGGL((phase2_lr_bwd_fast_kernel<DT, VB, CB, KJ, LERP, true>), g, b, L.lds, st, p);
+      else hipLaunchKernelGGL((phase2_lr_fwd_fast_kernel<DT, VB, CB, KJ, LERP, true>), g, b, 0, st, p);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
+  if (bwd) hipLaunchKernelGGL((phase2_lr_bwd_fast_kernel<DT, VB, CB, KJ, LERP, false>), g, b, L.lds, st, p);
+  else hipLaunchKernelGGL((phase2_lr_fwd_fast_kernel<DT, VB, CB, KJ, LERP, false>), g, b, 0, st, p);
   return hipGetLastError();
 }
 

@@ -58,6 +58,20 @@ class OracleOps:
                                            key_norm, complete, partial_scale, value_norm, scale_key)
 
     @staticmethod
+    def lrid_block_accumulate_read(projected, partial_value, partial_key, query, inter, lse, output_dim, rank,
+                                   logit_scale, num_heads=1, key_norm=True, merge_key_norm=None, lerp=False,
+                                   normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False,
+                                   query_row=None):
+        """The composition the fused op stands for: the accumulation, then the next site's merge."""
+        value, key = O.lrid_block_accumulate_ref(projected, partial_value, partial_key, output_dim, rank, num_heads,
+                                                 key_norm)
+        q = query[query_row] if query_row is not None else query
+        mkn = key_norm if merge_key_norm is None else merge_key_norm
+        out = _phase2(value, key, q, inter, lse, logit_scale, mkn, normalize_output, logit_bias, partial_scale,
+                      scale_key, "lerp" if lerp else "addcmul")
+        return value, key, out
+
+    @staticmethod
     def lrid_attention_residual_phase2(pv, pk, q, inter, lse, scale, key_norm, force_triton=False,
                                        normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False,
                                        query_row=None):

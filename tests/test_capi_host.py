@@ -42,7 +42,8 @@ def test_library_exports_every_declared_symbol():
                             "attnres_value_norm_forward", "attnres_value_norm_backward",
                             "attnres_block_accum_forward", "attnres_block_accum_backward",
                             "attnres_block_accum_backward_workspace_size", "attnres_phase1_backward_sites",
-                            "attnres_site_logits_forward", "attnres_site_logits_backward"])
+                            "attnres_site_logits_forward", "attnres_site_logits_backward",
+                            "attnres_accum_read_forward", "attnres_accum_read_backward"])
     for n in names:
         assert hasattr(lib, n), n
     nm = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True, text=True).stdout
@@ -53,7 +54,7 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_abi_version_and_error_reporting():
     lib = H.load()
-    assert lib.attnres_abi_version() == 8
+    assert lib.attnres_abi_version() == 9
     rc = lib.attnres_read_forward(None, None, None, None, None, None)
     assert rc == -1
     assert b"desc is NULL" in lib.attnres_last_error()
@@ -67,7 +68,8 @@ def test_abi_version_and_error_reporting():
 STRUCTS = ((H.ReadDesc, "attnres_read_desc"), (H.ReadGrads, "attnres_read_grads"),
            (H.Phase1Desc, "attnres_phase1_desc"), (H.Phase2Desc, "attnres_phase2_desc"),
            (H.Phase2Grads, "attnres_phase2_grads"), (H.KeyedSplitDesc, "attnres_keyed_split_desc"),
-           (H.BlockAccumDesc, "attnres_block_accum_desc"), (H.ValueKeyDesc, "attnres_value_key_desc"))
+           (H.BlockAccumDesc, "attnres_block_accum_desc"), (H.ValueKeyDesc, "attnres_value_key_desc"),
+           (H.AccumReadDesc, "attnres_accum_read_desc"))
 
 
 def _c_layout():
@@ -531,6 +533,65 @@ def test_block_accum_host_validation_rejects_bad_descriptions_without_launching(
     d = _badesc()
     d.split.n_tok = 0
     assert lib.attnres_block_accum_forward(ctypes.byref(d), None, None, None, None, None) == 0
+
+
+def _ardesc(**kw):
+    d = H.AccumReadDesc()
+    d.accum = _badesc(complete=0, value_scale=1.0)
+    d.read = _p2desc(n_tok=16, dim=768, rank=64)
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@needs_lib
+def test_accum_read_host_validation_rejects_bad_descriptions_without_launching():
+    lib = H.load()
+    value, key, out = ctypes.c_void_p(0x6000), ctypes.c_void_p(0x7000), ctypes.c_void_p(0x8000)
+    inv = ctypes.cast(ctypes.c_void_p(0x9000), ctypes.POINTER(ctypes.c_float))
+    d = _ardesc()
+    d.accum.complete = 1
+    assert lib.attnres_accum_read_forward(ctypes.byref(d), value, key, inv, out, None) == -1
+    assert b"complete = 0" in lib.attnres_last_error()
+    d = _ardesc()
+    d.read = _p2desc(n_tok=16, dim=768, rank=0)
+    assert lib.attnres_accum_read_forward(ctypes.byref(d), value, key, inv, out, None) == -1
+    assert b"LR merge" in lib.attnres_last_error()
+    d = _ardesc()
+    d.read.n_tok = 32
+    assert lib.attnres_accum_read_forward(ctypes.byref(d), value, key, inv, out, None) == -1
+    assert b"disagree" in lib.attnres_last_error()
+    # the block accumulation's own checks apply
+    d = _ardesc()
+    d.accum.split.heads = 3
+    assert lib.attnres_accum_read_forward(ctypes.byref(d), value, key, inv, out, None) == -1
+    assert b"heads" in lib.attnres_last_error()
+    # key norm needs the 1/rms output
+    assert lib.attnres_accum_read_forward(ctypes.byref(_ardesc()), value, key, None, out, None) == -1
+    assert b"key_inv_rms" in lib.attnres_last_error()
+    # the fused kernels take rank <= 64 only: the caller composes the two calls beyond
+    d = _ardesc()
+    d.accum.split = _ksdesc(rank=128, proj_cols=896, row_stride=896)
+    d.read = _p2desc(n_tok=16, dim=768, rank=128)
+    assert lib.attnres_accum_read_forward(ctypes.byref(d), value, key, inv, out, None) == -2
+    assert b"rank <= 64" in lib.attnres_last_error()
+    # backward: grads, the projection gradient and grad_value's row stride
+    d = _ardesc()
+    g = H.Phase2Grads()
+    assert lib.attnres_accum_read_backward(ctypes.byref(d), None, None, 768, None, inv, ctypes.c_void_p(0xa000),
+                                           None, None) == -1
+    assert b"grads is NULL" in lib.attnres_last_error()
+    assert lib.attnres_accum_read_backward(ctypes.byref(d), ctypes.byref(g), ctypes.c_void_p(0xb000), 700, None,
+                                           inv, ctypes.c_void_p(0xa000), None, None) == -1
+    assert b"grad_value_row_stride" in lib.attnres_last_error()
+    assert lib.attnres_accum_read_backward(ctypes.byref(d), ctypes.byref(g), None, 768, None, inv, None, None,
+                                           None) == -1
+    assert b"grad_projected" in lib.attnres_last_error()
+    # nothing to do for zero tokens
+    d = _ardesc()
+    d.accum.split.n_tok = 0
+    d.read.n_tok = 0
+    assert lib.attnres_accum_read_forward(ctypes.byref(d), None, None, None, None, None) == 0
 
 
 def test_block_accumulate_rejects_bad_calls_on_the_host():

@@ -18,13 +18,17 @@ from decoder_util import OracleOps, build_from_case, lm_step, load_model_case, m
 CASES = sorted(model_index())
 
 
-@pytest.mark.parametrize("fold,fuse", [(True, True), (True, False), (False, False)])
+@pytest.mark.parametrize("fold,fuse,fuse_read", [(True, True, True), (True, True, False), (True, False, False),
+                                                (False, False, False)])
 @pytest.mark.parametrize("name", CASES)
-def test_decoder_matches_reference_model(name, fold, fuse):
+def test_decoder_matches_reference_model(name, fold, fuse, fuse_read):
     """Also pins the oracle's block accumulation (``fuse``: split, partial-block
-    adds and block source composed in ``lrid_block_accumulate_ref``)."""
+    adds and block source composed in ``lrid_block_accumulate_ref``) and the
+    schedule of the fused accumulate-and-read (``fuse_read``: the read at the
+    site after a sublayer that does not end a block comes from that call)."""
     t, meta = load_model_case(name)
-    model = build_from_case(t, meta, OracleOps, fold_block_summary=fold, fuse_block_accumulation=fuse)
+    model = build_from_case(t, meta, OracleOps, fold_block_summary=fold, fuse_block_accumulation=fuse,
+                            fuse_accumulate_read=fuse_read)
     hidden, loss = lm_step(model, t["idx"], t["targets"])
     assert torch.equal(hidden, t["hidden"])
     assert torch.equal(loss.reshape(1), t["loss"])

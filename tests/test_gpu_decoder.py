@@ -116,6 +116,25 @@ class CheckingOps:
         self.calls.append(("accumulate", complete))
         return value, key
 
+    def lrid_block_accumulate_read(self, projected, partial_value, partial_key, query, inter, lse, output_dim, rank,
+                                   logit_scale, num_heads=1, key_norm=True, merge_key_norm=None, lerp=False,
+                                   normalize_output=False, logit_bias=0.0, partial_scale=None, scale_key=False,
+                                   query_row=None):
+        kw = dict(merge_key_norm=merge_key_norm, lerp=lerp, normalize_output=normalize_output,
+                  logit_bias=logit_bias, partial_scale=partial_scale, scale_key=scale_key, query_row=query_row)
+        value, key, out = ops.lrid_block_accumulate_read(projected, partial_value, partial_key, query, inter, lse,
+                                                         output_dim, rank, logit_scale, num_heads, key_norm, **kw)
+        cpu = lambda t: t.cpu() if t is not None else None  # noqa: E731
+        e_value, e_key, e_out = OracleOps.lrid_block_accumulate_read(
+            cpu(projected), cpu(partial_value), cpu(partial_key), cpu(query), cpu(inter), cpu(lse), output_dim, rank,
+            logit_scale, num_heads, key_norm, **kw)
+        assert torch.equal(value.cpu(), e_value)
+        assert_close(key, e_key, projected.dtype, "accumulated key")
+        assert_close(out, e_out, projected.dtype, "fused read")
+        self.calls.append(("accumulate", False))
+        self.calls.append(("phase2", "lerp" if lerp else "addcmul", partial_scale))
+        return value, key, out
+
     def _phase2(self, fn, merge, pv, pk, q, inter, lse, scale, key_norm, normalize_output, logit_bias,
                 partial_scale, scale_key, query_row=None):
         out = fn(pv, pk, q, inter, lse, scale, key_norm, normalize_output=normalize_output, logit_bias=logit_bias,
@@ -152,12 +171,13 @@ def _config5(**kw):
     return AD.DecoderConfig(**base)
 
 
-@pytest.mark.parametrize("torch_phase2", [True, False])
-def test_config5_every_read_matches_oracle(torch_phase2):
+@pytest.mark.parametrize("torch_phase2,fuse_read", [(True, False), (False, False), (True, True)])
+def test_config5_every_read_matches_oracle(torch_phase2, fuse_read):
     torch.manual_seed(5)
     checker = CheckingOps()
     with torch.device(DEV):
-        model = AD.Decoder(_config5(vocab_size=4096, attnres_training_torch_phase2=torch_phase2), ops=checker)
+        model = AD.Decoder(_config5(vocab_size=4096, attnres_training_torch_phase2=torch_phase2,
+                                    fuse_accumulate_read=fuse_read), ops=checker)
     model.to(torch.bfloat16)
     idx = torch.randint(0, 4096, (2, 1024), device=DEV)
     with torch.no_grad():
@@ -176,15 +196,19 @@ def test_config5_every_read_matches_oracle(torch_phase2):
     assert sum(1 for c in checker.calls if c == ("accumulate", True)) == 6
 
 
-def test_fused_block_accumulation_is_bit_identical_to_the_split_path():
+@pytest.mark.parametrize("fuse_read", [True, False])
+def test_fused_block_accumulation_is_bit_identical_to_the_split_path(fuse_read):
     """The decoder with sublayer projections folded by lrid_block_accumulate
-    against the same weights with the split + eager adds: hidden state, loss
-    and every gradient bit for bit (the kernels round as the eager ops do)."""
+    (with fuse_read, by lrid_block_accumulate_read together with the next
+    site's merge) against the same weights with the split + eager adds: hidden
+    state, loss and every gradient bit for bit (the kernels round as the eager
+    ops do)."""
     cfg = dict(n_layer=4, n_head=4, n_embd=256, mlp_hidden_dim=512, vocab_size=1000, block_size=256,
                attnres_num_blocks=3, lrid_rank=32, attn_res_query_init="normal")
     torch.manual_seed(13)
     with torch.device(DEV):
-        fused = AD.Decoder(AD.DecoderConfig(**cfg, fuse_block_accumulation=True)).to(torch.bfloat16)
+        fused = AD.Decoder(AD.DecoderConfig(**cfg, fuse_block_accumulation=True,
+                                            fuse_accumulate_read=fuse_read)).to(torch.bfloat16)
         split = AD.Decoder(AD.DecoderConfig(**cfg, fuse_block_accumulation=False)).to(torch.bfloat16)
     split.load_state_dict(fused.state_dict())
     g = torch.Generator().manual_seed(14)
