@@ -32,8 +32,7 @@ adds both to the partial block and, at a block end, forms the block source in
 one pass (``fuse_block_accumulation``; bit-identical too); a sublayer that does
 not end a block also merges the grown block into the next site's read in that
 pass (``lrid_block_accumulate_read``, ``fuse_accumulate_read``; bit-identical,
-gradients included; off by default: eager steps only, not cleared for HIP-graph
-capture).  Module and parameter names match the reference's, so a
+gradients included).  Module and parameter names match the reference's, so a
 reference state dict for this configuration loads with ``load_state_dict``.
 
 The read functions are looked up on ``ops`` (default: the HIP-backed
@@ -109,7 +108,7 @@ class DecoderConfig:
     lrid_logit_scale: Optional[float] = None
     fold_block_summary: bool = True
     fuse_block_accumulation: bool = True
-    fuse_accumulate_read: bool = False
+    fuse_accumulate_read: bool = True
 
     def __post_init__(self):
         if self.norm_pos not in {"before", "after", "both"}:

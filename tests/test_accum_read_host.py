@@ -13,6 +13,7 @@ parameters, as graph-capture harnesses call it.
 """
 
 import contextlib
+import weakref
 
 import pytest
 import torch
@@ -54,9 +55,12 @@ def oracle_kernels(monkeypatch):
         return _Desc(y=y, dim=dim, rank=rank, heads=heads, key_norm=key_norm, pv=pv, pk=pk)
 
     class Phase2:
+        # the grown block (the op's own outputs) by weak reference, as the real
+        # descriptor holds only its address: a strong one would be a cycle
         def __init__(self, pv, pk, q, pl, inter, lse, merge, key_norm, normalize_output, logit_scale, bias_value,
                      bias_t, scale_value, scale_t, scale_key):
-            self.__dict__.update(pv=pv, pk=pk, q=q, inter=inter, lse=lse, merge=merge, key_norm=key_norm,
+            self.__dict__.update(pv=weakref.ref(pv), pk=weakref.ref(pk), q=q, inter=inter, lse=lse, merge=merge,
+                                 key_norm=key_norm,
                                  normalize_output=normalize_output, logit_scale=logit_scale,
                                  bias_value=bias_value, bias_t=bias_t, scale_value=scale_value, scale_t=scale_t,
                                  scale_key=scale_key)
@@ -64,7 +68,7 @@ def oracle_kernels(monkeypatch):
     def accum_read_forward(d, value, key, kinv, out, device):
         calls["fwd"] += 1
         a, r = d.acc, d.read
-        assert r.pv is value and r.pk is key  # the merge reads the block this call grows
+        assert r.pv() is value and r.pk() is key  # the merge reads the block this call grows
         v, k, o = _compose(a, r, a.y, a.pv, a.pk, r.q, r.inter, r.lse)
         value.copy_(v)
         key.copy_(k)
@@ -160,3 +164,31 @@ def test_fused_read_under_autograd_grad_over_parameters(oracle_kernels):
             assert (a is None) == (b is None)
             if a is not None:
                 assert torch.equal(a, b)
+
+
+def test_fused_read_leaves_no_graph_behind(oracle_kernels):
+    """After a step, nothing of its autograd graph survives: the op's outputs
+    (and through their grad_fn the parameters' gradient accumulators, which
+    carry the stream they were made on) must die with the step.  A forward
+    that kept its outputs on ctx held every step's graph alive, so a later
+    HIP-graph capture met accumulators of an eager step on another stream."""
+    model = _small_decoder(_FusedOps, True)
+    idx = torch.randint(0, 128, (2, 24), generator=torch.Generator().manual_seed(6))
+    seen = []
+    real = ops._AccumReadFn.apply
+
+    def spy(*a):
+        out = real(*a)
+        seen.append(weakref.ref(out[0]))
+        return out
+
+    ops._AccumReadFn.apply = spy
+    try:
+        x0 = model.transformer.wte(idx).detach().requires_grad_(True)
+        h = model._forward_block_lrid(x0)
+        h.float().square().mean().backward()
+        del h, x0
+    finally:
+        ops._AccumReadFn.apply = real
+    assert seen
+    assert all(r() is None for r in seen)
