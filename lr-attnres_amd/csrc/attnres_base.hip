@@ -352,8 +352,20 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const ReduceParam
     const bool regular = slot < rp.n_part && !(slot >= rp.part_extra && slot < rp.part_extra + rp.n_extra);
     float a = 0.f;
     if (regular) {
-#pragma unroll 16
-      for (int w = rl; w < rp.n_groups; w += RL) a += rp.partials[part_index(rp.layout, w, slot, rp.n_groups, rp.n_part)];
+      // kRowLoads rows per pass, all loads issued before the first add (rows
+      // past the end re-read the last row and add +0, which leaves the sum
+      // as it is: the adds run in row order either way)
+      constexpr int kRowLoads = 8;
+      for (int w0 = rl; w0 < rp.n_groups; w0 += kRowLoads * RL) {
+        float x[kRowLoads];
+#pragma unroll
+        for (int u = 0; u < kRowLoads; ++u) {
+          const int w = min(w0 + u * RL, rp.n_groups - 1);
+          x[u] = rp.partials[part_index(rp.layout, w, slot, rp.n_groups, rp.n_part)];
+        }
+#pragma unroll
+        for (int u = 0; u < kRowLoads; ++u) a += w0 + u * RL < rp.n_groups ? x[u] : 0.f;
+      }
     }
     // the wave's row lanes of slot sl are the lanes congruent to sl mod SPB
     if constexpr (SPB == 1) {
