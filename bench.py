@@ -69,6 +69,10 @@ PHASE_CONFIGS = {
     # the reference's published block (24 layers, d1024, 4 blocks: 12 read sites
     # over up to 4 completed sources, LR rank 32) on 16384 tokens
     "p12lr": dict(B=8, T=2048, D=1024, S=4, Q=12, R=32, dtype=torch.bfloat16, lr=True),
+    # the same block in the block LR decoder's schedule: the Q - 1 sublayers that
+    # do not end the block grow it and form the next site's merge in one pass
+    # (attnres_accum_read_*), the last completes it (attnres_block_accum_*)
+    "p12ar": dict(B=8, T=2048, D=1024, S=4, Q=12, R=32, dtype=torch.bfloat16, lr=True, fused_read=True),
 }
 
 
@@ -90,6 +94,19 @@ def phase_bytes_per_token(c):
     R = c["R"]
     acf = (D + R) * s + (Q - 1) / Q * (D + R) * s + (D + R) * s + 4
     acb = (D + R) * s + R * s + 4 + (D + R) * s
+    if c.get("fused_read"):
+        # Q - 1 accumulate-and-read calls (the first without an old partial block)
+        # and one completing accumulation.  Forward: y, the old block, inter and
+        # lse read; the grown block, the key's 1/rms and the read written.
+        # Backward: the read's gradient, the grown block, inter, lse, the block's
+        # other gradients, the raw key and 1/rms read; d inter, d lse, the
+        # projection's gradient and the old key's gradient written.
+        old = (Q - 2) / (Q - 1)
+        arf = (D + R) * s + old * (D + R) * s + D * s + 4 + (D + R) * s + 4 + D * s
+        arb = (D * s + (D + R) * s + D * s + 4 + (D + R) * s + R * s + 4
+               + D * s + 4 + (D + R) * s + old * R * s)
+        acf = 3 * (D + R) * s + 4
+        return dict(phase1_fwd=p1f, phase1_bwd=p1b, ar_fwd=arf, ar_bwd=arb, accum_fwd=acf, accum_bwd=acb)
     return dict(phase1_fwd=p1f, phase1_bwd=p1b, phase2_fwd=p2f, phase2_bwd=p2b, accum_fwd=acf, accum_bwd=acb)
 
 
@@ -165,6 +182,22 @@ class PhaseWorkload:
         self.adesc = [H.block_accum_desc(self.ys[q], D, R, 1, True, self.avals[q - 1] if q else None,
                                          self.akeys[q - 1] if q else None, q == Q - 1, False, False, 1.0 / Q, None)
                       for q in range(Q)]
+        self.fused_read = bool(c.get("fused_read"))
+        if self.fused_read:
+            # sublayer q < Q - 1 grows the block into avals[q] / akeys[q] and site
+            # q + 1's merge (phase-1 read out[q]) reads it
+            self.ar = []
+            for q in range(Q - 1):
+                acc = H.block_accum_desc(self.ys[q], D, R, 1, True, self.avals[q - 1] if q else None,
+                                         self.akeys[q - 1] if q else None, False, False, False, 1.0, None)
+                read = H.Phase2(self.avals[q], self.akeys[q], self.query, None, self.out[q], self.lse[q],
+                                H.MERGE_LERP, True, True, 1.0 / math.sqrt(R), 0.693, None, 0.5, None, False)
+                self.ar.append((H.accum_read_desc(acc, read), read))
+            self.adpk = torch.empty((n, R), device=device, dtype=dt)
+            gq = H.Phase2Grads()
+            for f in ("grad_out", "dquery", "dinterblock_output", "dinterblock_lse", "workspace", "workspace_bytes"):
+                setattr(gq, f, getattr(gr, f))
+            self.gq = gq
 
     def _ok(self, rc):
         if rc:
@@ -187,14 +220,35 @@ class PhaseWorkload:
         for d in self.p2:
             self._ok(self.lib.attnres_phase2_backward(ctypes.byref(d.c), ctypes.byref(self.gr), sv))
 
+    def ar_fwd(self, sv):
+        for q, (d, _) in enumerate(self.ar):
+            self._ok(self.lib.attnres_accum_read_forward(ctypes.byref(d), ctypes.c_void_p(self.avals[q].data_ptr()),
+                                                         ctypes.c_void_p(self.akeys[q].data_ptr()),
+                                                         self.f(self.ainv[q]), ctypes.c_void_p(self.out2.data_ptr()),
+                                                         sv))
+
+    def ar_bwd(self, sv):
+        for q in reversed(range(len(self.ar))):
+            self._ok(self.lib.attnres_accum_read_backward(
+                ctypes.byref(self.ar[q][0]), ctypes.byref(self.gq), ctypes.c_void_p(self.agv[q].data_ptr()), self.D,
+                ctypes.c_void_p(self.agk[q].data_ptr()), self.f(self.ainv[q]), ctypes.c_void_p(self.agy[q].data_ptr()),
+                ctypes.c_void_p(self.adpk.data_ptr()) if q else None, sv))
+
     def accum_fwd(self, sv):
+        if self.fused_read:  # only the completing accumulation is separate
+            d, q = self.adesc[-1], len(self.adesc) - 1
+            self._ok(self.lib.attnres_block_accum_forward(ctypes.byref(d), ctypes.c_void_p(self.avals[q].data_ptr()),
+                                                          ctypes.c_void_p(self.akeys[q].data_ptr()),
+                                                          self.f(self.ainv[q]), None, sv))
+            return
         for q, d in enumerate(self.adesc):
             self._ok(self.lib.attnres_block_accum_forward(ctypes.byref(d), ctypes.c_void_p(self.avals[q].data_ptr()),
                                                           ctypes.c_void_p(self.akeys[q].data_ptr()),
                                                           self.f(self.ainv[q]), None, sv))
 
     def accum_bwd(self, sv):
-        for q in reversed(range(len(self.adesc))):
+        qs = [len(self.adesc) - 1] if self.fused_read else reversed(range(len(self.adesc)))
+        for q in qs:
             self._ok(self.lib.attnres_block_accum_backward(
                 ctypes.byref(self.adesc[q]), ctypes.c_void_p(self.agv[q].data_ptr()), self.D,
                 ctypes.c_void_p(self.agk[q].data_ptr()), self.f(self.ainv[q]), None,
@@ -206,7 +260,10 @@ def bench_phase(args, dev):
     wl = PhaseWorkload(c, dev)
     stream = torch.cuda.current_stream(dev)
     sv = ctypes.c_void_p(stream.cuda_stream)
-    parts = ("phase1_fwd", "phase1_bwd", "phase2_fwd", "phase2_bwd", "accum_fwd", "accum_bwd")
+    if c.get("fused_read"):
+        parts = ("phase1_fwd", "phase1_bwd", "ar_fwd", "ar_bwd", "accum_fwd", "accum_bwd")
+    else:
+        parts = ("phase1_fwd", "phase1_bwd", "phase2_fwd", "phase2_bwd", "accum_fwd", "accum_bwd")
     for _ in range(args.warmup):
         for k in parts:
             getattr(wl, k)(sv)
@@ -235,21 +292,29 @@ def bench_phase(args, dev):
         # median over the steps: a pair that spans a gap in the host's
         # submission (the GPU idle between the two events) would skew a mean
         ms = statistics.median(a.elapsed_time(b) for a, b in ev[k])
-        calls = c["Q"] if k.startswith(("phase2", "accum")) else 1
+        if c.get("fused_read"):
+            calls = c["Q"] - 1 if k.startswith("ar_") else 1
+        else:
+            calls = c["Q"] if k.startswith(("phase2", "accum")) else 1
         gbs = bpt[k] * wl.n_tok * calls / (ms / 1e3) / 1e9
         kern[k] = {"ms": round(ms, 5), "calls": calls, "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
                    "bytes_per_token": bpt[k]}
+    if c.get("fused_read"):
+        workload = (f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q'] - 1} x accumulate-and-read (block "
+                    f"accumulation r{c['R']} key_norm + LR merge: lerp, output norm) + 1 x completing block "
+                    f"accumulation, B{c['B']} T{c['T']} d{c['D']}")
+    else:
+        workload = (f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q']} x phase2 "
+                    + (f"(LR key r{c['R']}, key_norm, lerp, output norm) " if c.get("lr") else "(base, key_norm) ")
+                    + f"+ {c['Q']} x block accumulation (r{c['R']}, key_norm, the last completing "
+                    f"the block) B{c['B']} T{c['T']} d{c['D']}")
     print(json.dumps({
         "metric": "cached-logit block schedule (phase 1 + Q phase-2 merges + Q partial-block accumulations) "
                   "fwd+bwd tokens/s",
         "value": round(wl.n_tok / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"{args.config}: phase1 S{c['S']} Q{c['Q']} + {c['Q']} x phase2 "
-                               + (f"(LR key r{c['R']}, key_norm, lerp, output norm) " if c.get("lr")
-                                  else "(base, key_norm) ")
-                               + f"+ {c['Q']} x block accumulation (r{c['R']}, key_norm, the last completing "
-                               f"the block) B{c['B']} T{c['T']} d{c['D']}", "tokens": wl.n_tok,
+        "config": {"workload": workload, "tokens": wl.n_tok,
                    "phase_ms": round(sum(kern[k]["ms"] for k in parts if k.startswith("phase")), 5)},
         "kernels": kern}))
 
