@@ -645,3 +645,15 @@ def test_value_norm_host_validation():
 def test_value_key_projection_fails_loudly_on_cpu_tensors():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.lrid_value_key_projection([torch.randn(1, 2, 8)] * 2, torch.randn(4, 8))
+
+
+def test_accumulate_read_rejects_bad_calls_on_the_host():
+    proj, inter, lse = torch.randn(2, 3, 288), torch.randn(2, 3, 256), torch.randn(2, 3)
+    bank = torch.randn(4, 32)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lrid_block_accumulate_read(proj.bfloat16(), None, None, bank.bfloat16(), inter.bfloat16(), lse, 256, 32,
+                                       0.2, query_row=1)
+    with pytest.raises(RuntimeError, match=r"interblock_output must be \[B, T, 256\]"):
+        ops.lrid_block_accumulate_read(proj, None, None, bank, inter[0], lse, 256, 32, 0.2, query_row=1)
+    with pytest.raises(RuntimeError, match=r"interblock_output must be \[B, T, 256\]"):
+        ops.lrid_block_accumulate_read(proj, None, None, bank, inter[..., :128], lse, 256, 32, 0.2, query_row=1)
