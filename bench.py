@@ -66,6 +66,8 @@ PHASE_CONFIGS = {
     # (r=64, key norm, logit scale 1/8), the lerp merge and the next sublayer's
     # fused pre-norm
     "p5lr": dict(B=16, T=1024, D=768, S=6, Q=4, R=64, dtype=torch.bfloat16, lr=True),
+    # p5lr's block in the decoder's accumulate-and-read schedule (see p12ar)
+    "p5ar": dict(B=16, T=1024, D=768, S=6, Q=4, R=64, dtype=torch.bfloat16, lr=True, fused_read=True),
     # the reference's published block (24 layers, d1024, 4 blocks: 12 read sites
     # over up to 4 completed sources, LR rank 32) on 16384 tokens
     "p12lr": dict(B=8, T=2048, D=1024, S=4, Q=12, R=32, dtype=torch.bfloat16, lr=True),
