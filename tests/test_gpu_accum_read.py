@@ -192,3 +192,34 @@ def test_accumulate_read_composes_where_the_fused_kernels_do_not_reach(fused_cal
         v, k, o = ops.lrid_block_accumulate_read(*[t.to(DEV) for t in ins], D, R, 0.1, 1, True, query_row=1)
         assert o.shape == (B, T, D)
     assert len(fused_calls) == 0
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_accumulate_read_few_tokens(fused_calls, T):
+    """Fewer tokens than a workgroup's waves: idle waves, one partial row."""
+    dtype = torch.bfloat16
+    g = gen(70 + T)
+    B, D, R = 1, 768, 64
+    ins = _inputs(g, B, T, D, R, D + R, dtype, False, 3)
+    go, gv, gk = randn(g, (B, T, D), dtype), randn(g, (B, T, D), dtype), randn(g, (B, T, R), dtype)
+    kw = dict(lerp=True, normalize_output=True, logit_bias=0.2, partial_scale=0.5, scale_key=False, query_row=2)
+    lf, lc = _leaves(ins, DEV), _leaves(ins, DEV)
+    v, k, o = _run(True, lf, D, R, 1, True, kw, go.to(DEV), gv.to(DEV), gk.to(DEV))
+    assert len(fused_calls) == 1
+    ev, ek, eo = _run(False, lc, D, R, 1, True, kw, go.to(DEV), gv.to(DEV), gk.to(DEV))
+    assert torch.equal(v, ev) and torch.equal(k, ek) and torch.equal(o, eo)
+    for name, a, b in zip(("y", "pv", "pk", "query", "inter", "lse"), lf, lc):
+        assert torch.equal(a.grad, b.grad), name
+
+
+def test_accumulate_read_empty_batch(fused_calls):
+    """No tokens: empty outputs, zero gradients for the query bank (the two calls' behaviour)."""
+    dtype = torch.bfloat16
+    g = gen(80)
+    ins = _inputs(g, 2, 0, 768, 64, 832, dtype, False, 3)
+    lf = _leaves(ins, DEV)
+    v, k, o = ops.lrid_block_accumulate_read(*lf, 768, 64, 0.125, 1, True, lerp=True, query_row=1)
+    assert v.shape == (2, 0, 768) and k.shape == (2, 0, 64) and o.shape == (2, 0, 768)
+    o.sum().backward()
+    assert float(lf[3].grad.abs().max()) == 0.0
+    assert len(fused_calls) == 0
