@@ -114,3 +114,28 @@ def test_phase_schedule_graph_replays_match_eager():
         return [merged.detach(), *grads]
 
     _check_replays(fn, [*vals, logits, partial, q, up, g_outs, g_lse])
+
+
+def test_accumulate_read_graph_replays_match_eager():
+    """The fused accumulate-and-read in a captured fwd+bwd, as the graphed
+    decoder step runs it: the op's backward reads the forward's descriptor
+    from ctx, whose tensors live on as saved tensors only."""
+    g = gen(47)
+    B, T, D, R, rows = 2, 40, 768, 64, 5
+    dt = torch.bfloat16
+    y = randn(g, (B, T, D + R), dt).to(DEV).requires_grad_(True)
+    pv = randn(g, (B, T, D), dt).to(DEV).requires_grad_(True)
+    pk = randn(g, (B, T, R), dt).to(DEV).requires_grad_(True)
+    bank = randn(g, (rows, R), dt, 0.1).to(DEV).requires_grad_(True)
+    inter = randn(g, (B, T, D), dt).to(DEV).requires_grad_(True)
+    lse = randn(g, (B, T), torch.float32).to(DEV).requires_grad_(True)
+    go, gv, gk = randn(g, (B, T, D), dt).to(DEV), randn(g, (B, T, D), dt).to(DEV), randn(g, (B, T, R), dt).to(DEV)
+
+    def fn():
+        v, k, o = ops.lrid_block_accumulate_read(y, pv, pk, bank, inter, lse, D, R, 0.125, 1, True, lerp=True,
+                                                 normalize_output=True, logit_bias=0.4, partial_scale=0.5,
+                                                 query_row=2)
+        grads = torch.autograd.grad([o, v, k], [y, pv, pk, bank, inter, lse], [go, gv, gk])
+        return [v.detach(), k.detach(), o.detach(), *grads]
+
+    _check_replays(fn, [y, pv, pk, bank, inter, lse, go, gv, gk])
