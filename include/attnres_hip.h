@@ -550,7 +550,7 @@ int attnres_block_accum_backward(const attnres_block_accum_desc* desc, const voi
  *   accum: the sublayer's projection and the live block before it
  *          (complete = 0; partial_value / partial_key NULL for a block's first
  *          sublayer).
- *   read:  the merge at the next read site, rank <= 64, its rows one-wave
+ *   read:  the merge at the next read site, rank <= 256, its rows one-wave
  *          16-bit rows of 256/512/768/1024 (else ATTNRES_EUNSUPPORTED: compose
  *          the two calls then).  The forward ignores read.partial_value /
  *          partial_key; the backward takes them as the grown block the

@@ -1561,10 +1561,10 @@ class _AccumReadFn(torch.autograd.Function):
 
 def _accum_read_fits(y: Tensor, inter: Tensor, D: int, R: int, heads: int) -> bool:
     """Shapes the fused accumulate-and-read kernels take: 16-bit rows one wave
-    covers exactly (D = 256, 512, 768, 1024), rank <= 64, 16-byte aligned rows."""
+    covers exactly (D = 256, 512, 768, 1024), rank <= 256, 16-byte aligned rows."""
     if y.dtype not in (torch.bfloat16, torch.float16) or D not in (256, 512, 768, 1024):
         return False
-    if not 1 <= R <= 64 or R % heads != 0:
+    if not 1 <= R <= 256 or R % heads != 0:
         return False
     return all(t.data_ptr() % 16 == 0 and (t.stride(0) * t.element_size()) % 16 == 0 for t in (y, inter))
 

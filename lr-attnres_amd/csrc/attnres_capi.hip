@@ -1368,9 +1368,9 @@ int phase2_forward_impl(const attnres_phase2_desc* d, void* out, void* stream, c
   }
   const bool fast = L.teams > 0 && phase2_fast(d, wv);
   if (acc) {
-    if (!fast || L.nmax != 1 || d->rank > kWaveSize)
+    if (!fast || L.nmax != 1 || d->rank > 4 * kWaveSize)
       return fail(ATTNRES_EUNSUPPORTED, "the fused accumulation needs the one-wave LR merge (16-bit rows of "
-                  "256/512/768/1024 aligned to 16 bytes, rank <= 64)");
+                  "256/512/768/1024 aligned to 16 bytes, rank <= 256)");
     fill_accum(*acc, &p);
     L.feat |= 4;
   }
@@ -1466,9 +1466,9 @@ int phase2_backward_impl(const attnres_phase2_desc* d, const attnres_phase2_grad
   }
   const bool fast = L.teams > 0 && phase2_fast(d, wv);
   if (acc) {
-    if (!fast || L.nmax != 1 || d->rank > kWaveSize)
+    if (!fast || L.nmax != 1 || d->rank > 4 * kWaveSize)
       return fail(ATTNRES_EUNSUPPORTED, "the fused accumulation needs the one-wave LR merge (16-bit rows of "
-                  "256/512/768/1024 aligned to 16 bytes, rank <= 64)");
+                  "256/512/768/1024 aligned to 16 bytes, rank <= 256)");
     fill_accum(*acc, &p);
     L.feat |= 4;
   }

@@ -855,17 +855,14 @@ hipError_t p2fast_dt(bool bwd, const Phase2Params& p, const Launch& L, hipStream
 }
 
 // LR keys (L.nmax == 1): KJ key elements per lane from p.R, L.feat bit 1 =
-// lerp merge, bit 2 = the block accumulation fused in front (R <= 64)
+// lerp merge, bit 2 = the block accumulation fused in front
 template <class DT, int VB, int CB, int KJ, bool LERP>
 hipError_t p2lr_launch(bool bwd, const Phase2Params& p, const Launch& L, hipStream_t st) {
   const dim3 g(L.grid), b(kP2FastWaves * kWave);
   if (L.feat & 4) {
-    if constexpr (KJ == 1) {
-      if (bwd) hipLaunchKernelGGL((phase2_lr_bwd_fast_kernel<DT, VB, CB, KJ, LERP, true>), g, b, L.lds, st, p);
-      else hipLaunchKernelGGL((phase2_lr_fwd_fast_kernel<DT, VB, CB, KJ, LERP, true>), g, b, 0, st, p);
-      return hipGetLastError();
-    }
-    return hipErrorInvalidValue;
+    if (bwd) hipLaunchKernelGGL((phase2_lr_bwd_fast_kernel<DT, VB, CB, KJ, LERP, true>), g, b, L.lds, st, p);
+    else hipLaunchKernelGGL((phase2_lr_fwd_fast_kernel<DT, VB, CB, KJ, LERP, true>), g, b, 0, st, p);
+    return hipGetLastError();
   }
   if (bwd) hipLaunchKernelGGL((phase2_lr_bwd_fast_kernel<DT, VB, CB, KJ, LERP, false>), g, b, L.lds, st, p);
   else hipLaunchKernelGGL((phase2_lr_fwd_fast_kernel<DT, VB, CB, KJ, LERP, false>), g, b, 0, st, p);

@@ -569,12 +569,12 @@ def test_accum_read_host_validation_rejects_bad_descriptions_without_launching()
     # key norm needs the 1/rms output
     assert lib.attnres_accum_read_forward(ctypes.byref(_ardesc()), value, key, None, out, None) == -1
     assert b"key_inv_rms" in lib.attnres_last_error()
-    # the fused kernels take rank <= 64 only: the caller composes the two calls beyond
+    # the fused kernels take one-wave 16-bit rows only: the caller composes the two calls otherwise
     d = _ardesc()
-    d.accum.split = _ksdesc(rank=128, proj_cols=896, row_stride=896)
-    d.read = _p2desc(n_tok=16, dim=768, rank=128)
+    d.accum.split = _ksdesc(rank=64, proj_cols=864, row_stride=864, dim=800)
+    d.read = _p2desc(n_tok=16, dim=800, rank=64)
     assert lib.attnres_accum_read_forward(ctypes.byref(d), value, key, inv, out, None) == -2
-    assert b"rank <= 64" in lib.attnres_last_error()
+    assert b"rank <= 256" in lib.attnres_last_error()
     # backward: grads, the projection gradient and grad_value's row stride
     d = _ardesc()
     g = H.Phase2Grads()

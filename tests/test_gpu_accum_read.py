@@ -82,6 +82,9 @@ CASES = [
     (1024, 64, 64, 4, True),   # per-head norm, 16-byte vectors
     (512, 64, 80, 1, False),   # no key norm (the key scaled with the block), padding columns
     (768, 16, 16, 1, True),    # a narrow key
+    (1024, 128, 128, 1, True),  # two key elements per lane, one 128-column head
+    (512, 128, 128, 4, True),  # two key elements per lane, heads of 32
+    (768, 256, 256, 2, True),  # four key elements per lane, heads of 128
 ]
 
 
@@ -183,11 +186,12 @@ def test_accumulate_read_at_the_model_size(fused_calls):
 
 
 def test_accumulate_read_composes_where_the_fused_kernels_do_not_reach(fused_calls):
-    """fp32 rows and a 128-column key take the two calls; the results are the
-    composition's by construction."""
-    for dtype, R in ((torch.float32, 64), (torch.bfloat16, 128)):
-        g = gen(R)
-        B, T, D = 1, 19, 768
+    """fp32 rows and rows one wave does not cover (d800) take the two calls;
+    the results are the composition's by construction."""
+    for dtype, D in ((torch.float32, 768), (torch.bfloat16, 800)):
+        R = 64
+        g = gen(D)
+        B, T = 1, 19
         ins = _inputs(g, B, T, D, R, D + R, dtype, False, 2)
         v, k, o = ops.lrid_block_accumulate_read(*[t.to(DEV) for t in ins], D, R, 0.1, 1, True, query_row=1)
         assert o.shape == (B, T, D)
