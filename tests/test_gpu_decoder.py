@@ -171,7 +171,7 @@ def _config5(**kw):
     return AD.DecoderConfig(**base)
 
 
-@pytest.mark.parametrize("torch_phase2,fuse_read", [(True, False), (False, False), (True, True)])
+@pytest.mark.parametrize("torch_phase2,fuse_read", [(True, False), (False, False), (True, True), (False, True)])
 def test_config5_every_read_matches_oracle(torch_phase2, fuse_read):
     torch.manual_seed(5)
     checker = CheckingOps()
