@@ -320,6 +320,9 @@ def bench_phase(args, dev):
         "data": "synthetic",
         "config": {"workload": workload, "tokens": wl.n_tok,
                    "phase_ms": round(sum(kern[k]["ms"] for k in parts if k.startswith("phase")), 5)},
+        # the parts' device time (ms_per_step also holds the host's gaps between
+        # the Python-driven C calls)
+        "device_ms": round(sum(kern[k]["ms"] for k in parts), 5),
         "kernels": kern}))
 
 
