@@ -1588,8 +1588,11 @@ def lrid_block_accumulate_read(projected: Tensor, partial_value: Optional[Tensor
                                                      logit_scale, merge_key_norm, ...)
 
     (``_torch``, the ``lerp`` merge, with ``lerp``), and the gradients of all
-    three outputs as autograd sums them there.  ``merge_key_norm`` defaults to
-    ``key_norm``.  Returns ``(value, key, out)``: the grown block and the read.
+    three outputs as autograd sums them there; the cross-token sums (the
+    query's, a learned bias's or scale's gradient) group their fp32 partials
+    by the fused backward's own grid, which above about 3000 tokens has fewer
+    workgroups than the merge's, so there they agree to rounding, not bit for
+    bit.  ``merge_key_norm`` defaults to ``key_norm``.  Returns ``(value, key, out)``: the grown block and the read.
     Shapes the fused kernels do not take run the two calls.
     """
     mkn = key_norm if merge_key_norm is None else bool(merge_key_norm)

@@ -1456,6 +1456,9 @@ int phase2_backward_impl(const attnres_phase2_desc* d, const attnres_phase2_grad
     // and the reduction's chains of dependent loads half as long (measured at
     // p5: packed kernels 33.0 -> 29.9 us per call)
     if (cap > base_fast_streams() / kPhase2Teams) cap = base_fast_streams() / kPhase2Teams;
+    // the fused accumulation's backward holds 3 waves per SIMD (its registers),
+    // not the 4 the resident round above assumes: one round of those
+    if (acc && cap > 3 * base_fast_streams() / (4 * kPhase2Teams)) cap = 3 * base_fast_streams() / (4 * kPhase2Teams);
     L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
     L.feat = (d->key_norm ? 1 : 0) | (d->merge == ATTNRES_MERGE_LERP ? 2 : 0);
