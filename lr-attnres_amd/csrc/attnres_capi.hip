@@ -1456,8 +1456,10 @@ int phase2_backward_impl(const attnres_phase2_desc* d, const attnres_phase2_grad
     // and the reduction's chains of dependent loads half as long (measured at
     // p5: packed kernels 33.0 -> 29.9 us per call)
     if (cap > base_fast_streams() / kPhase2Teams) cap = base_fast_streams() / kPhase2Teams;
-    // the fused accumulation's backward holds 3 waves per SIMD (its registers),
-    // not the 4 the resident round above assumes: one round of those
+    // the fused accumulation's backward holds 3 waves per SIMD (its registers
+    // at d768 / d1024, one key element per lane), not the 4 the resident round
+    // above assumes: one round of those (the narrower instantiations, which fit
+    // 4-5 waves, run one wave per SIMD short of a full round)
     if (acc && cap > 3 * base_fast_streams() / (4 * kPhase2Teams)) cap = 3 * base_fast_streams() / (4 * kPhase2Teams);
     L.grid = (int)(wgs < cap ? wgs : cap);
     L.lds = (size_t)kPhase2Teams * (PL.n_part > 0 ? PL.n_part : 1) * sizeof(float);
